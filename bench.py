@@ -1,0 +1,248 @@
+"""Benchmark of the MI355X sparse-attention path (BASELINE metric: decode us/layer-step + % HBM roofline at
+128K x 4 slots; prefill tok/s at a 2K chunk).
+
+A "step" is one decode layer-step of config C2 (4 slots x 131072 context, k 2048): the SWA ring append, the
+compressed-KV and index-key appends, the indexer score over the e4m3 keys, the top-k and the sparse attention over
+ring + top-k rows.  Inputs are resident in HBM; NL independent copies of the layer's caches are rotated so every
+step misses the 256 MB last-level cache.  The timed region replays a HIP graph of NL layer-steps K/NL times
+(rounded up) with events on the launch stream; the per-kernel durations behind `roofline` come from an eager pass
+with events around each launch, on the same stream.
+
+Prints ONE JSON line (rank 0, N = 1)."""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "deepseekv4.1-a100-custom_amd"))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_TFLOPS = 2500.0
+MFMA_FP8_TFLOPS = 5000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_bytes(cfg, idx_sets=None):
+    """Algorithmic HBM bytes of one decode layer-step: per slot the valid index keys (128 B + 4 B scale each), the
+    union of the selected compressed rows, the ring, plus per query row q, index q, output and indices."""
+    from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN
+    per_kernel = {"index_score": 0, "topk": 0, "sattn": 0}
+    R = cfg.slots * cfg.rows_per_slot
+    for s in range(cfg.slots):
+        n = cfg.n_c(s)
+        per_kernel["index_score"] += n * (DI + 4) + cfg.rows_per_slot * n * 4  # keys + scores written
+        per_kernel["topk"] += cfg.rows_per_slot * n * 4 + cfg.rows_per_slot * cfg.topk * 4
+        sel = min(cfg.topk, n) if idx_sets is None else idx_sets[s]
+        per_kernel["sattn"] += (sel + WIN) * DQK * 2
+    per_kernel["index_score"] += R * (HI * DI * 2 + HI * 2)
+    per_kernel["sattn"] += R * (H * DQK * 2 + H * DV * 2 + cfg.topk * 4)
+    return per_kernel
+
+
+def survey_bytes(cfg):
+    """The per-step algorithmic byte count as the survey defines it (keys incl. scale, gathered rows, ring, q,
+    index q, output, idx write + read), used for the headline roofline fraction."""
+    from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN
+    tot = 0
+    for s in range(cfg.slots):
+        n = cfg.n_c(s)
+        r = cfg.rows_per_slot
+        tot += n * (DI + 4) + min(cfg.topk, n) * DQK * 2 + WIN * DQK * 2
+        tot += r * (H * DQK * 2 + HI * DI + H * DV * 2 + cfg.topk * 4 * 2)
+    return tot
+
+
+def run_decode(args, dev):
+    import torch
+    from dsv41_amd.decode import DecodeLayer
+    from dsv41_amd.workloads import CONFIGS, make_decode_inputs
+
+    cfg = CONFIGS[args.config]
+    NL = args.layers
+    log(f"[bench] building {args.config}: {cfg.slots} slots x {cfg.ctx[0]} ctx, {NL} cache copies")
+    layers, st = make_decode_inputs(cfg, dev, seed=0, cache_copies=NL)
+    cos = torch.zeros(1, 32, device=dev)
+    rd = 64
+    import numpy as np
+    max_pos = max(cfg.ctx) + 8
+    ang = torch.outer(torch.arange(max_pos, dtype=torch.float32),
+                      1.0 / (10000.0 ** (torch.arange(0, rd, 2, dtype=torch.float32) / rd)))
+    cos, sin = torch.cos(ang).to(dev), torch.sin(ang).to(dev)
+    L = [DecodeLayer(l["ring"], l["ckv"], l["k8"], l["ks"], st["sink"], cos, sin, cfg.ratio, cfg.topk, rd=rd)
+         for l in layers]
+    pos, seq, pmax = st["pos"], st["seq"], st["pmax"]
+
+    def layer_step(lay):
+        lay.appends(st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos, seq)
+        idx = lay.select(st["q_idx"], st["w_idx"], pos, seq)
+        return lay.attend(st["q"], idx, pos, seq, pmax, plim=pos)
+
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(max(1, args.warmup)):
+        for lay in L:
+            layer_step(lay)
+    torch.cuda.synchronize(dev)
+
+    # ---- per-kernel durations (eager, events around each launch on the launch stream)
+    E = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    phases = {"appends": [], "index_score": [], "topk": [], "sattn": []}
+    reps = max(2, min(args.steps, 20))
+    from dsv41_amd.fused3 import index_score, topk_indices
+    from dsv41_amd.fused2 import sattn2
+    sel_union = None
+    for rep in range(reps):
+        for lay in L:
+            ev = [E() for _ in range(5)]
+            ev[0].record(stream)
+            cl = lay.appends(st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos, seq)
+            ev[1].record(stream)
+            score = index_score(st["q_idx"], lay.k8, st["w_idx"], seq, cl, k_scale=lay.ks)
+            ev[2].record(stream)
+            idx = topk_indices(score, lay.topk, cl)
+            ev[3].record(stream)
+            o = sattn2(st["q"], lay.ring, lay.ckv, idx, pos, lay.sink, lay.cos, lay.sin, 0, lay.scale, seq, pmax,
+                       plim=pos, d_v=512)
+            ev[4].record(stream)
+            torch.cuda.synchronize(dev)
+            for i, k in enumerate(phases):
+                phases[k].append(ev[i].elapsed_time(ev[i + 1]) * 1000.0)
+            if sel_union is None:
+                ids = idx.view(cfg.slots, cfg.rows_per_slot, -1).cpu()
+                sel_union = [int(torch.unique(ids[s][ids[s] >= 0]).numel()) for s in range(cfg.slots)]
+    kern_us = {k: float(np.median(v)) for k, v in phases.items()}
+
+    # ---- graph of NL layer-steps, replayed; timed region bracketed by synchronize
+    g = torch.cuda.CUDAGraph()
+    s2 = torch.cuda.Stream(dev)
+    s2.wait_stream(stream)
+    with torch.cuda.stream(s2):
+        for lay in L:  # warm the allocator on the capture stream
+            layer_step(lay)
+    stream.wait_stream(s2)
+    torch.cuda.synchronize(dev)
+    with torch.cuda.graph(g, stream=s2):
+        for lay in L:
+            layer_step(lay)
+    torch.cuda.synchronize(dev)
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize(dev)
+    replays = max(1, math.ceil(args.steps / NL))
+    e0, e1 = E(), E()
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(replays):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    step_us = e0.elapsed_time(e1) * 1000.0 / (replays * NL)
+    log(f"[bench] graph: {replays} replays x {NL} layer-steps: {step_us:.2f} us/layer-step (wall {wall*1e3:.1f} ms)")
+    log(f"[bench] eager per-kernel medians (us): {kern_us}")
+    kb = decode_bytes(cfg, sel_union)
+    return dict(cfg=cfg, step_us=step_us, kern_us=kern_us, kern_bytes=kb, steps=replays * NL, sel_union=sel_union)
+
+
+def cpu_baseline(cfg, budget_s: float):
+    """The oracle (numpy port of the reference's decode path) on the host: index score + top-k + sattn2 for one
+    slot of the workload, repeated until the budget is spent; scaled to a full layer-step (x slots)."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import dsv41_oracle as O
+    from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    rng = np.random.default_rng(0)
+    n = cfg.n_c(0)
+    keys = O.fake_quant_fp4(rng.standard_normal((1, n, DI)).astype(np.float32) * 0.1, 32)
+    q8, s8 = O.key_encode_fp8(keys)
+    ckv = O.bf16(rng.standard_normal((1, n + 1, DQK)).astype(np.float32) * 0.1)
+    ring = O.bf16(rng.standard_normal((1, WIN, DQK)).astype(np.float32) * 0.1)
+    q = O.bf16(rng.standard_normal((1, 1, H, DQK)).astype(np.float32) * 0.1)
+    qi = O.fake_quant_fp4(rng.standard_normal((1, 1, HI, DI)).astype(np.float32), 32)
+    w = (rng.standard_normal((1, HI)) * 0.01).astype(np.float32)
+    sink = rng.standard_normal(H).astype(np.float32)
+    pos = cfg.ctx[0] - 1
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or not times:
+        t0 = time.perf_counter()
+        sc = O.index_score(qi, q8, w, [0], [n], k_scale=s8[..., 0])
+        idx = O.topk_indices(sc, cfg.topk, [n])
+        O.sattn2(q, ring, ckv, idx[:, None], [pos], [0], [pos], None, sink, None, None, 0, DQK ** -0.5, dv=DV)
+        times.append(time.perf_counter() - t0)
+    per_slot = float(np.median(times))
+    return {"value": per_slot * cfg.slots * cfg.rows_per_slot * 1e6, "unit": "us/layer-step", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle (numpy) index score + top-k + sattn2 for 1 of {cfg.slots} slots ({n} keys, k "
+                      f"{cfg.topk}), {len(times)} reps in {budget_s:.0f} s, median x {cfg.slots} slots"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="C2")
+    ap.add_argument("--layers", type=int, default=8, help="independent cache copies rotated per step")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the path shards by slot with no exchange; see the design "
+              "notes); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    r = run_decode(args, dev)
+    cfg = r["cfg"]
+    kb, ku = r["kern_bytes"], r["kern_us"]
+    dom = max(("index_score", "sattn"), key=lambda k: ku[k])
+    achieved = kb[dom] / (ku[dom] * 1e-6) / 1e9
+    alg = survey_bytes(cfg)
+    frac_step = alg / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS
+    cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_budget)
+    out = {
+        "metric": "attn decode us/layer-step + % HBM roofline @128Kx4 slots; prefill tok/s @2K chunk",
+        "value": round(r["step_us"], 3),
+        "unit": "us/layer-step",
+        "n_gpus": 1,
+        "steps": r["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(r["step_us"] / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16+fp8e4m3",
+        "data": "synthetic (seeded Gaussian, FP4-grid index keys with x8 outlier channels, e4m3 + per-row scale)",
+        "config": {"workload": f"{cfg.name}: decode, 1 layer, {cfg.slots} slots x {cfg.ctx[0]} ctx, ratio "
+                               f"{cfg.ratio}, top-k {cfg.topk}, SWA {128}, 64 heads x 576 (V 512)",
+                   "cache_copies": args.layers},
+        "hbm_roofline_pct": round(100.0 * frac_step, 2),
+        "algorithmic_bytes_per_step": alg,
+        "kernel_us": {k: round(v, 3) for k, v in ku.items()},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": kb[dom]},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

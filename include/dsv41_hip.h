@@ -1,0 +1,108 @@
+/*
+ * dsv41_hip.h -- C ABI of the MI355X (gfx950) sparse-attention path of DeepSeek-V4.1 as the dsv41 runtime runs it.
+ *
+ * Conventions (every entry point):
+ *   - plain device pointers, element counts / strides in ELEMENTS of the pointed-to type unless stated (bytes for
+ *     e4m3 key tables), bf16 tensors passed as raw 16-bit storage;
+ *   - `stream` is a hipStream_t (the caller's current stream); nothing synchronises, nothing allocates: scratch
+ *     memory is a caller-provided workspace sized by the matching *_workspace_bytes query;
+ *   - every call is legal under stream capture;
+ *   - return value: 0 on success, otherwise a hipError_t code (hipErrorInvalidValue = 1 for rejected shapes).
+ * The Python shims in dsv41_amd/ keep the reference's call signatures and raise RuntimeError on a non-zero code
+ * (the reference's launch helper does the same, dsv41/cukern.py:19-21, :34-57).
+ */
+#ifndef DSV41_HIP_H
+#define DSV41_HIP_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------------------------------ attention */
+
+/* Workspace bytes for R query rows x H heads over L key positions with output width dv (0 when one split covers
+ * a row).  want_nsplit <= 0 lets the library choose the split count; pass the same value to the launch. */
+long dsv41_attn_workspace_bytes(int R, int H, int L, int dv, int want_nsplit);
+
+/* kernels.sparse_attn (dsv41/kernels.py:172-256) and fused.sparse_attn_decode (dsv41/fused.py:269-280).
+ * q [b, s, h, dqk] bf16; kv [b, n_kv, dqk] bf16 (slot stride kv_bstride); idx [b, s, t] int32, -1 or >= n_kv =
+ * empty; sink [h] fp32; out [b, s, h, dv] bf16 (V = the first dv columns of each kv row). */
+int dsv41_sparse_attn(const void* q, const void* kv, const float* sink, const int* idx, void* out, int b, int s, int h,
+                      int dqk, int dv, int n_kv, long kv_bstride, int t, float scale, int want_nsplit, void* ws,
+                      long ws_bytes, void* stream);
+
+/* fused.sparse_attn_decode2 / sparse_attn_decode_split (dsv41/fused.py:352-403, :406-472): one query per batch
+ * row; index < n1 reads kv1[b, index], otherwise kv2[b, index - n1]. */
+int dsv41_sparse_attn2(const void* q, const void* kv1, const void* kv2, const float* sink, const int* idx, void* out,
+                       int b, int h, int d, int n1, long kv1_bstride, int n2, long kv2_bstride, int t, float scale,
+                       int want_nsplit, void* ws, long ws_bytes, void* stream);
+
+/* fused2.sattn2 (dsv41/fused2.py:334-446): query row b at position pos[b] of sequence seq[b] over that sequence's
+ * SWA ring kv_win[seq, 0..win) (slot validity from pos/pmax/plim, dsv41/fused2.py:355-360) and the compressed rows
+ * kv_c[seq, idx[b, :]]; LSE combine with the sink, bf16 round, inverse rope on the last rd output columns (rd = 0:
+ * none).  dqk = 512 with dv = 512 is the reference geometry (K = V = the row); dqk = 576, dv = 512 is absorbed MLA
+ * (V = the 512 latent columns).  plim may be null (= pos). */
+int dsv41_sattn2(const void* q, const void* kv_win, long win_sstride, int win, const void* kv_c, long c_sstride,
+                 int n_c_rows, const int* idx, int t, const long* pos, const long* seq, const long* pmax,
+                 const long* plim, const float* sink, const float* cos_t, const float* sin_t, int rd, float scale,
+                 void* out, int B, int h, int dqk, int dv, int want_nsplit, void* ws, long ws_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------ indexer */
+
+/* fused3.index_score (dsv41/fused3.py:20-62) and the score half of Indexer.__call__ (dsv41/model.py:766-893):
+ * out[r, t] = sum_h w[r,h] * relu(q[r,h,:] . key[slot(r), t, :]) for t < cl(r), -inf for cl(r) <= t < n_pos when
+ * write_masked.  q [R, HI, 128] bf16, w [R, HI] fp32 (HI <= 64).  kfmt 0: keys bf16 [S, rows, 128] (k_sstride in
+ * elements); kfmt 1: keys e4m3 [S, rows, 128] (k_sstride in bytes) times kscale [S, rows] fp32.
+ * slot(r) = seq[r] (or r / rows_per_slot when seq is null); cl(r) = cl[r] (or (cl_start + r % rows_per_slot + 1) /
+ * cl_ratio, the causal compressed length of a prefill chunk, dsv41/model.py:819-830, when cl is null). */
+int dsv41_index_score(const void* q, long q_rstride, const float* w, long w_rstride, int R, int HI, int D, int kfmt,
+                      const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
+                      int rows_per_slot, const long* cl, long cl_start, int cl_ratio, int n_pos, int write_masked,
+                      float* out, long out_rstride, void* stream);
+
+/* fused3.topk_indices + cuda/topk_select.cu (dsv41/fused3.py:65-75, dsv41/cuda/topk_select.cu:94-168), also the
+ * selection of Indexer.__call__ (dsv41/model.py:868-893): per row the k largest of score[r, 0..c) with c =
+ * min(cl(r), n), ascending, + offset; positions past the selection (c < k) are -1.  Ties: lower index first. */
+int dsv41_topk_indices(const float* score, long ld, int R, int n, int k, const long* cl, long cl_start, int cl_ratio,
+                       int rows_per_seq, int offset, int* out, long out_rstride, void* stream);
+
+/* ------------------------------------------------------------------------------------------------ appends */
+
+/* fused2.kv_write (dsv41/fused2.py:276-330) and the ring commit of Attention._window_kv (dsv41/model.py:1057-1298):
+ * row r of x -> rmsnorm(w) -> bf16 -> rope(last rd, position p) -> bf16 -> fq8/32 -> cache[s, p % W] (rows r >=
+ * commit_from only) and tmp[r] (when tmp != null).  p = pos[r] or pos0 + r * pos_stride; s = seq[r] or
+ * r / rows_per_seq. */
+int dsv41_kv_write(const void* x, long x_rstride, const void* w, const float* cos_t, const float* sin_t,
+                   const long* pos, const long* seq, long pos0, long pos_stride, int rows_per_seq, void* cache,
+                   long cache_sstride, int W, void* tmp, int n_rows, int D, int rd, float eps, int commit_from,
+                   void* stream);
+
+/* Compressed-KV append (dsv41/decode.py:157-164, dsv41/model.py:1320-1348, SharedAttn.write_compress_kv :508-541)
+ * and index-key append (dsv41/decode.py:270-282, dsv41/model.py:696-732, SharedAttn.write_index_k :543-574):
+ * row r of x -> [rmsnorm(norm_w)] -> [rope(last rd) at (pos[r] or pos0 + r*pos_stride) + pos_add] -> fake quant
+ * (qmode 0 fp8 pow2, 1 fp4 pow2, 2 fp4 e4m3-scale; group 16/32; -1 none) -> bf16 cache[s, row] with s = seq[r] or
+ * r / rows_per_seq and row = row[r] or row0 + r % rows_per_seq (row < 0: no write).  When k8 != null also writes
+ * the e4m3 encoding with a per-row power-of-two scale: k8[s, row, :] (bytes) and ks[s, row]. */
+int dsv41_append_rows(const void* x, long x_rstride, const void* norm_w, float eps, const float* cos_t,
+                      const float* sin_t, int rd, const long* pos, long pos0, long pos_stride, long pos_add,
+                      const long* seq, int rows_per_seq, const long* row, long row0, void* cache, long cache_sstride,
+                      int qmode, int group, void* k8, long k8_sstride, float* ks, long ks_sstride, int n_rows, int D,
+                      void* stream);
+
+/* ------------------------------------------------------------------------------------------------ numerics */
+
+/* fake_quant_fp8 / fake_quant_fp4 (dsv41/fused.py:46-87, dsv41/quant.py:45-87) on rows of D bf16 values. */
+int dsv41_fake_quant(const void* x, void* y, long n_rows, int D, int group, int mode, void* stream);
+
+/* rope_ / rope_dev_ (dsv41/fused.py:203-234, :319-349): in place on the last rd of each row of x [n_rows, D]
+ * (rows ordered (b, s, h)); position = (pos ? pos[b] + add : pos0) + s * pos_stride. */
+int dsv41_rope(void* x, const float* cos_t, const float* sin_t, const long* pos, long pos0, long add, long pos_stride,
+               long n_rows, int H, int S, int D, int rd, int inverse, void* stream);
+
+/* rmsnorm (dsv41/fused.py:91-109): y = x / sqrt(mean(x^2) + eps) * w, bf16 rows. */
+int dsv41_rmsnorm(const void* x, const void* w, void* y, long n_rows, int D, float eps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DSV41_HIP_H */

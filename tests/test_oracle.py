@@ -1,0 +1,265 @@
+"""Pins the CPU oracle (oracle/dsv41_oracle.py) against known answers, library routines, closed forms and brute
+force -- never against a retyped copy of its own formula.  CPU only."""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dsv41_oracle as O
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "known_answers.json")))
+
+
+def test_bf16_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10.0,
+                        np.array([0.0, -0.0, 1e-40, 3.4e38, 1.00390625, 1.01171875], np.float32)])
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(O.bf16(x), ref)
+
+
+def test_round_e4m3_known_and_torch():
+    np.testing.assert_array_equal(O.round_e4m3(np.array(GOLD["round_e4m3_in"], np.float32)),
+                                  np.array(GOLD["round_e4m3_out"], np.float32))
+    rng = np.random.default_rng(1)
+    x = np.clip(rng.standard_normal(65536).astype(np.float32) * np.exp2(rng.integers(-12, 9, 65536)), -448, 448)
+    x = x.astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(O.round_e4m3(x), ref)
+    # every e4m3 value is a fixed point
+    allv = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    allv = allv[np.isfinite(allv)]
+    np.testing.assert_array_equal(O.round_e4m3(allv), allv)
+
+
+def test_round_e2m1_known_answers():
+    np.testing.assert_array_equal(O.round_e2m1(np.array(GOLD["round_e2m1_in"], np.float32)),
+                                  np.array(GOLD["round_e2m1_out"], np.float32))
+    g = np.array(GOLD["e2m1_grid"], np.float32)
+    np.testing.assert_array_equal(O.round_e2m1(g), g)
+
+
+def test_ceil_log2_known():
+    np.testing.assert_array_equal(O.ceil_log2(np.array(GOLD["ceil_log2_in"], np.float32)), GOLD["ceil_log2_out"])
+    for v in [1e-30, 0.3, 1.0, 7.0, 1e20]:
+        assert int(O.ceil_log2(np.array([v], np.float32))[0]) == math.ceil(math.log2(np.float32(v)))
+
+
+def test_fake_quant_fp8_against_library_cast():
+    rng = np.random.default_rng(2)
+    x = O.bf16(rng.standard_normal((64, 256)).astype(np.float32) * 3)
+    y = O.fake_quant_fp8(x, 32)
+    g = x.reshape(-1, 32)
+    amax = np.maximum(np.abs(g).max(1, keepdims=True), 1e-4)
+    s = np.exp2(np.ceil(np.log2(amax.astype(np.float64) / 448.0))).astype(np.float32)
+    ref = torch.from_numpy(np.clip(g / s, -448, 448)).to(torch.float8_e4m3fn).float().numpy() * s
+    np.testing.assert_array_equal(y.reshape(-1, 32), ref)
+    np.testing.assert_array_equal(O.fake_quant_fp8(y, 32), y)  # idempotent
+    row = ((np.arange(32) - 15.5) * 0.25).astype(np.float32)
+    q = O.fake_quant_fp8(row, 32)
+    assert GOLD["fake_quant_fp8_row"]["scale"] == 0.015625
+    # |v| < 2: at most 4 significant bits at scale 2^-6 -> exact; above 2 the e4m3 ulp (16 x 2^-6) rounds to even
+    np.testing.assert_array_equal(q[8:24], row[8:24])
+    np.testing.assert_array_equal(q[:8], [-4.0, -3.5, -3.5, -3.0, -3.0, -2.5, -2.5, -2.0])
+
+
+@pytest.mark.parametrize("scale_e4m3,block", [(False, 32), (True, 16)])
+def test_fake_quant_fp4_grid_and_idempotence(scale_e4m3, block):
+    rng = np.random.default_rng(3)
+    x = O.bf16(rng.standard_normal((32, 576)).astype(np.float32))
+    y = O.fake_quant_fp4(x, block, scale_e4m3)
+    g = y.reshape(-1, block)
+    xg = x.reshape(-1, block)
+    amax = np.abs(xg).max(1, keepdims=True)
+    if scale_e4m3:
+        s = torch.from_numpy(np.maximum(amax, 6 * 2.0 ** -9).astype(np.float32) / 6).to(torch.float8_e4m3fn)
+        s = s.float().numpy()
+    else:
+        s = np.exp2(np.ceil(np.log2(amax.astype(np.float64) / 6.0))).astype(np.float32)
+    q = g / s
+    grid = np.array(GOLD["e2m1_grid"], np.float32)
+    assert np.isin(q, grid).all()
+    # nearest grid value (brute force over the grid); ties to the even code
+    xs = np.clip(xg / s, -6, 6)
+    d = np.abs(xs[..., None] - grid[None, None, :])
+    best = d.min(-1)
+    assert np.all(np.abs(np.abs(xs - q) - best) <= 1e-6)
+    np.testing.assert_array_equal(O.fake_quant_fp4(y, block, scale_e4m3), y)
+
+
+def test_key_encode_fp8_exact_on_fp4_grid_rows():
+    rng = np.random.default_rng(4)
+    k = O.bf16(O.fake_quant_fp4(O.bf16(rng.standard_normal((512, 128)).astype(np.float32) * 0.1), 32))
+    q, s = O.key_encode_fp8(k)
+    np.testing.assert_array_equal(q * s, k)
+    ref = torch.from_numpy(q).to(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(ref, q)
+
+
+def test_rope_against_complex_rotation_and_inverse():
+    cos, sin = O.rope_tables(64, 4096, 65536, 160000.0, 16.0, 32, 1)
+    rng = np.random.default_rng(5)
+    x = O.bf16(rng.standard_normal((3, 512)).astype(np.float32))
+    pos = np.array([100, 101, 102])
+    y = O.rope(x, cos, sin, pos, 64)
+    z = x[:, -64:].reshape(3, 32, 2)
+    c = (z[..., 0] + 1j * z[..., 1]) * (cos[pos] + 1j * sin[pos])
+    ref = np.stack([c.real, c.imag], -1).reshape(3, 64)
+    np.testing.assert_allclose(y[:, -64:], ref, atol=0.02, rtol=0.01)
+    np.testing.assert_array_equal(y[:, :-64], x[:, :-64])
+    back = O.rope(y, cos, sin, pos, 64, inverse=True)
+    np.testing.assert_allclose(back, x, atol=0.03)
+    # the table itself: angle = pos * freq with freq from the YaRN ramp; pos 0 is the identity
+    np.testing.assert_array_equal(cos[0], np.ones(32, np.float32))
+    np.testing.assert_array_equal(sin[0], np.zeros(32, np.float32))
+
+
+@pytest.mark.parametrize("start", [0, 3, 127, 128, 300])
+def test_window_idx_brute_force(start):
+    W, S = 128, 7
+    idx = O.window_idx(W, S, start)
+    for i in range(S):
+        q = start + i
+        if start == 0:
+            want = [p for p in range(max(0, q - W + 1), q + 1)]
+            got = [v for v in idx[i] if v >= 0]
+            assert got == want
+        else:
+            want = sorted(p % W for p in range(max(0, q - W + 1), q + 1))
+            got = sorted(v for v in idx[i] if v >= 0)
+            assert got == want
+
+
+@pytest.mark.parametrize("pos,pmax,plim", [(50, 50, 50), (300, 300, 300), (301, 305, 301), (0, 0, 0), (130, 135, 132)])
+def test_ring_valid_brute_force(pos, pmax, plim):
+    W = 128
+    v = O.ring_valid(pos, pmax, plim, W)
+    # brute force: slot s holds the newest position p <= pmax with p % W == s
+    for s in range(W):
+        held = max([p for p in range(0, pmax + 1) if p % W == s], default=-1)
+        want = held >= 0 and held <= plim and pos - held < W
+        assert bool(v[s]) == want
+
+
+def _dense_attn(q, rows, valid, sink, scale):
+    """Dense softmax over [scores ; sink], sink column dropped after the softmax (dsv41/test_kernels.py:40-49)."""
+    sc = (q.astype(np.float64) @ rows.astype(np.float64).T) * scale
+    sc = np.where(valid[None, :], sc, -np.inf)
+    sc = np.concatenate([sc, sink[:, None].astype(np.float64)], 1)
+    sc = sc - sc.max(1, keepdims=True)
+    p = np.exp(sc)
+    p = p / p.sum(1, keepdims=True)
+    return p[:, :-1] @ rows.astype(np.float64)
+
+
+def test_sparse_attn_vs_dense_softmax():
+    rng = np.random.default_rng(6)
+    b, s, h, d, n = 1, 5, 4, 64, 40
+    q = O.bf16(rng.standard_normal((b, s, h, d)).astype(np.float32))
+    kv = O.bf16(rng.standard_normal((b, n, d)).astype(np.float32))
+    sink = rng.standard_normal(h).astype(np.float32)
+    idx = rng.integers(0, n, (b, s, 8)).astype(np.int32)
+    idx[0, 0, :3] = -1
+    o = O.sparse_attn(q, kv, sink, idx, d ** -0.5)
+    for i in range(s):
+        sel = idx[0, i]
+        ref = _dense_attn(q[0, i], kv[0, np.maximum(sel, 0)], sel >= 0, sink, d ** -0.5)
+        np.testing.assert_allclose(o[0, i], ref, atol=2e-2)
+    # all-invalid row -> zeros
+    idx2 = np.full((1, 1, 8), -1, np.int32)
+    assert np.all(O.sparse_attn(q[:, :1], kv, sink, idx2, 0.1) == 0)
+
+
+def test_sattn2_equals_decode_over_explicit_indices():
+    rng = np.random.default_rng(7)
+    H, d, W, rd = 16, 64, 32, 16
+    cos, sin = O.rope_tables(rd, 1024, 0, 10000.0, 1.0, 32, 1)
+    q = O.bf16(rng.standard_normal((1, 1, H, d)).astype(np.float32))
+    ring = O.bf16(rng.standard_normal((1, W, d)).astype(np.float32))
+    ckv = O.bf16(rng.standard_normal((1, 300, d)).astype(np.float32))
+    sink = rng.standard_normal(H).astype(np.float32)
+    for p in (10, 100):
+        idx = rng.integers(0, 150, (1, 1, 48)).astype(np.int32)
+        idx[..., 40:] = -1
+        o = O.sattn2(q, ring, ckv, idx, [p], [0], [p], None, sink, cos, sin, rd, d ** -0.5)
+        slot = p % W
+        widx = (np.arange(W) + slot + 1) % W
+        widx = np.where(widx > p, -1, widx).astype(np.int32)
+        full = np.concatenate([widx, np.where(idx[0, 0] >= 0, idx[0, 0] + W, -1)])[None, None]
+        ref = O.sparse_attn_decode2(q, ring, ckv, sink, full, d ** -0.5)
+        ref = O.rope(ref[0, 0], cos, sin, np.int64(p), rd, inverse=True)
+        np.testing.assert_allclose(o[0, 0], ref, atol=1e-6)
+        # split invariance: two halves merged by log-sum-exp == single pass (dsv41/test_fused.py:90-94)
+        rows = np.concatenate([ring[0], ckv[0][np.maximum(idx[0, 0], 0)]])
+        valid = np.concatenate([O.ring_valid(p, p, p, W), idx[0, 0] >= 0])
+        sc = (q[0, 0] @ rows.T) * d ** -0.5
+        sc = np.where(valid[None], sc, -1e30)
+        parts = []
+        for a, b in ((0, 40), (40, rows.shape[0])):
+            m = sc[:, a:b].max(1)
+            pp = np.where(valid[None, a:b], np.exp(sc[:, a:b] - m[:, None]), 0)
+            parts.append((m, pp.sum(1), pp @ rows[a:b]))
+        mx = np.maximum(parts[0][0], parts[1][0])
+        num = sum(np.exp(m - mx)[:, None] * acc for m, l, acc in parts)
+        den = sum(np.exp(m - mx) * l for m, l, acc in parts) + np.exp(sink - mx)
+        merged = O.rope(O.bf16(num / den[:, None]), cos, sin, np.int64(p), rd, inverse=True)
+        np.testing.assert_allclose(o[0, 0], merged, atol=2e-2)
+
+
+def test_index_score_brute_force_and_chunk_invariance():
+    rng = np.random.default_rng(8)
+    B, H, D, n = 2, 8, 128, 50
+    q = rng.standard_normal((B, 1, H, D)).astype(np.float32)
+    keys = rng.standard_normal((3, n, D)).astype(np.float32)
+    w = rng.standard_normal((B, H)).astype(np.float32)
+    seq = [2, 0]
+    cl = [37, 50]
+    s = O.index_score(q, keys, w, seq, cl)
+    for b in range(B):
+        for t in range(n):
+            if t >= cl[b]:
+                assert s[b, t] == -np.inf
+                continue
+            ref = sum(float(w[b, h]) * max(0.0, float(np.dot(q[b, 0, h].astype(np.float64), keys[seq[b], t])))
+                      for h in range(H))
+            assert abs(s[b, t] - ref) <= 1e-4 * (1 + abs(ref))
+    # prefill: chunked == full exactly (dsv41/test_long_prefill.py:66-96)
+    qp = O.bf16(rng.standard_normal((1, 40, H, D)).astype(np.float32))
+    wp = rng.standard_normal((1, 40, H)).astype(np.float32)
+    kp = O.bf16(rng.standard_normal((1, 60, D)).astype(np.float32))
+    a = O.indexer_prefill(qp, wp, kp, 200, 4, 16, 128, query_chunk=7)
+    b = O.indexer_prefill(qp, wp, kp, 200, 4, 16, 128, query_chunk=1000)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_topk_brute_force():
+    rng = np.random.default_rng(9)
+    for n, k, cl in [(100, 10, 100), (100, 10, 60), (100, 10, 7), (1000, 64, 999), (37, 37, 37)]:
+        sc = rng.standard_normal((3, n)).astype(np.float32)
+        sc[1, ::3] = sc[1, 0]  # ties
+        out = O.topk_indices(sc, k, [cl] * 3)
+        for r in range(3):
+            c = min(cl, n)
+            want = sorted(sorted(range(c), key=lambda i: (-float(sc[r, i]), i))[:k])
+            want = want + [-1] * (k - len(want))
+            assert out[r].tolist() == want
+    for name in ("topk_ties", "topk_cl_short", "topk_negzero"):
+        g = GOLD[name]
+        out = O.topk_indices(np.array([g["score"]], np.float32), g["k"], [g["cl"]])
+        assert out[0].tolist() == g["out"], name
+
+
+def test_kv_write_composition():
+    rng = np.random.default_rng(10)
+    d, W, rd = 512, 128, 64
+    cos, sin = O.rope_tables(rd, 4096, 0, 10000.0, 1.0, 32, 1)
+    x = O.bf16(rng.standard_normal((2, d)).astype(np.float32) * 2)
+    w = O.bf16(rng.random(d).astype(np.float32) + 0.5)
+    cache = np.zeros((3, W, d), np.float32)
+    out = O.kv_write(x, w, cos, sin, [300, 5], [2, 0], cache, rd, 1e-6)
+    row = O.rope(O.bf16(O.rmsnorm(x[0:1], w, 1e-6)), cos, sin, np.int64(300), rd)
+    np.testing.assert_array_equal(out[2, 300 % W], O.bf16(O.fake_quant_fp8(row, 32))[0])
+    assert np.count_nonzero(out) == np.count_nonzero(out[2, 300 % W]) + np.count_nonzero(out[0, 5])
