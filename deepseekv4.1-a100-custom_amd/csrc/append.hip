@@ -1,36 +1,20 @@
 // Cache-append kernels of the sparse-attention path and the small per-row numerics they fuse:
-//   dsv41_kv_write      SWA ring append (rmsnorm -> bf16 -> rope -> bf16 -> fq8/32 -> ring[seq, pos % W])
-//   dsv41_append_rows   compressed-KV / index-key append (optional rmsnorm, rope, fq4 or fq8, optional e4m3 sidecar)
-//   dsv41_fake_quant    standalone fake quantisation (fp8 pow2 / fp4 pow2 / fp4 e4m3-scale)
-//   dsv41_rope          in-place rotary on the last rd columns (host or device positions)
-//   dsv41_rmsnorm       standalone rmsnorm
-// One workgroup of 64 lanes (one wave) per row: rows are <= 576 wide, so a wave owns a row and every reduction is
-// a cross-lane shuffle; per-32/16 groups map onto lane groups.  These are tiny HBM-bound kernels.
+//   dsv41_kv_write        SWA ring append (rmsnorm -> bf16 -> rope -> bf16 -> fq8/32 -> ring[seq, pos % W])
+//   dsv41_append_rows     compressed-KV / index-key append (optional rmsnorm, rope, fq4 or fq8, optional e4m3 copy)
+//   dsv41_decode_appends  every cache write of a decode step + the e4m3 preparation of the index queries, one launch
+//   dsv41_index_qprep     the index-query preparation alone
+//   dsv41_fake_quant / dsv41_rope / dsv41_rmsnorm   standalone numerics
+//
+// One 256-thread block per row operation; element e of a row lives in thread e % 256 (iteration e / 256), so a
+// quantisation group of 16/32 elements is 16/32 consecutive lanes of one wave (shuffle reductions) and a rope pair
+// (2j, 2j+1) is a lane pair (xor 1).  The code is deliberately small and loop-shaped: these launches sit on the
+// decode critical path, where a cold instruction cache costs more than the arithmetic.
 #include "common.h"
 
 namespace {
 
-constexpr int kMaxD = 1024;  // widest row handled (elements); each lane holds kMaxD/64 = 16 values
-
-// Reduction over the 64 lanes of a wave.
-DSV41_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += wave_shfl_xor(v, m);
-  return v;
-}
-
-// Lane l owns columns [l*per, (l+1)*per) of the row (per = PER, chosen by pick_per); lanes past the row hold zeros.
-
-// Group amax across the lanes sharing a quantisation group of `group` columns (group = 16 or 32, per | group or
-// group | per).
-DSV41_DEV float group_amax(float local, int per, int group) {
-  float a = local;
-  if (per < group) {
-    const int lanes = group / per;  // 2..32, power of two
-    for (int m = 1; m < lanes; m <<= 1) a = fmaxf(a, wave_shfl_xor(a, m));
-  }
-  return a;
-}
+constexpr int kRowThreads = 256;
+constexpr int kMaxIters = 4;  // rows up to 1024 elements
 
 // mode 0: fp8 e4m3, pow2 scale (amax >= 1e-4);  1: fp4 e2m1, pow2 scale;  2: fp4 e2m1, e4m3-rounded scale.
 DSV41_DEV float fq_scale(float amax, int mode) {
@@ -44,188 +28,356 @@ DSV41_DEV float fq_value(float x, float s, int mode) {
   return round_e2m1(fminf(fmaxf(__fdiv_rn(x, s), -6.0f), 6.0f)) * s;
 }
 
-// Quantise the lane's `per` contiguous values in place (groups of `group` columns).
-template <int PER>
-DSV41_DEV void fake_quant_lane(float (&v)[PER], int per, int group, int mode) {
-  if (per <= group) {
+// Block-wide sum / max of one float per thread (256 threads); red holds >= 4 floats.
+DSV41_DEV float block_sum(float v, float* red) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += wave_shfl_xor(v, m);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+DSV41_DEV float block_max(float v, float* red) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, wave_shfl_xor(v, m));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+struct RowOp {
+  const uint16_t* x;  // input row (bf16), D elements
+  int D;
+  const uint16_t* norm_w;  // rmsnorm weight (bf16) or null
+  float eps;
+  const float* cos_t;  // rope tables [pos][rd/2] (rd = 0: no rope)
+  const float* sin_t;
+  int rd;
+  long pos;
+  int qmode, group;  // fake quantisation (qmode < 0: none)
+  uint16_t* out;     // bf16 destination row or null
+  uint16_t* out2;    // second bf16 destination (temporary KV) or null
+  uint8_t* k8;       // e4m3 destination row (per-row pow2 scale in *ks) or null
+  float* ks;
+};
+
+// [rmsnorm -> bf16] -> [rope -> bf16] -> [fake quant] -> stores.  Every thread of the block must call it.
+DSV41_DEV void row_op(const RowOp& o, float* red) {
+  const int t = threadIdx.x;
+  const int p = o.pos < 0 ? 0 : (int)o.pos;
+  float v[kMaxIters], w[kMaxIters], cs[kMaxIters], sn[kMaxIters];
+#pragma unroll
+  for (int u = 0; u < kMaxIters; ++u) {  // all loads first
+    const int e = t + u * kRowThreads;
+    const int ec = e < o.D ? e : 0;
+    v[u] = bf2f(o.x[ec]);
+    w[u] = o.norm_w ? bf2f(o.norm_w[ec]) : 1.0f;
+    const int j = (ec - (o.D - o.rd)) >> 1;
+    const bool rope = o.rd > 0 && e < o.D && e >= o.D - o.rd;
+    cs[u] = rope ? o.cos_t[(long)p * (o.rd / 2) + j] : 1.0f;
+    sn[u] = rope ? o.sin_t[(long)p * (o.rd / 2) + j] : 0.0f;
+    if (e >= o.D) v[u] = 0.0f;
+  }
+  if (o.norm_w) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kMaxIters; ++u) ss += v[u] * v[u];
+    ss = block_sum(ss, red);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)o.D) + o.eps));
+#pragma unroll
+    for (int u = 0; u < kMaxIters; ++u) v[u] = round_bf16(v[u] * inv * w[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < kMaxIters; ++u) {
+    if (u * kRowThreads >= o.D) break;
+    if (o.rd > 0) {
+      const float partner = wave_shfl_xor(v[u], 1);
+      const int e = t + u * kRowThreads;
+      if (e >= o.D - o.rd && e < o.D)
+        v[u] = (e & 1) ? round_bf16(partner * sn[u] + v[u] * cs[u]) : round_bf16(v[u] * cs[u] - partner * sn[u]);
+    }
+    if (o.qmode >= 0) {
+      float a = fabsf(v[u]);
+#pragma unroll 1
+      for (int m = 1; m < o.group; m <<= 1) a = fmaxf(a, wave_shfl_xor(a, m));
+      v[u] = fq_value(v[u], fq_scale(a, o.qmode), o.qmode);
+    }
+    const int e = t + u * kRowThreads;
+    if (e < o.D) {
+      const uint16_t b = f2bf(v[u]);
+      if (o.out) o.out[e] = b;
+      if (o.out2) o.out2[e] = b;
+    }
+  }
+  if (o.k8) {  // e4m3 copy of the stored bf16 values with one power-of-two scale per row
     float a = 0.0f;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) if (i < per) a = fmaxf(a, fabsf(v[i]));
-    a = group_amax(a, per, group);
-    const float s = fq_scale(a, mode);
+    for (int u = 0; u < kMaxIters; ++u) a = fmaxf(a, fabsf(round_bf16(v[u])));
+    a = block_max(a, red);
+    int ex = ceil_log2_f(__fdiv_rn(fmaxf(a, 1e-30f), 448.0f));
+    ex = ex < -126 ? -126 : ex;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) if (i < per) v[i] = fq_value(v[i], s, mode);
-  } else {  // several groups inside one lane
-    for (int g0 = 0; g0 < per; g0 += group) {
-      float a = 0.0f;
+    for (int u = 0; u < kMaxIters; ++u) {
+      const int e = t + u * kRowThreads;
+      if (e < o.D)
+        o.k8[e] = (uint8_t)e4m3_bits(round_e4m3(fminf(fmaxf(round_bf16(v[u]) * pow2i(-ex), -448.0f), 448.0f)));
+    }
+    if (t == 0) *o.ks = pow2i(ex);
+  }
+}
+
+// Index-query preparation for the fp8 score MFMA: per head h (<= 64 heads, 128 wide) a power-of-two scale
+// 2^e = 2^ceil(log2(amax / 448)), q8[h] = e4m3(q[h] / 2^e) and wf[h] = w[h] * 2^e (the scale folds into the head
+// weight because relu(s * x) = s * relu(x) for s > 0).  Exact for the reference's FP4-grid queries.
+DSV41_DEV void qprep_op(const uint16_t* q, const uint16_t* w_bf16, const float* w_f32, int HI, uint8_t* q8,
+                        float* wf) {
+  const int t = threadIdx.x, h = t >> 2, part = t & 3;
+  const int hc = h < HI ? h : HI - 1;
+  const uint4* src = (const uint4*)(q + (long)hc * 128 + part * 32);
+  uint4 raw[4];
 #pragma unroll
-      for (int i = 0; i < PER; ++i) if (i >= g0 && i < g0 + group) a = fmaxf(a, fabsf(v[i]));
-      const float s = fq_scale(a, mode);
+  for (int u = 0; u < 4; ++u) raw[u] = src[u];
+  const float wv = w_bf16 ? bf2f(w_bf16[hc]) : w_f32[hc];
+  float x[32];
+  float amax = 0.0f;
 #pragma unroll
-      for (int i = 0; i < PER; ++i) if (i >= g0 && i < g0 + group) v[i] = fq_value(v[i], s, mode);
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t ww[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[u * 8 + 2 * e] = __uint_as_float(ww[e] << 16);
+      x[u * 8 + 2 * e + 1] = __uint_as_float(ww[e] & 0xffff0000u);
     }
   }
-}
-
-// Rotate the interleaved (re, im) pairs of the last rd columns at position pos; values stay fp32 and are
-// rounded to bf16 (the reference stores each rotated component as bf16).  `per` is even, so pairs never straddle
-// lanes.
-template <int PER>
-DSV41_DEV void rope_lane(float (&v)[PER], int lane, int per, int D, int rd, const float* cos_t, const float* sin_t,
-                         long pos, bool inverse) {
-  const int c0 = lane * per;
 #pragma unroll
-  for (int i = 0; i < PER; i += 2) {
-    const int c = c0 + i;
-    if (i < per && c >= D - rd && c < D) {
-      const int j = (c - (D - rd)) >> 1;
-      const float cs = cos_t[pos * (rd / 2) + j];
-      float sn = sin_t[pos * (rd / 2) + j];
-      if (inverse) sn = -sn;
-      const float xr = v[i], xi = v[i + 1];
-      v[i] = round_bf16(xr * cs - xi * sn);
-      v[i + 1] = round_bf16(xr * sn + xi * cs);
-    }
+  for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(x[e]));
+  amax = fmaxf(amax, wave_shfl_xor(amax, 1));
+  amax = fmaxf(amax, wave_shfl_xor(amax, 2));
+  int ex = ceil_log2_f(fmaxf(amax, 1e-30f) * (1.0f / 448.0f));
+  ex = ex < -126 ? -126 : ex;
+  const float inv = pow2i(-ex);
+  uint32_t pk[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    int wd = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * d] * inv, x[4 * d + 1] * inv, 0, false);
+    wd = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * d + 2] * inv, x[4 * d + 3] * inv, wd, true);
+    pk[d] = (uint32_t)wd;
+  }
+  if (h < 64) {
+    uint4* dst = (uint4*)(q8 + (long)h * 128 + part * 32);
+    dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+    if (part == 0) wf[h] = h < HI ? wv * pow2i(ex) : 0.0f;
   }
 }
 
-template <int PER>
-DSV41_DEV void load_row(float (&v)[PER], const uint16_t* x, int lane, int per, int D) {
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int c = lane * per + i;
-    v[i] = (i < per && c < D) ? bf2f(x[c]) : 0.0f;
-  }
-}
+// ---------------------------------------------------------------------------------------------- kernels
+struct KvWriteArgs {
+  const uint16_t* x;
+  long x_rstride;
+  const uint16_t* w;
+  const float* cos_t;
+  const float* sin_t;
+  const long* pos;
+  const long* seq;
+  long pos0, pos_stride;
+  int rows_per_seq;
+  uint16_t* cache;
+  long cache_sstride;
+  int W;
+  uint16_t* tmp;
+  int D, rd;
+  float eps;
+  int commit_from;
+};
 
-template <int PER>
-DSV41_DEV void rmsnorm_lane(float (&v)[PER], int lane, int per, int D, const uint16_t* w, float eps) {
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) ss += v[i] * v[i];
-  ss = wave_sum(ss);
-  const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)D) + eps));
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int c = lane * per + i;
-    if (i < per && c < D) v[i] = round_bf16(v[i] * inv * bf2f(w[c]));
-  }
-}
-
-// ---------------------------------------------------------------------------------------------- kv_write
-// Row r: x[r] -> ring[seq[r], pos[r] % W] (and, when tmp != null, tmp[r]).  pos/seq may be null: then
-// pos = pos0 + r*pos_stride and seq = r / rows_per_seq.
-template <int PER>
-__global__ void __launch_bounds__(64) kv_write_kernel(const uint16_t* __restrict__ x, long x_rstride,
-                                                      const uint16_t* __restrict__ w, const float* __restrict__ cos_t,
-                                                      const float* __restrict__ sin_t, const long* __restrict__ pos,
-                                                      const long* __restrict__ seq, long pos0, long pos_stride,
-                                                      int rows_per_seq, uint16_t* __restrict__ cache,
-                                                      long cache_sstride, int W, uint16_t* __restrict__ tmp, int D,
-                                                      int rd, float eps, int commit_from) {
+__global__ void __launch_bounds__(kRowThreads) kv_write_kernel(const KvWriteArgs a) {
+  __shared__ float red[4];
   const int r = blockIdx.x;
-  const int lane = threadIdx.x;
-  constexpr int per = PER;
-  float v[PER];
-  load_row<PER>(v, x + (long)r * x_rstride, lane, per, D);
-  rmsnorm_lane<PER>(v, lane, per, D, w, eps);
-  long p = pos ? pos[r] : pos0 + (long)r * pos_stride;
+  long p = a.pos ? a.pos[r] : a.pos0 + (long)(r % a.rows_per_seq) * a.pos_stride;
   p = p < 0 ? 0 : p;
-  rope_lane<PER>(v, lane, per, D, rd, cos_t, sin_t, p, false);
-  fake_quant_lane<PER>(v, per, 32, 0);
-  uint16_t o[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) o[i] = f2bf(v[i]);
-  const long s = seq ? seq[r] : (long)(r / rows_per_seq);
-  if (r >= commit_from) {
-    uint16_t* dst = cache + s * cache_sstride + (p % W) * (long)D;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = lane * per + i;
-      if (i < per && c < D) dst[c] = o[i];
-    }
-  }
-  if (tmp) {
-    uint16_t* dst = tmp + (long)r * D;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = lane * per + i;
-      if (i < per && c < D) dst[c] = o[i];
-    }
-  }
+  const long s = a.seq ? a.seq[r] : (long)(r / a.rows_per_seq);
+  RowOp o{};
+  o.x = a.x + (long)r * a.x_rstride;
+  o.D = a.D;
+  o.norm_w = a.w;
+  o.eps = a.eps;
+  o.cos_t = a.cos_t;
+  o.sin_t = a.sin_t;
+  o.rd = a.rd;
+  o.pos = p;
+  o.qmode = 0;
+  o.group = 32;
+  o.out = r >= a.commit_from ? a.cache + s * a.cache_sstride + (p % a.W) * (long)a.D : nullptr;
+  o.out2 = a.tmp ? a.tmp + (long)r * a.D : nullptr;
+  row_op(o, red);
 }
 
-// ---------------------------------------------------------------------------------------------- append_rows
-// Row r of x -> [rmsnorm] -> [rope at pos] -> fake quant -> bf16 cache[seq, row]; optional e4m3 sidecar with a
-// per-row pow2 scale (k8[seq,row,:], ks[seq,row]).  row[r] < 0 skips the write.
-template <int PER>
-__global__ void __launch_bounds__(64) append_rows_kernel(
-    const uint16_t* __restrict__ x, long x_rstride, const uint16_t* __restrict__ norm_w, float eps,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int rd, const long* __restrict__ pos,
-    long pos0, long pos_stride, long pos_add, const long* __restrict__ seq, int rows_per_seq,
-    const long* __restrict__ row, long row0, uint16_t* __restrict__ cache, long cache_sstride, int qmode, int group,
-    uint8_t* __restrict__ k8, long k8_sstride, float* __restrict__ ks, long ks_sstride, int D) {
+struct AppendArgs {
+  const uint16_t* x;
+  long x_rstride;
+  const uint16_t* norm_w;
+  float eps;
+  const float* cos_t;
+  const float* sin_t;
+  int rd;
+  const long* pos;
+  long pos0, pos_stride, pos_add;
+  const long* seq;
+  int rows_per_seq;
+  const long* row;
+  long row0;
+  uint16_t* cache;
+  long cache_sstride;
+  int qmode, group;
+  uint8_t* k8;
+  long k8_sstride;
+  float* ks;
+  long ks_sstride;
+  int D;
+};
+
+__global__ void __launch_bounds__(kRowThreads) append_rows_kernel(const AppendArgs a) {
+  __shared__ float red[4];
   const int r = blockIdx.x;
-  const int lane = threadIdx.x;
-  constexpr int per = PER;
-  float v[PER];
-  load_row<PER>(v, x + (long)r * x_rstride, lane, per, D);
-  if (norm_w) rmsnorm_lane<PER>(v, lane, per, D, norm_w, eps);
-  if (rd > 0) {
-    long p = (pos ? pos[r] : pos0 + (long)r * pos_stride) + pos_add;
-    p = p < 0 ? 0 : p;
-    rope_lane<PER>(v, lane, per, D, rd, cos_t, sin_t, p, false);
-  }
-  if (qmode >= 0) fake_quant_lane<PER>(v, per, group, qmode);
-  const long s = seq ? seq[r] : (long)(r / rows_per_seq);
-  const long dr = row ? row[r] : row0 + (r % rows_per_seq);
-  if (dr < 0) return;
-  if (cache) {
-    uint16_t* dst = cache + s * cache_sstride + dr * (long)D;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = lane * per + i;
-      if (i < per && c < D) dst[c] = f2bf(v[i]);
-    }
-  }
-  if (k8) {
-    float a = 0.0f;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) a = fmaxf(a, fabsf(round_bf16(v[i])));
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) a = fmaxf(a, wave_shfl_xor(a, m));
-    int e = ceil_log2_f(__fdiv_rn(fmaxf(a, 1e-30f), 448.0f));
-    e = e < -126 ? -126 : e;
-    const float sc = pow2i(e);
-    uint8_t* d8 = k8 + s * k8_sstride + dr * (long)D;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = lane * per + i;
-      if (i < per && c < D)
-        d8[c] = (uint8_t)e4m3_bits(round_e4m3(fminf(fmaxf(round_bf16(v[i]) * pow2i(-e), -448.0f), 448.0f)));
-    }
-    if (lane == 0) ks[s * ks_sstride + dr] = sc;
-  }
+  const long s = a.seq ? a.seq[r] : (long)(r / a.rows_per_seq);
+  const long dr = a.row ? a.row[r] : a.row0 + (r % a.rows_per_seq);
+  if (dr < 0) return;  // uniform per block
+  RowOp o{};
+  o.x = a.x + (long)r * a.x_rstride;
+  o.D = a.D;
+  o.norm_w = a.norm_w;
+  o.eps = a.eps;
+  o.cos_t = a.cos_t;
+  o.sin_t = a.sin_t;
+  o.rd = a.rd;
+  o.pos = (a.pos ? a.pos[r] : a.pos0 + (long)(r % a.rows_per_seq) * a.pos_stride) + a.pos_add;
+  o.qmode = a.qmode;
+  o.group = a.group;
+  o.out = a.cache ? a.cache + s * a.cache_sstride + dr * (long)a.D : nullptr;
+  o.k8 = a.k8 ? a.k8 + s * a.k8_sstride + dr * (long)a.D : nullptr;
+  o.ks = a.ks ? a.ks + s * a.ks_sstride + dr : nullptr;
+  row_op(o, red);
 }
 
-// ---------------------------------------------------------------------------------------------- fake quant
-template <int PER>
-__global__ void __launch_bounds__(64) fake_quant_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
-                                                        int D, int group, int mode) {
-  const long r = blockIdx.x;
-  const int lane = threadIdx.x;
-  constexpr int per = PER;
-  float v[PER];
-  load_row<PER>(v, x + r * D, lane, per, D);
-  fake_quant_lane<PER>(v, per, group, mode);
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int c = lane * per + i;
-    if (i < per && c < D) y[r * D + c] = f2bf(v[i]);
+// Decode step: block (r, op): op 0 the SWA ring row, 1 the compressed-KV row, 2 the index-key row, 3 the index
+// query preparation.  Compressed / index-key rows go to compress_len - 1 when (pos + 1) % ratio == 0, else to the
+// table's spare last row (dsv41/decode.py:150-164, :176-181, :270-282).
+struct DecAppArgs {
+  const uint16_t* kv_raw;
+  const uint16_t* kv_norm;
+  uint16_t* ring;
+  long ring_sstride;
+  int W, Dw;
+  const uint16_t* latent;
+  uint16_t* ckv;
+  long ckv_sstride;
+  int cap;
+  const uint16_t* k_raw;
+  const uint16_t* k_norm;
+  uint16_t* kbf;
+  long kbf_sstride;
+  uint8_t* k8;
+  long k8_sstride;
+  float* ks;
+  long ks_sstride;
+  int kcap, Dk;
+  const long* pos;
+  const long* seq;
+  int ratio, rd;
+  const float* cos_t;
+  const float* sin_t;
+  float eps;
+  const uint16_t* q_idx;  // [B, HI, 128] or null
+  const uint16_t* w_idx;  // [B, HI] bf16
+  int HI;
+  uint8_t* q8;  // [B, 64, 128]
+  float* wf;    // [B, 64]
+};
+
+__global__ void __launch_bounds__(kRowThreads) decode_appends_kernel(const DecAppArgs a) {
+  __shared__ float red[4];
+  const int r = blockIdx.x, op = blockIdx.y;
+  const long p = a.pos[r];
+  const long s = a.seq[r];
+  if (op == 3) {
+    if (a.q_idx)
+      qprep_op(a.q_idx + (long)r * a.HI * 128, a.w_idx + (long)r * a.HI, nullptr, a.HI, a.q8 + (long)r * 64 * 128,
+               a.wf + (long)r * 64);
+    return;
   }
+  const bool closes = ((p + 1) % a.ratio) == 0;
+  RowOp o{};
+  o.cos_t = a.cos_t;
+  o.sin_t = a.sin_t;
+  o.rd = a.rd;
+  o.eps = a.eps;
+  if (op == 0) {
+    o.x = a.kv_raw + (long)r * a.Dw;
+    o.D = a.Dw;
+    o.norm_w = a.kv_norm;
+    o.pos = p < 0 ? 0 : p;
+    o.qmode = 0;
+    o.group = 32;
+    o.out = a.ring + s * a.ring_sstride + (o.pos % a.W) * (long)a.Dw;
+  } else if (op == 1) {
+    if (!a.latent || !a.ckv) return;
+    const long row = closes ? (p + 1) / a.ratio - 1 : a.cap - 1;
+    o.x = a.latent + (long)r * a.Dw;
+    o.D = a.Dw;
+    o.pos = p + 1 - a.ratio;
+    o.qmode = 2;
+    o.group = 16;
+    o.out = a.ckv + s * a.ckv_sstride + row * (long)a.Dw;
+  } else {
+    if (!a.k_raw || (!a.kbf && !a.k8)) return;
+    const long row = closes ? (p + 1) / a.ratio - 1 : a.kcap - 1;
+    o.x = a.k_raw + (long)r * a.Dk;
+    o.D = a.Dk;
+    o.norm_w = a.k_norm;
+    o.pos = p + 1 - a.ratio;
+    o.qmode = 1;
+    o.group = 32;
+    o.out = a.kbf ? a.kbf + s * a.kbf_sstride + row * (long)a.Dk : nullptr;
+    o.k8 = a.k8 ? a.k8 + s * a.k8_sstride + row * (long)a.Dk : nullptr;
+    o.ks = a.k8 ? a.ks + s * a.ks_sstride + row : nullptr;
+  }
+  row_op(o, red);
 }
 
-// ---------------------------------------------------------------------------------------------- rope
+__global__ void __launch_bounds__(kRowThreads) qprep_kernel(const uint16_t* q, const float* w, int HI, uint8_t* q8,
+                                                            float* wf) {
+  const int r = blockIdx.x;
+  qprep_op(q + (long)r * HI * 128, nullptr, w + (long)r * HI, HI, q8 + (long)r * 64 * 128, wf + (long)r * 64);
+}
+
+__global__ void __launch_bounds__(kRowThreads) fake_quant_kernel(const uint16_t* x, uint16_t* y, int D, int group,
+                                                                 int mode) {
+  __shared__ float red[4];
+  RowOp o{};
+  o.x = x + (long)blockIdx.x * D;
+  o.D = D;
+  o.qmode = mode;
+  o.group = group;
+  o.out = y + (long)blockIdx.x * D;
+  row_op(o, red);
+}
+
+__global__ void __launch_bounds__(kRowThreads) rmsnorm_kernel(const uint16_t* x, const uint16_t* w, uint16_t* y, int D,
+                                                              float eps) {
+  __shared__ float red[4];
+  RowOp o{};
+  o.x = x + (long)blockIdx.x * D;
+  o.D = D;
+  o.norm_w = w;
+  o.eps = eps;
+  o.qmode = -1;
+  o.out = y + (long)blockIdx.x * D;
+  row_op(o, red);
+}
+
 // Row r of x ([n_rows, D], rows ordered (b, s, h)): position = base(b) + ((r / H) % S) * pos_stride, with
 // base(b) = pos[b] + add (device positions) or pos0 (host position).
 __global__ void __launch_bounds__(64) rope_kernel(uint16_t* __restrict__ x, const float* __restrict__ cos_t,
@@ -246,29 +398,8 @@ __global__ void __launch_bounds__(64) rope_kernel(uint16_t* __restrict__ x, cons
   base[2 * j + 1] = f2bf(xr * s + xi * c);
 }
 
-template <int PER>
-__global__ void __launch_bounds__(64) rmsnorm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                     uint16_t* __restrict__ y, int D, float eps) {
-  const long r = blockIdx.x;
-  const int lane = threadIdx.x;
-  constexpr int per = PER;
-  float v[PER];
-  load_row<PER>(v, x + r * D, lane, per, D);
-  rmsnorm_lane<PER>(v, lane, per, D, w, eps);
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int c = lane * per + i;
-    if (i < per && c < D) y[r * D + c] = f2bf(v[i]);
-  }
-}
-
-// Columns per lane: the smallest of 2/4/8/16 that covers the row with 64 lanes and divides D, so rope pairs and
-// quantisation groups never straddle a lane boundary in an unaligned way.
-int pick_per(int D) {
-  const int c[4] = {2, 4, 8, 16};
-  for (int i = 0; i < 4; ++i)
-    if (D % c[i] == 0 && D <= 64 * c[i]) return c[i];
-  return 0;
+bool row_ok(int D, int group) {
+  return D > 0 && D <= kRowThreads * kMaxIters && (group <= 0 || D % group == 0) && D % 2 == 0;
 }
 
 }  // namespace
@@ -280,18 +411,11 @@ int dsv41_kv_write(const void* x, long x_rstride, const void* w, const float* co
                    long cache_sstride, int W, void* tmp, int n_rows, int D, int rd, float eps, int commit_from,
                    void* stream) {
   if (n_rows <= 0) return 0;
-  const int per = pick_per(D);
-  if (per == 0 || rd % 2 != 0 || rd > D || W <= 0) return (int)hipErrorInvalidValue;
-  hipStream_t st = (hipStream_t)stream;
-#define KVW(P)                                                                                                   \
-  kv_write_kernel<P><<<n_rows, 64, 0, st>>>((const uint16_t*)x, x_rstride, (const uint16_t*)w, cos_t, sin_t, pos, \
-                                             seq, pos0, pos_stride, rows_per_seq, (uint16_t*)cache, cache_sstride, W, \
-                                             (uint16_t*)tmp, D, rd, eps, commit_from)
-  if (per <= 2) KVW(2);
-  else if (per <= 4) KVW(4);
-  else if (per <= 8) KVW(8);
-  else KVW(16);
-#undef KVW
+  if (!row_ok(D, 32) || rd % 2 != 0 || rd > D || W <= 0) return (int)hipErrorInvalidValue;
+  KvWriteArgs a{(const uint16_t*)x, x_rstride, (const uint16_t*)w, cos_t, sin_t, pos, seq, pos0, pos_stride,
+                rows_per_seq > 0 ? rows_per_seq : 1, (uint16_t*)cache, cache_sstride, W, (uint16_t*)tmp, D, rd, eps,
+                commit_from};
+  kv_write_kernel<<<n_rows, kRowThreads, 0, (hipStream_t)stream>>>(a);
   DSV41_CHECK_LAUNCH();
   return 0;
 }
@@ -302,35 +426,48 @@ int dsv41_append_rows(const void* x, long x_rstride, const void* norm_w, float e
                       int qmode, int group, void* k8, long k8_sstride, float* ks, long ks_sstride, int n_rows, int D,
                       void* stream) {
   if (n_rows <= 0) return 0;
-  const int per = pick_per(D);
-  if (per == 0 || rd % 2 != 0 || rd > D) return (int)hipErrorInvalidValue;
-  if (qmode >= 0 && (group != 16 && group != 32)) return (int)hipErrorInvalidValue;
-  if (rows_per_seq <= 0) rows_per_seq = 1;
-  hipStream_t st = (hipStream_t)stream;
-#define APP(P)                                                                                                      \
-  append_rows_kernel<P><<<n_rows, 64, 0, st>>>((const uint16_t*)x, x_rstride, (const uint16_t*)norm_w, eps, cos_t, \
-                                                sin_t, rd, pos, pos0, pos_stride, pos_add, seq, rows_per_seq, row,    \
-                                                row0, (uint16_t*)cache, cache_sstride, qmode, group, (uint8_t*)k8,    \
-                                                k8_sstride, ks, ks_sstride, D)
-  if (per <= 2) APP(2);
-  else if (per <= 4) APP(4);
-  else if (per <= 8) APP(8);
-  else APP(16);
-#undef APP
+  if (qmode >= 0 && group != 16 && group != 32) return (int)hipErrorInvalidValue;
+  if (!row_ok(D, qmode >= 0 ? group : 0) || rd % 2 != 0 || rd > D) return (int)hipErrorInvalidValue;
+  AppendArgs a{(const uint16_t*)x, x_rstride, (const uint16_t*)norm_w, eps, cos_t, sin_t, rd, pos, pos0, pos_stride,
+               pos_add, seq, rows_per_seq > 0 ? rows_per_seq : 1, row, row0, (uint16_t*)cache, cache_sstride, qmode,
+               group, (uint8_t*)k8, k8_sstride, ks, ks_sstride, D};
+  append_rows_kernel<<<n_rows, kRowThreads, 0, (hipStream_t)stream>>>(a);
+  DSV41_CHECK_LAUNCH();
+  return 0;
+}
+
+int dsv41_decode_appends(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
+                         const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
+                         const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
+                         long ks_sstride, int kcap, int Dk, const long* pos, const long* seq, int ratio,
+                         const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
+                         const void* w_idx, int HI, void* q8, float* wf, int B, void* stream) {
+  if (B <= 0) return 0;
+  if (!row_ok(Dw, 32) || !row_ok(Dk, 32) || ratio <= 0 || rd % 2 != 0 || rd > Dw || rd > Dk || W <= 0 ||
+      cap <= 0 || kcap <= 0 || (q_idx && (!w_idx || !q8 || !wf || HI <= 0 || HI > 64)))
+    return (int)hipErrorInvalidValue;
+  DecAppArgs a{(const uint16_t*)kv_raw, (const uint16_t*)kv_norm, (uint16_t*)ring, ring_sstride, W, Dw,
+               (const uint16_t*)latent, (uint16_t*)ckv, ckv_sstride, cap, (const uint16_t*)k_raw,
+               (const uint16_t*)k_norm, (uint16_t*)kbf, kbf_sstride, (uint8_t*)k8, k8_sstride, ks, ks_sstride, kcap,
+               Dk, pos, seq, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx, HI,
+               (uint8_t*)q8, wf};
+  decode_appends_kernel<<<dim3(B, q_idx ? 4 : 3), kRowThreads, 0, (hipStream_t)stream>>>(a);
+  DSV41_CHECK_LAUNCH();
+  return 0;
+}
+
+int dsv41_index_qprep(const void* q, const float* w, int R, int HI, void* q8, float* wf, void* stream) {
+  if (R <= 0) return 0;
+  if (HI <= 0 || HI > 64) return (int)hipErrorInvalidValue;
+  qprep_kernel<<<R, kRowThreads, 0, (hipStream_t)stream>>>((const uint16_t*)q, w, HI, (uint8_t*)q8, wf);
   DSV41_CHECK_LAUNCH();
   return 0;
 }
 
 int dsv41_fake_quant(const void* x, void* y, long n_rows, int D, int group, int mode, void* stream) {
   if (n_rows <= 0) return 0;
-  const int per = pick_per(D);
-  if (per == 0 || (group != 16 && group != 32) || mode < 0 || mode > 2 || D % group != 0)
-    return (int)hipErrorInvalidValue;
-  hipStream_t st = (hipStream_t)stream;
-  if (per <= 2) fake_quant_kernel<2><<<n_rows, 64, 0, st>>>((const uint16_t*)x, (uint16_t*)y, D, group, mode);
-  else if (per <= 4) fake_quant_kernel<4><<<n_rows, 64, 0, st>>>((const uint16_t*)x, (uint16_t*)y, D, group, mode);
-  else if (per <= 8) fake_quant_kernel<8><<<n_rows, 64, 0, st>>>((const uint16_t*)x, (uint16_t*)y, D, group, mode);
-  else fake_quant_kernel<16><<<n_rows, 64, 0, st>>>((const uint16_t*)x, (uint16_t*)y, D, group, mode);
+  if ((group != 16 && group != 32) || mode < 0 || mode > 2 || !row_ok(D, group)) return (int)hipErrorInvalidValue;
+  fake_quant_kernel<<<n_rows, kRowThreads, 0, (hipStream_t)stream>>>((const uint16_t*)x, (uint16_t*)y, D, group, mode);
   DSV41_CHECK_LAUNCH();
   return 0;
 }
@@ -347,13 +484,9 @@ int dsv41_rope(void* x, const float* cos_t, const float* sin_t, const long* pos,
 
 int dsv41_rmsnorm(const void* x, const void* w, void* y, long n_rows, int D, float eps, void* stream) {
   if (n_rows <= 0) return 0;
-  const int per = pick_per(D);
-  if (per == 0) return (int)hipErrorInvalidValue;
-  hipStream_t st = (hipStream_t)stream;
-  if (per <= 2) rmsnorm_kernel<2><<<n_rows, 64, 0, st>>>((const uint16_t*)x, (const uint16_t*)w, (uint16_t*)y, D, eps);
-  else if (per <= 4) rmsnorm_kernel<4><<<n_rows, 64, 0, st>>>((const uint16_t*)x, (const uint16_t*)w, (uint16_t*)y, D, eps);
-  else if (per <= 8) rmsnorm_kernel<8><<<n_rows, 64, 0, st>>>((const uint16_t*)x, (const uint16_t*)w, (uint16_t*)y, D, eps);
-  else rmsnorm_kernel<16><<<n_rows, 64, 0, st>>>((const uint16_t*)x, (const uint16_t*)w, (uint16_t*)y, D, eps);
+  if (!row_ok(D, 0)) return (int)hipErrorInvalidValue;
+  rmsnorm_kernel<<<n_rows, kRowThreads, 0, (hipStream_t)stream>>>((const uint16_t*)x, (const uint16_t*)w, (uint16_t*)y,
+                                                                  D, eps);
   DSV41_CHECK_LAUNCH();
   return 0;
 }

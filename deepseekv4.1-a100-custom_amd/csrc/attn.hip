@@ -106,7 +106,9 @@ __global__ void __launch_bounds__(256) attn_split_kernel(const AttnArgs a) {
       const uint16_t* p = nullptr;
       if (j < j1) {
         if (a.mode == 1 && j < W) {
-          const long held = pmax - (((pmax - j) % W + W) % W);
+          int m = (int)(pmax - j) % W;  // positions fit in 31 bits
+          m = m < 0 ? m + W : m;
+          const long held = pmax - m;
           if (held >= 0 && held <= plim && pos - held < W) p = base1 + (long)j * DQK;
         } else {
           const int ix = irow[a.mode == 1 ? j - W : j];
@@ -259,8 +261,321 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const AttnArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------ decode kernel
+// Few query rows (decode): the key list of a row is split across many workgroups, so each workgroup owns only 16
+// heads (its partial output is 16 x DV) and the 4 waves of a workgroup split every 64-key tile 16 rows each.  Each
+// wave keeps its own online-softmax state; the 4 states are merged through LDS at the end.  Partials are stored
+// normalised (acc / l) in bf16 next to fp32 (m, l), which halves the partial traffic at an error far below bf16
+// output rounding.
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+
+DSV41_DEV f32x4_t mfma_bf16_16x16x16(uint2 a, uint2 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b), c,
+                                                   0, 0, 0);
+}
+
+// Zero row used as the gather source of invalid key positions (p = 0 then multiplies exact zeros, as the
+// reference's masked loads do).
+__device__ __align__(16) uint16_t g_zero_row[1024];
+
+template <int DQK, int DV>
+__global__ void __launch_bounds__(256) attn_decode_kernel(const AttnArgs a) {
+  constexpr int KS = DQK / 32;
+  constexpr int CT = DV / 16;
+  constexpr int U = DQK / 8;  // 16-byte chunks per row; LDS tile = [64 rows][U chunks], chunk c of row j stored at
+                              // j*U + (c ^ (j & 7)) (XOR swizzle against bank conflicts of the column reads)
+  static_assert(U % 8 == 0, "row width must be a multiple of 64 elements");
+  constexpr int TILE = 64;
+  constexpr int TILE_ELEMS = TILE * DQK;
+  constexpr int KT_ELEMS = 2 * TILE_ELEMS > 4 * 16 * DV * 2 ? 2 * TILE_ELEMS : 4 * 16 * DV * 2;
+  __shared__ __align__(16) uint16_t ktile[KT_ELEMS];  // two tile buffers; the merge buffer aliases them
+  __shared__ const uint16_t* rptr[3][TILE];            // resolved row pointers of tiles i, i+1, i+2 (null: invalid)
+  __shared__ float wm[4][16], wl[4][16];
+
+  const int sp = blockIdx.x, hg = blockIdx.y, r = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int h0 = hg * 16;
+  const int H = a.H;
+
+  uint4 qf[KS];
+  {
+    const int h = h0 + l16 < H ? h0 + l16 : H - 1;  // rows of missing heads are never written
+    const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)h * DQK;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qrow + ks * 32 + g * 8);
+  }
+  long slot, pos = 0, pmax = 0, plim = 0;
+  const int W = a.n1;
+  if (a.mode == 1) {
+    slot = a.seq[r];
+    pos = a.pos[r];
+    pmax = a.pmax[r];
+    plim = a.plim ? a.plim[r] : pos;
+  } else {
+    slot = r / a.rows_per_slot;
+  }
+  const uint16_t* base1 = a.kv1 + slot * a.kv1_sstride;
+  const uint16_t* base2 = a.kv2 ? a.kv2 + slot * a.kv2_sstride : nullptr;
+  const int* irow = a.t > 0 ? a.idx + (long)r * a.idx_rstride : nullptr;
+
+  const int j0 = sp * a.chunk;
+  const int j1 = min(a.L, j0 + a.chunk);
+  const int ntiles = (j1 - j0 + TILE - 1) / TILE;
+
+  auto resolve = [&](int ti) {  // threads 0..63: row pointer of key position j0 + ti*TILE + tid
+    if (tid < TILE) {
+      const int j = j0 + ti * TILE + tid;
+      const uint16_t* p = nullptr;
+      if (j < j1) {
+        if (a.mode == 1 && j < W) {
+          int m = (int)(pmax - j) % W;  // positions fit in 31 bits
+          m = m < 0 ? m + W : m;
+          const long held = pmax - m;
+          if (held >= 0 && held <= plim && pos - held < W) p = base1 + (long)j * DQK;
+        } else {
+          const int ix = irow[a.mode == 1 ? j - W : j];
+          if (a.mode == 1) {
+            if (ix >= 0 && ix < a.n2) p = base2 + (long)ix * DQK;
+          } else if (ix >= 0 && ix < a.n1 + a.n2) {
+            p = ix < a.n1 ? base1 + (long)ix * DQK : base2 + (long)(ix - a.n1) * DQK;
+          }
+        }
+      }
+      rptr[ti % 3][tid] = p;
+    }
+  };
+  // every thread issues U*TILE/256 direct-to-LDS 16-byte loads per tile; no VGPRs hold the data
+  auto issue = [&](int ti) {
+    uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
+    const uint16_t* const* rp = rptr[ti % 3];
+#pragma unroll 2
+    for (int rd = 0; rd < TILE * U / 256; ++rd) {  // fire-and-forget: a rolled loop keeps every load in flight
+      const int q = rd * 256 + wave * 64 + lane;  // LDS chunk position
+      const int j = q / U, cs = q - j * U;
+      const int c = cs ^ (j & 7);
+      const uint16_t* p = rp[j];
+      const uint16_t* src = p ? p + c * 8 : g_zero_row;
+      __builtin_amdgcn_global_load_lds((const void*)src, (void*)(buf + (rd * 256 + wave * 64) * 8), 16, 0, 0);
+    }
+  };
+
+  float m_run = -1e30f, l_run = 0.0f;
+  f32x4_t o[CT];
+#pragma unroll
+  for (int c = 0; c < CT; ++c) o[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll 1
+  for (int ti = 0; ti < 2 && ti < ntiles; ++ti) resolve(ti);
+  __syncthreads();
+  issue(0);
+  for (int ti = 0; ti < ntiles; ++ti) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (ti + 1 < ntiles) issue(ti + 1);
+    const uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
+    const uint16_t* const* rp = rptr[ti % 3];
+    const int rb = wave * 16;  // this wave's 16 key rows of the tile
+    f32x4_t s = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    {
+      const int j = rb + l16;
+      const uint16_t* krow = buf + j * DQK;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        s = mfma_bf16_16x16x32(*(const uint4*)(krow + (((ks * 4 + g) ^ (j & 7)) * 8)), qf[ks], s);
+    }
+    float p[4];
+    float tmax = -1e30f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = rp[rb + 4 * g + i] ? s[i] * a.scale : -1e30f;
+      p[i] = x;
+      tmax = fmaxf(tmax, x);
+    }
+    tmax = fmaxf(tmax, wave_shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, wave_shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = exp2f((m_run - m_new) * kLog2e);
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = rp[rb + 4 * g + i] ? exp2f((p[i] - m_new) * kLog2e) : 0.0f;
+      psum += p[i];
+    }
+    psum += wave_shfl_xor(psum, 16);
+    psum += wave_shfl_xor(psum, 32);
+    l_run = alpha * l_run + psum;
+    m_run = m_new;
+    float al[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i, 64);
+    const uint2 pa = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
+    const int jv = rb + 4 * g;  // rows jv..jv+3; jv % 4 == 0 so (jv + i) & 7 = (jv & 7) + i
+    const uint16_t* vr = buf + jv * DQK + (l16 & 7);
+    const int sw = jv & 7;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[ct][i] *= al[i];
+      const int cch = ct * 2 + (l16 >> 3);  // chunk of column ct*16 + l16
+      const uint16_t v0 = vr[0 * DQK + ((cch ^ (sw + 0)) * 8)];
+      const uint16_t v1 = vr[1 * DQK + ((cch ^ (sw + 1)) * 8)];
+      const uint16_t v2 = vr[2 * DQK + ((cch ^ (sw + 2)) * 8)];
+      const uint16_t v3 = vr[3 * DQK + ((cch ^ (sw + 3)) * 8)];
+      const uint2 vb = make_uint2((uint32_t)v0 | ((uint32_t)v1 << 16), (uint32_t)v2 | ((uint32_t)v3 << 16));
+      o[ct] = mfma_bf16_16x16x16(pa, vb, o[ct]);
+    }
+    if (ti + 2 < ntiles) resolve(ti + 2);
+  }
+  __syncthreads();
+
+  // ---- merge the 4 waves' states (per head): M = max m_w, factor_w = exp(m_w - M), L = sum factor_w * l_w.
+  // Every wave parks its scaled accumulator in LDS ([wave][16 heads][DV] fp32, aliasing the tile buffers), then the
+  // block sums the 4 copies with a rolled loop over column pairs.
+  if (g == 0) {
+    wm[wave][l16] = m_run;
+    wl[wave][l16] = l_run;
+  }
+  __syncthreads();
+  {
+    float fac[4];  // this wave's factor for the heads 4g + i its accumulators hold
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hh = 4 * g + i;
+      const float M = fmaxf(fmaxf(wm[0][hh], wm[1][hh]), fmaxf(wm[2][hh], wm[3][hh]));
+      fac[i] = exp2f((wm[wave][hh] - M) * kLog2e);
+    }
+    float* xw = (float*)ktile + wave * 16 * DV;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xw[(4 * g + i) * DV + ct * 16 + l16] = o[ct][i] * fac[i];
+  }
+  __syncthreads();
+  const float* xb = (const float*)ktile;
+  const bool final_out = a.nsplit == 1;
+  const long pr = pos < 0 ? 0 : pos;
+#pragma unroll 2
+  for (int e = tid; e < 16 * DV / 2; e += 256) {  // column pairs (2c, 2c + 1) of head hh
+    const int hh = e / (DV / 2), c = 2 * (e - hh * (DV / 2));
+    const int hout = h0 + hh;
+    if (hout >= H) continue;
+    const float M = fmaxf(fmaxf(wm[0][hh], wm[1][hh]), fmaxf(wm[2][hh], wm[3][hh]));
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) L += wl[w][hh] * exp2f((wm[w][hh] - M) * kLog2e);
+    float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float2 x = *(const float2*)(xb + (w * 16 + hh) * DV + c);
+      v0 += x.x;
+      v1 += x.y;
+    }
+    if (final_out) {
+      const float inv = 1.0f / (L + exp2f((a.sink[hout] - M) * kLog2e));
+      float re = round_bf16(v0 * inv), im = round_bf16(v1 * inv);
+      if (a.rd > 0 && c >= DV - a.rd) {
+        const int jj = (c - (DV - a.rd)) >> 1;
+        const float cs = a.cos_t[pr * (a.rd / 2) + jj];
+        const float sn = -a.sin_t[pr * (a.rd / 2) + jj];
+        const float yr = re * cs - im * sn, yi = re * sn + im * cs;
+        re = yr;
+        im = yi;
+      }
+      *(uint32_t*)(a.out + (long)r * a.out_rstride + (long)hout * DV + c) = pack_bf16x2(re, im);
+    } else {
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      const long pi = ((long)r * H + hout) * a.nsplit + sp;
+      *(uint32_t*)((uint16_t*)a.pacc + pi * DV + c) = pack_bf16x2(v0 * inv, v1 * inv);
+      if (c == 0) {
+        a.pm[pi] = M;
+        a.pl[pi] = L;
+      }
+    }
+  }
+}
+
+// Merge bf16-normalised partials: out = sum_s w_s l_s o_s / (sum_s w_s l_s + exp(sink - M)), w_s = exp(m_s - M).
+// One workgroup per (row, 4 heads); thread -> (head, 8 consecutive columns); all split loads are independent.
+template <int DV>
+__global__ void __launch_bounds__(256) attn_decode_combine_kernel(const AttnArgs a) {
+  constexpr int MAXS = 32;  // splits held in registers; more are merged in further rounds
+  constexpr int B = 8;      // partial rows loaded per batch
+  const int r = blockIdx.y;
+  const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int H = a.H, ns = a.nsplit;
+  if (h >= H) return;
+  const long base = ((long)r * H + h) * ns;
+  float mx = -1e30f;
+  for (int s0 = 0; s0 < ns; s0 += MAXS) {
+    float mv[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) mv[s] = s0 + s < ns ? a.pm[base + s0 + s] : -1e30f;
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) mx = fmaxf(mx, mv[s]);
+  }
+  const long pr = (a.mode == 1 && a.pos) ? (a.pos[r] < 0 ? 0 : a.pos[r]) : 0;
+  const uint16_t* pb = (const uint16_t*)a.pacc;
+  const float sink_term = exp2f((a.sink[h] - mx) * kLog2e);
+  for (int c = (threadIdx.x & 63) * 8; c < DV; c += 512) {
+    float num[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float den = sink_term;
+    for (int s0 = 0; s0 < ns; s0 += B) {
+      uint4 v[B];
+      float wg[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int s = s0 + u < ns ? s0 + u : ns - 1;
+        v[u] = *(const uint4*)(pb + (base + s) * DV + c);
+        wg[u] = s0 + u < ns ? a.pl[base + s] * exp2f((a.pm[base + s] - mx) * kLog2e) : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        den += wg[u];
+        const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          num[2 * e] += wg[u] * __uint_as_float(vv[e] << 16);
+          num[2 * e + 1] += wg[u] * __uint_as_float(vv[e] & 0xffff0000u);
+        }
+      }
+    }
+    const float inv = 1.0f / den;
+    uint32_t pk[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float re = round_bf16(num[e] * inv), im = round_bf16(num[e + 1] * inv);
+      const int cc = c + e;
+      if (a.rd > 0 && cc >= DV - a.rd) {
+        const int jj = (cc - (DV - a.rd)) >> 1;
+        const float cs = a.cos_t[pr * (a.rd / 2) + jj];
+        const float sn = -a.sin_t[pr * (a.rd / 2) + jj];
+        const float yr = re * cs - im * sn, yi = re * sn + im * cs;
+        re = yr;
+        im = yi;
+      }
+      pk[e / 2] = pack_bf16x2(re, im);
+    }
+    *(uint4*)(a.out + (long)r * a.out_rstride + (long)h * DV + c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  }
+}
+
+// Kernel choice: few (row, 64-head) pairs -> decode kernel (16-head workgroups, key splits, bf16 partials);
+// otherwise the 64-head kernel with one split per row when there are enough rows to fill the chip.
+bool use_decode_kernel(int R, int H) { return (long)R * ((H + 63) / 64) < 128; }
+
 template <int DQK, int DV>
 int launch_attn(AttnArgs& a, hipStream_t st) {
+  if (use_decode_kernel(a.R, a.H)) {
+    dim3 grid(a.nsplit, (a.H + 15) / 16, a.R);
+    attn_decode_kernel<DQK, DV><<<grid, 256, 0, st>>>(a);
+    DSV41_CHECK_LAUNCH();
+    if (a.nsplit > 1) {
+      attn_decode_combine_kernel<DV><<<dim3((a.H + 3) / 4, a.R), 256, 0, st>>>(a);
+      DSV41_CHECK_LAUNCH();
+    }
+    return 0;
+  }
   dim3 grid(a.nsplit, (a.H + 63) / 64, a.R);
   attn_split_kernel<DQK, DV><<<grid, 256, 0, st>>>(a);
   DSV41_CHECK_LAUNCH();
@@ -277,26 +592,40 @@ int dispatch(AttnArgs& a, int dqk, int dv, hipStream_t st) {
   if (dqk == 256 && dv == 256) return launch_attn<256, 256>(a, st);
   if (dqk == 128 && dv == 128) return launch_attn<128, 128>(a, st);
   if (dqk == 64 && dv == 64) return launch_attn<64, 64>(a, st);
+  // head widths: 512 (reference), 576/512 (absorbed MLA); 256/128/64 for reduced test geometries
   return (int)hipErrorInvalidValue;
 }
 
-// Split plan: enough workgroups to cover the chip (>= 512) when there are few query rows; chunks of >= 64 keys.
+// Split plan.  Decode kernel: ~256 workgroups over (rows x 16-head groups x splits), >= 2 tiles of 64 keys per
+// split.  64-head kernel: >= 512 workgroups when rows are few, >= 2 tiles of 32 keys per split.
 void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
-  const int hblocks = (H + 63) / 64;
-  const int tiles = (L + 31) / 32;
-  int ns = want;
-  if (ns <= 0) {
-    const long wgs = (long)R * hblocks;
-    ns = wgs >= 512 ? 1 : (int)((512 + wgs - 1) / wgs);
+  const bool dec = use_decode_kernel(R, H);
+  const int tile = dec ? 64 : 32;
+  const int tiles = (L + tile - 1) / tile < 1 ? 1 : (L + tile - 1) / tile;
+  int per;
+  if (want > 0) {
+    per = (tiles + want - 1) / want;
+  } else if (dec) {
+    const long wgs = (long)R * ((H + 15) / 16);
+    const long target = wgs >= 256 ? 1 : (256 + wgs - 1) / wgs;
+    per = (int)((tiles + target - 1) / target);
+    if (per < 2) per = 2;
+  } else {
+    const long wgs = (long)R * ((H + 63) / 64);
+    const long target = wgs >= 512 ? 1 : (512 + wgs - 1) / wgs;
+    per = (int)((tiles + target - 1) / target);
+    if (per < 2 && target > 1) per = 2;
   }
-  const int max_ns = tiles < 1 ? 1 : (tiles + 1) / 2;  // >= 2 tiles per split
-  if (want <= 0 && ns > max_ns) ns = max_ns;
-  if (ns > tiles) ns = tiles < 1 ? 1 : tiles;
-  if (ns < 1) ns = 1;
-  const int per = (tiles + ns - 1) / ns;
-  *chunk = per * 32;
+  if (per < 1) per = 1;
+  if (per > tiles) per = tiles;
+  *chunk = per * tile;
   *nsplit = (tiles + per - 1) / per;
-  if (*nsplit < 1) *nsplit = 1;
+}
+
+long workspace_bytes(int R, int H, int ns, int dv) {
+  if (ns <= 1) return 0;
+  if (use_decode_kernel(R, H)) return (long)R * H * ns * (8 + 2L * dv);
+  return (long)R * H * ns * (2 + dv) * 4;
 }
 
 int finish_plan(AttnArgs& a, int want_nsplit, void* ws, long ws_bytes, int dv) {
@@ -305,7 +634,7 @@ int finish_plan(AttnArgs& a, int want_nsplit, void* ws, long ws_bytes, int dv) {
   a.nsplit = ns;
   a.chunk = chunk;
   if (ns > 1) {
-    const long need = (long)a.R * a.H * ns * (2 + dv) * 4;
+    const long need = workspace_bytes(a.R, a.H, ns, dv);
     if (!ws || ws_bytes < need) return (int)hipErrorInvalidValue;
     float* f = (float*)ws;
     a.pm = f;
@@ -322,7 +651,7 @@ extern "C" {
 long dsv41_attn_workspace_bytes(int R, int H, int L, int dv, int want_nsplit) {
   int ns, chunk;
   plan(R, H, L, want_nsplit, &ns, &chunk);
-  return ns > 1 ? (long)R * H * ns * (2 + dv) * 4 : 0;
+  return workspace_bytes(R, H, ns, dv);
 }
 
 int dsv41_sparse_attn(const void* q, const void* kv, const float* sink, const int* idx, void* out, int b, int s, int h,

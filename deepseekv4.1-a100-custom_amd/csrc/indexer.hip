@@ -8,8 +8,8 @@
 //   dsv41_topk_indices   the k largest scores of each row, ascending index order, -1 padding / masking
 //                        (dsv41/fused3.py:65-75, dsv41/cuda/topk_select.cu); ties resolved lowest index first.
 //
-// Score kernel: 4 waves per workgroup, each wave owns 64 consecutive key positions of one query row (4 MFMA
-// column tiles of 16 keys); the query fragments live in VGPRs.  MFMA output layout: lane l holds key (l & 15) and
+// Score kernel: 4 waves per workgroup, each wave owns 128 consecutive key positions of one query row (8 MFMA
+// column tiles of 16 keys, loads issued before the query preparation); the query fragments live in VGPRs.  MFMA output layout: lane l holds key (l & 15) and
 // heads 4*(l >> 4) + i, so the head reduction is 16 in-lane FMAs plus two cross-lane shuffles.
 // Keys at positions >= cl are never read: the scan is bounded by the valid count, not the allocated capacity.
 #include "common.h"
@@ -17,8 +17,8 @@
 namespace {
 
 struct ScoreArgs {
-  const uint16_t* q;  // [R, HI, 128] bf16
-  long q_rstride;
+  const uint16_t* q;  // bf16 [R, HI, 128] (bf16 keys) or prepared e4m3 [R, 64, 128] bytes (e4m3 keys)
+  long q_rstride;     // elements (bf16) or bytes (e4m3) between rows
   const float* w;  // [R, HI] fp32
   long w_rstride;
   int HI, R;
@@ -36,6 +36,7 @@ struct ScoreArgs {
   int write_masked;  // write -inf for cl <= t < n_pos
   float* out;
   long out_rstride;
+  int* hist;  // optional [R, kHistBins]: counts of score_key(score) >> 20 over t < cl (decode selection)
 };
 
 DSV41_DEV long row_cl(const ScoreArgs& a, int r) {
@@ -43,75 +44,110 @@ DSV41_DEV long row_cl(const ScoreArgs& a, int r) {
   return (a.cl_start + (long)(r % a.rows_per_slot) + 1) / a.cl_ratio;
 }
 
-constexpr int kHT = 4;  // head tiles of 16 (up to 64 indexer heads)
+constexpr int kHT = 4;            // head tiles of 16 (up to 64 indexer heads)
+constexpr int kHistBins = 4096;   // top 12 bits of the order-preserving score key (8 bins per octave)
+constexpr int kKeysPerWave = 128;  // 8 column tiles of 16 keys
+constexpr int kKeysPerWG = 4 * kKeysPerWave;
 
+// One column tile (16 keys) against all head tiles; returns this lane's partial weighted relu sum for key l16.
 template <int KFMT>
+DSV41_DEV float score_tile(const i32x8_t (&qa8)[kHT], const uint4 (&qa16)[kHT][4], const float (&wr)[kHT][4],
+                           int nht, uint4 k0, uint4 k1, const uint4* kb16) {
+  f32x4_t acc[kHT];
+#pragma unroll
+  for (int ht = 0; ht < kHT; ++ht) acc[ht] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if (KFMT == 1) {
+    const i32x8_t kb = i32x8_t{(int)k0.x, (int)k0.y, (int)k0.z, (int)k0.w, (int)k1.x, (int)k1.y, (int)k1.z, (int)k1.w};
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht)
+      if (ht < nht) acc[ht] = mfma_fp8_16x16x128(qa8[ht], kb, acc[ht]);
+  } else {
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht)
+      if (ht < nht)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc[ht] = mfma_bf16_16x16x32(qa16[ht][ks], kb16[ks], acc[ht]);
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int ht = 0; ht < kHT; ++ht)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sum += wr[ht][i] * fmaxf(acc[ht][i], 0.0f);
+  sum += wave_shfl_xor(sum, 16);
+  sum += wave_shfl_xor(sum, 32);
+  return sum;
+}
+
+template <int KFMT, bool HIST>
 __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
+  __shared__ int lhist[HIST ? kHistBins : 1];
   const int r = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (HIST) {
+#pragma unroll 1
+    for (int i = threadIdx.x; i < kHistBins; i += 256) lhist[i] = 0;
+    __syncthreads();
+  }
   const int l16 = lane & 15, g = lane >> 4;
-  const int kt0 = blockIdx.x * 256 + wave * 64;
-  if (kt0 >= a.n_pos) return;
+  const int kt0 = blockIdx.x * kKeysPerWG + wave * kKeysPerWave;
   long cl = row_cl(a, r);
   if (cl > a.n_pos) cl = a.n_pos;
   float* orow = a.out + (long)r * a.out_rstride;
-  if (kt0 >= cl) {
-    if (a.write_masked) {
-      const int t = kt0 + lane;
-      if (t < a.n_pos) orow[t] = -__builtin_inff();
-    }
-    return;
-  }
+  if (kt0 >= cl) {  // nothing to score in this wave (the whole-block barrier below is still reached)
+    if (a.write_masked)
+      for (int t = kt0 + lane; t < kt0 + kKeysPerWave && t < a.n_pos; t += 64) orow[t] = -__builtin_inff();
+    if (!HIST) return;
+  } else {
   const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
   const int nht = (a.HI + 15) / 16;
+  const int lim = (int)cl;
 
-  // ---- query fragments and folded head weights
+  // ---- issue the key loads of the first column tiles before the query preparation
+  constexpr int NT = KFMT == 1 ? 8 : 4;  // column tiles prefetched per round
+  uint4 k0[NT], k1[NT];
+  uint4 kb16[NT][4];
+  float ksc[NT];
+  auto load_round = [&](int base) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int t = base + nt * 16 + l16;
+      const bool tv = t < lim;
+      if (KFMT == 1) {
+        const uint8_t* krow = (const uint8_t*)a.keys + slot * a.k_sstride + (long)t * 128 + g * 32;
+        k0[nt] = tv ? *(const uint4*)krow : make_uint4(0, 0, 0, 0);
+        k1[nt] = tv ? *(const uint4*)(krow + 16) : make_uint4(0, 0, 0, 0);
+        ksc[nt] = tv ? a.kscale[slot * a.ks_sstride + t] : 0.0f;
+      } else {
+        const uint16_t* krow = (const uint16_t*)a.keys + slot * a.k_sstride + (long)t * 128 + g * 8;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) kb16[nt][ks] = tv ? *(const uint4*)(krow + ks * 32) : make_uint4(0, 0, 0, 0);
+        ksc[nt] = 1.0f;
+      }
+    }
+  };
+  load_round(kt0);
+
+  // ---- query fragments and head weights.  e4m3 keys: q is the prepared e4m3 query [64 heads][128 bytes] and w the
+  // folded weights [64] (dsv41_index_qprep); bf16 keys: q is bf16 [HI][128] and w fp32 [HI].
   i32x8_t qa8[kHT];
   uint4 qa16[kHT][4];
-  float wl[kHT];  // weight (x query scale) of head ht*16 + l16
+  float wl[kHT];  // weight of head ht*16 + l16
 #pragma unroll
   for (int ht = 0; ht < kHT; ++ht) {
     const int h = ht * 16 + l16;
     const bool hv = ht < nht && h < a.HI;
-    const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)h * 128;
-    const float wv = hv ? a.w[(long)r * a.w_rstride + h] : 0.0f;
+    const int hc = hv ? h : 0;
     if (KFMT == 1) {
-      float x[32];
-      float amax = 0.0f;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint4 v = hv ? *(const uint4*)(qrow + g * 32 + u * 8) : make_uint4(0, 0, 0, 0);
-        const uint32_t ww[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          x[u * 8 + 2 * e] = __uint_as_float(ww[e] << 16);
-          x[u * 8 + 2 * e + 1] = __uint_as_float(ww[e] & 0xffff0000u);
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(x[e]));
-      amax = fmaxf(amax, wave_shfl_xor(amax, 16));
-      amax = fmaxf(amax, wave_shfl_xor(amax, 32));
-      int ex = ceil_log2_f(fmaxf(amax, 1e-30f) / 448.0f);
-      ex = ex < -126 ? -126 : ex;
-      const float inv = pow2i(-ex);
-      uint32_t pk[8];
-#pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        uint32_t b = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          b |= e4m3_bits(round_e4m3(fminf(fmaxf(x[d * 4 + e] * inv, -448.0f), 448.0f))) << (8 * e);
-        pk[d] = b;
-      }
-      qa8[ht] = i32x8_t{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3], (int)pk[4], (int)pk[5], (int)pk[6], (int)pk[7]};
-      wl[ht] = wv * pow2i(ex);
+      const uint4* qrow = (const uint4*)((const uint8_t*)a.q + (long)r * a.q_rstride + (long)hc * 128 + g * 32);
+      const uint4 u0 = qrow[0], u1 = qrow[1];
+      qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
     } else {
+      const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)hc * 128;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        qa16[ht][ks] = hv ? *(const uint4*)(qrow + ks * 32 + g * 8) : make_uint4(0, 0, 0, 0);
-      wl[ht] = wv;
+      for (int ks = 0; ks < 4; ++ks) qa16[ht][ks] = *(const uint4*)(qrow + ks * 32 + g * 8);
     }
+    wl[ht] = a.w[(long)r * a.w_rstride + hc];
+    if (!hv) wl[ht] = 0.0f;
   }
   float wr[kHT][4];  // weights of the heads this lane's accumulators hold: ht*16 + 4g + i
 #pragma unroll
@@ -119,48 +155,30 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[ht], 4 * g + i, 64);
 
-  const int lim = (int)cl;
+  for (int base = kt0; base < kt0 + kKeysPerWave; base += NT * 16) {
+    if (base != kt0) load_round(base);
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int t = kt0 + nt * 16 + l16;
-    const bool tv = t < lim;
-    f32x4_t acc[kHT];
-#pragma unroll
-    for (int ht = 0; ht < kHT; ++ht) acc[ht] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    float ksc = 1.0f;
-    if (KFMT == 1) {
-      const uint8_t* krow = (const uint8_t*)a.keys + slot * a.k_sstride + (long)t * 128 + g * 32;
-      uint4 k0 = make_uint4(0, 0, 0, 0), k1 = make_uint4(0, 0, 0, 0);
-      if (tv) {
-        k0 = *(const uint4*)krow;
-        k1 = *(const uint4*)(krow + 16);
-        ksc = a.kscale[slot * a.ks_sstride + t];
+    for (int nt = 0; nt < NT; ++nt) {
+      const int t = base + nt * 16 + l16;
+      const float sum = score_tile<KFMT>(qa8, qa16, wr, nht, k0[nt], k1[nt], kb16[nt]);
+      if (g == 0 && t < a.n_pos) {
+        if (t < lim) {
+          orow[t] = sum * ksc[nt];
+          if (HIST) atomicAdd(&lhist[score_key(sum * ksc[nt]) >> 20], 1);
+        } else if (a.write_masked) {
+          orow[t] = -__builtin_inff();
+        }
       }
-      const i32x8_t kb = i32x8_t{(int)k0.x, (int)k0.y, (int)k0.z, (int)k0.w, (int)k1.x, (int)k1.y, (int)k1.z, (int)k1.w};
-#pragma unroll
-      for (int ht = 0; ht < kHT; ++ht)
-        if (ht < nht) acc[ht] = mfma_fp8_16x16x128(qa8[ht], kb, acc[ht]);
-    } else {
-      const uint16_t* krow = (const uint16_t*)a.keys + slot * a.k_sstride + (long)t * 128 + g * 8;
-      uint4 kb[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kb[ks] = tv ? *(const uint4*)(krow + ks * 32) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int ht = 0; ht < kHT; ++ht)
-        if (ht < nht)
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) acc[ht] = mfma_bf16_16x16x32(qa16[ht][ks], kb[ks], acc[ht]);
     }
-    float s = 0.0f;
-#pragma unroll
-    for (int ht = 0; ht < kHT; ++ht)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s += wr[ht][i] * fmaxf(acc[ht][i], 0.0f);
-    s += wave_shfl_xor(s, 16);
-    s += wave_shfl_xor(s, 32);
-    if (g == 0 && t < a.n_pos) {
-      if (tv) orow[t] = s * ksc;
-      else if (a.write_masked) orow[t] = -__builtin_inff();
+  }
+  }  // kt0 < cl
+  if (HIST) {
+    __syncthreads();
+    int* gh = a.hist + (long)r * kHistBins;
+#pragma unroll 1
+    for (int i = threadIdx.x; i < kHistBins; i += 256) {
+      const int v = lhist[i];
+      if (v) atomicAdd(&gh[i], v);
     }
   }
 }
@@ -210,16 +228,19 @@ DSV41_DEV int block_excl_scan(int v, int* tmp, int* total) {
   return r;
 }
 
+// Radix select on d = key - kmin (the row's own key range), 11-bit digits from the top of the range down, so the
+// first histogram already spreads the scores over 2048 bins whatever their magnitude; then an ordered emission in
+// which every wave owns a contiguous chunk and places its selected indices with ballots (ascending order, ties at
+// the threshold taken lowest index first).  Rows with <= kTopkCache valid positions are staged in LDS once.
 __global__ void __launch_bounds__(kTopkThreads) topk_kernel(const TopkArgs a) {
+  constexpr int B = 8;  // independent loads in flight per thread per batch
   __shared__ uint32_t keys[kTopkCache];
   __shared__ int hist[2048];
   __shared__ int scan_tmp[32];
+  __shared__ uint32_t red_min[16], red_max[16];
+  __shared__ int w_gt[16], w_eq[16], w_take[16], w_base[16];
   __shared__ int s_digit, s_rem;
-  if (threadIdx.x == 0) {
-    s_digit = 0;
-    s_rem = 0;
-  }
-  const int r = blockIdx.x, tid = threadIdx.x;
+  const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* row = a.score + (long)r * a.ld;
   int* orow = a.out + (long)r * a.out_rstride;
   long clr = a.cl ? a.cl[r] : (a.cl_start + (long)(r % a.rows_per_seq) + 1) / a.cl_ratio;
@@ -230,22 +251,72 @@ __global__ void __launch_bounds__(kTopkThreads) topk_kernel(const TopkArgs a) {
     return;
   }
   const bool cached = c <= kTopkCache;
-  if (cached)
-    for (int i = tid; i < c; i += kTopkThreads) keys[i] = score_key(row[i]);
+  // key of element i (i < c), from LDS when staged
+  auto key_at = [&](int i) -> uint32_t { return cached ? keys[i] : score_key(row[i]); };
+
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+  for (int i0 = tid; i0 < c; i0 += B * kTopkThreads) {
+    float v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int i = i0 + u * kTopkThreads;
+      v[u] = row[i < c ? i : 0];
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int i = i0 + u * kTopkThreads;
+      if (i < c) {
+        const uint32_t key = score_key(v[u]);
+        if (cached) keys[i] = key;
+        kmin = min(kmin, key);
+        kmax = max(kmax, key);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, m, 64));
+    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, m, 64));
+  }
+  if (lane == 0) {
+    red_min[wave] = kmin;
+    red_max[wave] = kmax;
+  }
+  if (tid == 0) {
+    s_digit = 0;
+    s_rem = k;
+  }
+  __syncthreads();
+  kmin = red_min[0];
+  kmax = red_max[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) {
+    kmin = min(kmin, red_min[w]);
+    kmax = max(kmax, red_max[w]);
+  }
+  const uint32_t range = kmax - kmin;
+  int shift = range ? 32 - __clz((int)range) : 0;
   uint32_t prefix = 0u, pmask = 0u;
   int remaining = k;
-  const int shifts[3] = {21, 10, 0};
-  const int nbits[3] = {11, 11, 10};
-  for (int pass = 0; pass < 3; ++pass) {
-    const int shift = shifts[pass], nb = 1 << nbits[pass];
+  while (shift > 0) {
+    const int bits = shift < 11 ? shift : 11;
+    shift -= bits;
+    const int nb = 1 << bits;
     for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
     __syncthreads();
-    for (int i = tid; i < c; i += kTopkThreads) {
-      const uint32_t key = cached ? keys[i] : score_key(row[i]);
-      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & (nb - 1)], 1);
+    for (int i0 = tid; i0 < c; i0 += B * kTopkThreads) {
+      uint32_t d[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int i = i0 + u * kTopkThreads;
+        d[u] = key_at(i < c ? i : 0) - kmin;
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u)
+        if (i0 + u * kTopkThreads < c && (d[u] & pmask) == prefix) atomicAdd(&hist[(d[u] >> shift) & (nb - 1)], 1);
     }
     __syncthreads();
-    // descending suffix counts: thread t owns bins 2u, 2u+1 with u = 1023 - t (so the scan runs high -> low)
+    // descending suffix counts: thread t owns bins 2u, 2u+1 with u = 1023 - t (the scan runs high -> low)
     const int u = kTopkThreads - 1 - tid;
     const int hlo = 2 * u < nb ? hist[2 * u] : 0, hhi = 2 * u + 1 < nb ? hist[2 * u + 1] : 0;
     int total;
@@ -265,30 +336,67 @@ __global__ void __launch_bounds__(kTopkThreads) topk_kernel(const TopkArgs a) {
     remaining = s_rem;
     __syncthreads();
   }
-  const uint32_t thr = prefix;
-  // ordered emission: thread t owns a contiguous span; two block scans give each thread its output offset
-  const int span = (c + kTopkThreads - 1) / kTopkThreads;
-  const int i0 = min(c, tid * span), i1 = min(c, i0 + span);
+  const uint32_t thr = kmin + prefix;  // the k-th largest key; `remaining` elements equal to it are taken
+  // ---- ordered emission: wave w owns [w*chunk, (w+1)*chunk) of the row, 64 positions per step
+  const int chunk = ((c + 16 * 64 - 1) / (16 * 64)) * 64;
+  const int i0 = min(c, wave * chunk), i1 = min(c, i0 + chunk);
   int gt = 0, eq = 0;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t key = cached ? keys[i] : score_key(row[i]);
-    gt += key > thr;
-    eq += key == thr;
+  for (int b0 = i0; b0 < i1; b0 += 64 * B) {
+    uint32_t kk[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int i = b0 + u * 64 + lane;
+      kk[u] = key_at(i < i1 ? i : i0);
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const bool in = b0 + u * 64 + lane < i1;
+      gt += in && kk[u] > thr;
+      eq += in && kk[u] == thr;
+    }
   }
-  int total;
-  const int eq_before = block_excl_scan(eq, scan_tmp, &total);
-  int take = remaining - eq_before;
-  take = take < 0 ? 0 : (take > eq ? eq : take);
-  int pos = block_excl_scan(gt + take, scan_tmp, &total);
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t key = cached ? keys[i] : score_key(row[i]);
-    if (key > thr) {
-      if (pos < k) orow[pos] = i + a.offset;
-      ++pos;
-    } else if (key == thr && take > 0) {
-      if (pos < k) orow[pos] = i + a.offset;
-      ++pos;
-      --take;
+  gt = __reduce_add_sync(~0ull, gt);
+  eq = __reduce_add_sync(~0ull, eq);
+  if (lane == 0) {
+    w_gt[wave] = gt;
+    w_eq[wave] = eq;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int eq_before = 0, sel_before = 0;
+    for (int w = 0; w < 16; ++w) {
+      int take = remaining - eq_before;
+      take = take < 0 ? 0 : (take > w_eq[w] ? w_eq[w] : take);
+      w_take[w] = take;
+      w_base[w] = sel_before;
+      eq_before += w_eq[w];
+      sel_before += w_gt[w] + take;
+    }
+  }
+  __syncthreads();
+  const int take = w_take[wave];
+  int base = w_base[wave], eq_seen = 0;
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  for (int b0 = i0; b0 < i1; b0 += 64 * B) {
+    uint32_t kk[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int i = b0 + u * 64 + lane;
+      kk[u] = key_at(i < i1 ? i : i0);
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int i = b0 + u * 64 + lane;
+      const bool in = i < i1;
+      const bool is_gt = in && kk[u] > thr;
+      const bool is_eq = in && kk[u] == thr;
+      const unsigned long long beq = __ballot(is_eq);
+      const bool sel = is_gt || (is_eq && eq_seen + __popcll(beq & lt) < take);
+      const unsigned long long bsel = __ballot(sel);
+      const int p = base + __popcll(bsel & lt);
+      if (sel && p < k) orow[p] = i + a.offset;
+      base += __popcll(bsel);
+      eq_seen += __popcll(beq);
     }
   }
 }
@@ -296,9 +404,14 @@ __global__ void __launch_bounds__(kTopkThreads) topk_kernel(const TopkArgs a) {
 int launch_score(ScoreArgs& a, hipStream_t st) {
   if (a.R <= 0 || a.n_pos <= 0) return 0;
   if (a.HI <= 0 || a.HI > 64) return (int)hipErrorInvalidValue;
-  dim3 grid((a.n_pos + 255) / 256, a.R);
-  if (a.kfmt == 1) index_score_kernel<1><<<grid, 256, 0, st>>>(a);
-  else index_score_kernel<0><<<grid, 256, 0, st>>>(a);
+  dim3 grid((a.n_pos + kKeysPerWG - 1) / kKeysPerWG, a.R);
+  if (a.hist) {
+    if (a.kfmt == 1) index_score_kernel<1, true><<<grid, 256, 0, st>>>(a);
+    else index_score_kernel<0, true><<<grid, 256, 0, st>>>(a);
+  } else {
+    if (a.kfmt == 1) index_score_kernel<1, false><<<grid, 256, 0, st>>>(a);
+    else index_score_kernel<0, false><<<grid, 256, 0, st>>>(a);
+  }
   DSV41_CHECK_LAUNCH();
   return 0;
 }
@@ -310,7 +423,7 @@ extern "C" {
 int dsv41_index_score(const void* q, long q_rstride, const float* w, long w_rstride, int R, int HI, int D, int kfmt,
                       const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
                       int rows_per_slot, const long* cl, long cl_start, int cl_ratio, int n_pos, int write_masked,
-                      float* out, long out_rstride, void* stream) {
+                      float* out, long out_rstride, int* hist, void* stream) {
   if (D != 128 || (kfmt == 1 && !kscale) || (!cl && cl_ratio <= 0)) return (int)hipErrorInvalidValue;
   ScoreArgs a{};
   a.q = (const uint16_t*)q;
@@ -333,6 +446,7 @@ int dsv41_index_score(const void* q, long q_rstride, const float* w, long w_rstr
   a.write_masked = write_masked;
   a.out = out;
   a.out_rstride = out_rstride;
+  a.hist = hist;
   return launch_score(a, (hipStream_t)stream);
 }
 

@@ -137,3 +137,33 @@ def append_index_k_decode(cache: torch.Tensor, k_raw: torch.Tensor, norm_w: torc
          ptr(k8) if k8 is not None else None, k8.stride(0) if k8 is not None else 0,
          ptr(k_scale) if k_scale is not None else None, k_scale.stride(0) if k_scale is not None else 0, B, D,
          stream(dev))
+
+
+def decode_appends(kv_raw, kv_norm, ring, latent, ckv, k_raw, k_norm, kbf, k8, k_scale, pos, seq, ratio: int,
+                   cos, sin, rd: int, eps: float, q_idx=None, w_idx=None, q8=None, wf=None) -> None:
+    """Every cache write of one decode step in one launch (dsv41/decode.py:129-164, :270-282): the SWA ring row
+    (kv_write), the compressed-KV row and the index-key row (bf16 table kbf and/or e4m3 table k8 + k_scale), each at
+    compress_len - 1 when the step closes a compression group, else at the table's spare last row.  latent / k_raw
+    may be None (layers that own no compressor / indexer keys).  With q_idx ([B, 1, HI, 128] bf16) and w_idx
+    ([B, HI] bf16) it also writes the prepared e4m3 index queries q8 [B, 64, 128] (uint8) and folded weights
+    wf [B, 64] of the e4m3 score path."""
+    dev = require_gpu(kv_raw, ring, latent, ckv, k_raw, kbf, k8)
+    Dw = ring.shape[-1]
+    x = kv_raw.reshape(-1, Dw).contiguous()
+    B = x.shape[0]
+    assert ring.stride(2) == 1 and ring.stride(1) == Dw
+    lat = latent.reshape(B, -1).contiguous() if latent is not None else None
+    kr = k_raw.reshape(B, -1).contiguous() if k_raw is not None else None
+    tab = k8 if k8 is not None else kbf
+    Dk = tab.shape[-1] if tab is not None else 128
+    kcap = tab.shape[1] if tab is not None else 1
+    call("dsv41_decode_appends", ptr(x), ptr(kv_norm.to(torch.bfloat16).contiguous()), ptr(ring), ring.stride(0),
+         ring.shape[1], Dw, ptr(lat), ptr(ckv), ckv.stride(0) if ckv is not None else 0,
+         ckv.shape[1] if ckv is not None else 1, ptr(kr),
+         ptr(k_norm.to(torch.bfloat16).contiguous()) if k_norm is not None else None, ptr(kbf),
+         kbf.stride(0) if kbf is not None else 0, ptr(k8), k8.stride(0) if k8 is not None else 0, ptr(k_scale),
+         k_scale.stride(0) if k_scale is not None else 0, kcap, Dk, ptr(as_i64(pos.reshape(-1), dev)),
+         ptr(as_i64(seq.reshape(-1), dev)), int(ratio), ptr(cos), ptr(sin), int(rd), float(eps),
+         ptr(q_idx.contiguous()) if q_idx is not None else None,
+         ptr(w_idx.to(torch.bfloat16).contiguous()) if q_idx is not None else None,
+         q_idx.shape[-2] if q_idx is not None else 0, ptr(q8), ptr(wf), B, stream(dev))

@@ -10,8 +10,8 @@ from __future__ import annotations
 import torch
 
 from . import cache as C
-from .fused2 import kv_write, sattn2
-from .fused3 import index_score, topk_indices
+from .fused2 import sattn2
+from .fused3 import DecodeSelector
 
 
 class DecodeLayer:
@@ -25,23 +25,39 @@ class DecodeLayer:
         self.ratio, self.topk, self.rd, self.dv, self.eps = ratio, topk, rd, dv, eps
         self.kbf16 = kbf16
         self.scale = ckv.shape[-1] ** -0.5
+        self._selectors = {}
+        self._qbufs = {}
+        self._prepared = None
 
-    def appends(self, kv_raw, kv_norm, latent, k_raw, k_norm, pos, seq):
-        """Cache writes of this step (dsv41/decode.py:134, :157-164, :270-282)."""
-        kv_write(kv_raw, kv_norm, self.cos, self.sin, pos, self.ring, self.rd, self.eps, seq)
-        cl = torch.div(pos + 1, self.ratio, rounding_mode="floor")
-        should = torch.remainder(pos + 1, self.ratio) == 0
-        row = torch.where(should, cl - 1, torch.full_like(cl, self.ckv.shape[1] - 1))
-        C.append_compressed_decode(self.ckv, latent, pos, seq, row, self.ratio, self.cos, self.sin, self.rd)
-        C.append_index_k_decode(self.kbf16, k_raw, k_norm, self.eps, pos, seq, row, self.ratio, self.cos, self.sin,
-                                self.rd, k8=self.k8, k_scale=self.ks)
-        return cl
+    def _qbuf(self, B, dev):
+        buf = self._qbufs.get(B)
+        if buf is None:
+            buf = self._qbufs[B] = (torch.empty(B, 64, 128, dtype=torch.uint8, device=dev),
+                                    torch.empty(B, 64, dtype=torch.float32, device=dev))
+        return buf
+
+    def appends(self, kv_raw, kv_norm, latent, k_raw, k_norm, pos, seq, q_idx=None, w_idx=None):
+        """Cache writes of this step in one launch (dsv41/decode.py:134, :157-164, :270-282); with q_idx/w_idx the
+        same launch prepares the e4m3 index queries that select() then uses."""
+        q8 = wf = None
+        if q_idx is not None:
+            q8, wf = self._qbuf(q_idx.shape[0], q_idx.device)
+        C.decode_appends(kv_raw, kv_norm, self.ring, latent, self.ckv, k_raw, k_norm, self.kbf16, self.k8, self.ks,
+                         pos, seq, self.ratio, self.cos, self.sin, self.rd, self.eps, q_idx, w_idx, q8, wf)
+        self._prepared = (q8, wf) if q_idx is not None else None
 
     def select(self, q_idx, w_idx, pos, seq, cl=None):
+        """Indexer score over the e4m3 keys + top-k (dsv41/decode.py:284-294), histogram-assisted selection."""
         if cl is None:
             cl = torch.div(pos + 1, self.ratio, rounding_mode="floor")
-        score = index_score(q_idx, self.k8, w_idx, seq, cl, k_scale=self.ks)
-        return topk_indices(score, self.topk, cl)
+        sel = self.selector(q_idx.shape[0], q_idx.device)
+        return sel(q_idx, self.k8, w_idx, seq, cl, k_scale=self.ks, prepared=self._prepared)
+
+    def selector(self, rows: int, device) -> DecodeSelector:
+        sel = self._selectors.get(rows)
+        if sel is None:
+            sel = self._selectors[rows] = DecodeSelector(rows, self.k8.shape[1], self.topk, device)
+        return sel
 
     def attend(self, q, idx, pos, seq, pmax, plim=None):
         return sattn2(q, self.ring, self.ckv, idx, pos, self.sink, self.cos, self.sin, 0 if self.dv < q.shape[-1]

@@ -1,9 +1,43 @@
-"""Drop-ins for dsv41/fused3.py: the decode indexer score and the top-k selection."""
+"""Drop-ins for dsv41/fused3.py: the decode indexer score and the top-k selection, plus the fused decode selector
+(score + histogram-assisted multi-workgroup top-k) used by the graph-decode layer step."""
 from __future__ import annotations
 
 import torch
 
-from ._lib import as_i64, call, ptr, require_gpu, stream
+from ._lib import as_i64, call, lib, ptr, require_gpu, stream
+
+
+def qprep(q: torch.Tensor, weights: torch.Tensor):
+    """e4m3 index queries [B, 64, 128] (bytes) + folded head weights [B, 64] fp32 for the e4m3 score path."""
+    B, _, H, D = q.shape
+    dev = q.device
+    q8 = torch.empty(B, 64, 128, dtype=torch.uint8, device=dev)
+    wf = torch.empty(B, 64, dtype=torch.float32, device=dev)
+    w = weights.reshape(B, H).float().contiguous()
+    call("dsv41_index_qprep", ptr(q.contiguous()), ptr(w), B, H, ptr(q8), ptr(wf), stream(dev))
+    return q8, wf
+
+
+def _score(q, index_k, weights, seq, cl, k_scale, out, write_masked: bool, hist, prepared=None):
+    """prepared = (q8, wf) from qprep / decode_appends for e4m3 keys (computed here when None)."""
+    B, _, H, D = q.shape
+    dev = q.device
+    n_pos = index_k.shape[1]
+    assert index_k.stride(2) == 1 and index_k.stride(1) == D and D == 128 and H <= 64
+    if index_k.dtype == torch.float8_e4m3fn:
+        if k_scale is None:
+            raise RuntimeError("index_score: e4m3 keys need k_scale")
+        ks = k_scale if k_scale.dtype == torch.float32 else k_scale.float()
+        assert ks.stride(-1) == 1
+        q8, wf = prepared if prepared is not None else qprep(q, weights)
+        call("dsv41_index_score", ptr(q8), 64 * 128, ptr(wf), 64, B, H, D, 1, ptr(index_k), index_k.stride(0), ptr(ks),
+             ks.stride(0), ptr(seq), 1, ptr(cl), 0, 1, n_pos, int(write_masked), ptr(out), out.stride(0), ptr(hist),
+             stream(dev))
+    else:
+        qc = q.contiguous()
+        w = weights.reshape(B, H).float().contiguous()
+        call("dsv41_index_score", ptr(qc), H * D, ptr(w), H, B, H, D, 0, ptr(index_k), index_k.stride(0), None, 0,
+             ptr(seq), 1, ptr(cl), 0, 1, n_pos, int(write_masked), ptr(out), out.stride(0), ptr(hist), stream(dev))
 
 
 def index_score(q: torch.Tensor, index_k: torch.Tensor, weights: torch.Tensor, seq: torch.Tensor, cl: torch.Tensor,
@@ -15,23 +49,8 @@ def index_score(q: torch.Tensor, index_k: torch.Tensor, weights: torch.Tensor, s
         raise NotImplementedError("index_score: candidate-block masks are not supported by this path")
     B, _, H, D = q.shape
     dev = require_gpu(q, index_k, weights)
-    n_pos = index_k.shape[1]
-    out = torch.empty(B, n_pos, device=dev, dtype=torch.float32)
-    qc = q.contiguous()
-    w = weights.reshape(B, H).float().contiguous()
-    seq = as_i64(seq.reshape(-1), dev)
-    cl = as_i64(cl.reshape(-1), dev)
-    assert index_k.stride(2) == 1 and index_k.stride(1) == D
-    if index_k.dtype == torch.float8_e4m3fn:
-        if k_scale is None:
-            raise RuntimeError("index_score: e4m3 keys need k_scale")
-        ks = k_scale if k_scale.dtype == torch.float32 else k_scale.float()
-        assert ks.stride(-1) == 1
-        call("dsv41_index_score", ptr(qc), H * D, ptr(w), H, B, H, D, 1, ptr(index_k), index_k.stride(0), ptr(ks),
-             ks.stride(0), ptr(seq), 1, ptr(cl), 0, 1, n_pos, 1, ptr(out), n_pos, stream(dev))
-    else:
-        call("dsv41_index_score", ptr(qc), H * D, ptr(w), H, B, H, D, 0, ptr(index_k), index_k.stride(0), None, 0,
-             ptr(seq), 1, ptr(cl), 0, 1, n_pos, 1, ptr(out), n_pos, stream(dev))
+    out = torch.empty(B, index_k.shape[1], device=dev, dtype=torch.float32)
+    _score(q, index_k, weights, as_i64(seq.reshape(-1), dev), as_i64(cl.reshape(-1), dev), k_scale, out, True, None)
     return out
 
 
@@ -45,3 +64,39 @@ def topk_indices(score: torch.Tensor, k: int, cl: torch.Tensor) -> torch.Tensor:
     out = torch.empty(B, k, device=dev, dtype=torch.int32)
     call("dsv41_topk_indices", ptr(score), score.stride(0), B, n, k, ptr(cl), 0, 1, 1, 0, ptr(out), k, stream(dev))
     return out.view(B, 1, k)
+
+
+class DecodeSelector:
+    """index_score + topk_indices of the graph decode (dsv41/decode.py:289-294) for a fixed (rows, n_pos, k): the
+    score kernel also builds a 4096-bin histogram of the score keys, from which the top-k needs one compaction pass
+    over many workgroups plus one small finalize per row.  Holds the score buffer and the zero-initialised
+    workspace (the finalize leaves the histogram zeroed, so the object is reusable and graph-capturable)."""
+
+    def __init__(self, rows: int, n_pos: int, k: int, device):
+        self.rows, self.n_pos, self.k = rows, n_pos, k
+        nbytes = lib().dsv41_select_workspace_bytes(rows, n_pos)
+        self.ws = torch.zeros(nbytes // 4, dtype=torch.int32, device=device)
+        self.nbytes = nbytes
+        self.score = torch.empty(rows, n_pos, dtype=torch.float32, device=device)
+        self.out = torch.empty(rows, 1, k, dtype=torch.int32, device=device)
+
+    def score_into(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None) -> None:
+        """The score kernel alone (scores + histogram into this object's buffers)."""
+        require_gpu(q, index_k, weights)
+        B = q.shape[0]
+        if B != self.rows or index_k.shape[1] != self.n_pos:
+            raise RuntimeError(f"DecodeSelector built for {self.rows} x {self.n_pos}, got {B} x {index_k.shape[1]}")
+        _score(q, index_k, weights, seq, cl, k_scale, self.score, False, self.ws, prepared)
+
+    def select(self, cl) -> torch.Tensor:
+        """Top-k from the buffered scores + histogram (two launches); leaves the histogram zeroed."""
+        call("dsv41_select_topk", ptr(self.score), self.n_pos, self.rows, self.n_pos, self.k, ptr(cl), 0, ptr(self.ws),
+             self.nbytes, ptr(self.out), self.k, stream(self.score.device))
+        return self.out
+
+    def __call__(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None) -> torch.Tensor:
+        dev = require_gpu(q, index_k, weights)
+        seq = as_i64(seq.reshape(-1), dev)
+        cl = as_i64(cl.reshape(-1), dev)
+        self.score_into(q, index_k, weights, seq, cl, k_scale, prepared)
+        return self.select(cl)

@@ -32,11 +32,14 @@ def index_topk(q: torch.Tensor, weights: torch.Tensor, index_k: torch.Tensor, st
         if k_scale is None:
             raise RuntimeError("index_topk: e4m3 keys need k_scale")
         ks = k_scale.float() if k_scale.dtype != torch.float32 else k_scale
-        call("dsv41_index_score", ptr(qc), H * D, ptr(w), H, b * s, H, D, 1, ptr(index_k), index_k.stride(0), ptr(ks),
-             ks.stride(0), None, s, None, start_pos, ratio, T, 1, ptr(score), T, st)
+        q8 = torch.empty(b * s, 64, 128, dtype=torch.uint8, device=dev)
+        wf = torch.empty(b * s, 64, dtype=torch.float32, device=dev)
+        call("dsv41_index_qprep", ptr(qc), ptr(w), b * s, H, ptr(q8), ptr(wf), st)
+        call("dsv41_index_score", ptr(q8), 64 * 128, ptr(wf), 64, b * s, H, D, 1, ptr(index_k), index_k.stride(0),
+             ptr(ks), ks.stride(0), None, s, None, start_pos, ratio, T, 1, ptr(score), T, None, st)
     else:
         call("dsv41_index_score", ptr(qc), H * D, ptr(w), H, b * s, H, D, 0, ptr(index_k), index_k.stride(0), None, 0,
-             None, s, None, start_pos, ratio, T, 1, ptr(score), T, st)
+             None, s, None, start_pos, ratio, T, 1, ptr(score), T, None, st)
     call("dsv41_topk_indices", ptr(score), T, b * s, T, kk, None, start_pos, ratio, s, int(offset), ptr(out), kk, st)
     if return_score:
         return out, score.view(b, s, T)

@@ -51,14 +51,34 @@ int dsv41_sattn2(const void* q, const void* kv_win, long win_sstride, int win, c
 
 /* fused3.index_score (dsv41/fused3.py:20-62) and the score half of Indexer.__call__ (dsv41/model.py:766-893):
  * out[r, t] = sum_h w[r,h] * relu(q[r,h,:] . key[slot(r), t, :]) for t < cl(r), -inf for cl(r) <= t < n_pos when
- * write_masked.  q [R, HI, 128] bf16, w [R, HI] fp32 (HI <= 64).  kfmt 0: keys bf16 [S, rows, 128] (k_sstride in
- * elements); kfmt 1: keys e4m3 [S, rows, 128] (k_sstride in bytes) times kscale [S, rows] fp32.
+ * write_masked.  kfmt 0: keys bf16 [S, rows, 128] (k_sstride in elements), q bf16 [R, HI, 128] (q_rstride in
+ * elements), w fp32 [R, HI].  kfmt 1: keys e4m3 [S, rows, 128] (k_sstride in bytes) times kscale [S, rows] fp32;
+ * q and w are the prepared e4m3 queries [R, 64, 128] (q_rstride in bytes) and folded weights [R, 64] of
+ * dsv41_index_qprep / dsv41_decode_appends.  HI <= 64.
  * slot(r) = seq[r] (or r / rows_per_slot when seq is null); cl(r) = cl[r] (or (cl_start + r % rows_per_slot + 1) /
- * cl_ratio, the causal compressed length of a prefill chunk, dsv41/model.py:819-830, when cl is null). */
+ * cl_ratio, the causal compressed length of a prefill chunk, dsv41/model.py:819-830, when cl is null).
+ * hist (may be null): [R, 4096] int32 histogram of the top 12 bits of the order-preserving key of every score
+ * written (t < cl), accumulated atomically -- the input of dsv41_select_topk; it must be zero on entry. */
 int dsv41_index_score(const void* q, long q_rstride, const float* w, long w_rstride, int R, int HI, int D, int kfmt,
                       const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
                       int rows_per_slot, const long* cl, long cl_start, int cl_ratio, int n_pos, int write_masked,
-                      float* out, long out_rstride, void* stream);
+                      float* out, long out_rstride, int* hist, void* stream);
+
+/* Index-query preparation for the e4m3 score path (the query side of dsv41/decode.py:284-288 after the reference's
+ * FP4 rounding): per (row, head) a power-of-two scale 2^e = 2^ceil(log2(amax/448)), q8 = e4m3(q / 2^e) and
+ * wf = w * 2^e.  q bf16 [R, HI, 128], w fp32 [R, HI] -> q8 [R, 64, 128] bytes, wf [R, 64] (heads >= HI: weight 0). */
+int dsv41_index_qprep(const void* q, const float* w, int R, int HI, void* q8, float* wf, void* stream);
+
+/* Workspace of dsv41_select_topk for R rows of n positions; its first R*4096 int32 are the histogram that
+ * dsv41_index_score fills.  Allocate it zeroed once: every dsv41_select_topk call leaves the histogram zeroed. */
+long dsv41_select_workspace_bytes(int R, int n);
+
+/* Decode top-k (the topk_indices of dsv41/fused3.py:65-75 after fused3.index_score, dsv41/decode.py:289-294) from
+ * the scores and the histogram built by dsv41_index_score: per row the k largest of score[r, 0..cl[r]), ascending,
+ * + offset, -1 padding when cl[r] < k; ties lowest index first (the same set as dsv41_topk_indices).  Two launches
+ * (per-chunk compaction over many workgroups, then one workgroup per row); n <= 262144, k <= n. */
+int dsv41_select_topk(const float* score, long ld, int R, int n, int k, const long* cl, int offset, void* ws,
+                      long ws_bytes, int* out, long out_rstride, void* stream);
 
 /* fused3.topk_indices + cuda/topk_select.cu (dsv41/fused3.py:65-75, dsv41/cuda/topk_select.cu:94-168), also the
  * selection of Indexer.__call__ (dsv41/model.py:868-893): per row the k largest of score[r, 0..c) with c =
@@ -70,7 +90,7 @@ int dsv41_topk_indices(const float* score, long ld, int R, int n, int k, const l
 
 /* fused2.kv_write (dsv41/fused2.py:276-330) and the ring commit of Attention._window_kv (dsv41/model.py:1057-1298):
  * row r of x -> rmsnorm(w) -> bf16 -> rope(last rd, position p) -> bf16 -> fq8/32 -> cache[s, p % W] (rows r >=
- * commit_from only) and tmp[r] (when tmp != null).  p = pos[r] or pos0 + r * pos_stride; s = seq[r] or
+ * commit_from only) and tmp[r] (when tmp != null).  p = pos[r] or pos0 + (r % rows_per_seq) * pos_stride; s = seq[r] or
  * r / rows_per_seq. */
 int dsv41_kv_write(const void* x, long x_rstride, const void* w, const float* cos_t, const float* sin_t,
                    const long* pos, const long* seq, long pos0, long pos_stride, int rows_per_seq, void* cache,
@@ -79,7 +99,7 @@ int dsv41_kv_write(const void* x, long x_rstride, const void* w, const float* co
 
 /* Compressed-KV append (dsv41/decode.py:157-164, dsv41/model.py:1320-1348, SharedAttn.write_compress_kv :508-541)
  * and index-key append (dsv41/decode.py:270-282, dsv41/model.py:696-732, SharedAttn.write_index_k :543-574):
- * row r of x -> [rmsnorm(norm_w)] -> [rope(last rd) at (pos[r] or pos0 + r*pos_stride) + pos_add] -> fake quant
+ * row r of x -> [rmsnorm(norm_w)] -> [rope(last rd) at (pos[r] or pos0 + (r % rows_per_seq)*pos_stride) + pos_add] -> fake quant
  * (qmode 0 fp8 pow2, 1 fp4 pow2, 2 fp4 e4m3-scale; group 16/32; -1 none) -> bf16 cache[s, row] with s = seq[r] or
  * r / rows_per_seq and row = row[r] or row0 + r % rows_per_seq (row < 0: no write).  When k8 != null also writes
  * the e4m3 encoding with a per-row power-of-two scale: k8[s, row, :] (bytes) and ks[s, row]. */
@@ -88,6 +108,22 @@ int dsv41_append_rows(const void* x, long x_rstride, const void* norm_w, float e
                       const long* seq, int rows_per_seq, const long* row, long row0, void* cache, long cache_sstride,
                       int qmode, int group, void* k8, long k8_sstride, float* ks, long ks_sstride, int n_rows, int D,
                       void* stream);
+
+/* All cache writes of one decode step in one launch (dsv41/decode.py:129-164 kv_write + compressed append,
+ * :270-282 index-key append, :176-181 spare row), plus the index-query preparation: per query row r at position
+ * pos[r] of sequence seq[r]
+ *   ring[seq, pos % W]        <- fq8(rope(rmsnorm(kv_raw[r], kv_norm)))                       (Dw wide)
+ *   ckv[seq, row]             <- fq4/16-e4m3(rope(latent[r], pos + 1 - ratio))                (latent may be null)
+ *   kbf[seq, row], k8/ks      <- fq4/32(rope(rmsnorm(k_raw[r], k_norm), pos + 1 - ratio))     (Dk = 128; k_raw may be
+ *                                                                                               null; kbf or k8 may be null)
+ *   q8[r], wf[r]              <- dsv41_index_qprep(q_idx[r], w_idx[r] (bf16))                  (q_idx may be null)
+ * with row = (pos + 1) / ratio - 1 when (pos + 1) % ratio == 0, else the table's spare last row (cap - 1 / kcap - 1). */
+int dsv41_decode_appends(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
+                         const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
+                         const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
+                         long ks_sstride, int kcap, int Dk, const long* pos, const long* seq, int ratio,
+                         const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
+                         const void* w_idx, int HI, void* q8, float* wf, int B, void* stream);
 
 /* ------------------------------------------------------------------------------------------------ numerics */
 
