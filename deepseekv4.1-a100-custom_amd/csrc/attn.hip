@@ -278,33 +278,41 @@ DSV41_DEV f32x4_t mfma_bf16_16x16x16(uint2 a, uint2 b, f32x4_t c) {
 // reference's masked loads do).
 __device__ __align__(16) uint16_t g_zero_row[1024];
 
+// LDS transpose read (gfx950 ds_read_b64_tr_b16): within each group of 16 lanes, output lane i receives element
+// (i % 4) of the 4-element (8-byte) reads of input lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12.
+DSV41_DEV uint2 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((ext_vector_type(4))) short s4;
+  const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)p);
+  return __builtin_bit_cast(uint2, v);
+}
+
+// Decode attention, 8 waves per workgroup (2 per SIMD): wave w handles key rows 16*(w&3)..+15 of every 64-key tile
+// and output columns [(w>>2)*DV/2, +DV/2) (QK^T and the softmax are computed by both column halves, identically).
+// The softmax keeps a reference maximum per head and rescales the accumulators only when the tile maximum exceeds
+// it by more than kRescale (log2 units): p = 2^(s*log2e - m_ref) <= 2^kRescale stays far from fp32/bf16 range
+// limits, and the final normalisation uses the same reference, so the result is the exact softmax.
 template <int DQK, int DV>
-__global__ void __launch_bounds__(256) attn_decode_kernel(const AttnArgs a) {
+__global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   constexpr int KS = DQK / 32;
-  constexpr int CT = DV / 16;
-  constexpr int U = DQK / 8;  // 16-byte chunks per row; LDS tile = [64 rows][U chunks], chunk c of row j stored at
-                              // j*U + (c ^ (j & 7)) (XOR swizzle against bank conflicts of the column reads)
+  constexpr int CTH = DV / 32;  // 16-column output tiles per wave (half of DV)
+  constexpr int U = DQK / 8;    // 16-byte chunks per row; chunk c of row j stored at j*U + (c ^ (j & 7))
   static_assert(U % 8 == 0, "row width must be a multiple of 64 elements");
   constexpr int TILE = 64;
   constexpr int TILE_ELEMS = TILE * DQK;
+  constexpr float kRescale = 8.0f;
   constexpr int KT_ELEMS = 2 * TILE_ELEMS > 4 * 16 * DV * 2 ? 2 * TILE_ELEMS : 4 * 16 * DV * 2;
   __shared__ __align__(16) uint16_t ktile[KT_ELEMS];  // two tile buffers; the merge buffer aliases them
   __shared__ const uint16_t* rptr[3][TILE];            // resolved row pointers of tiles i, i+1, i+2 (null: invalid)
   __shared__ float wm[4][16], wl[4][16];
 
+  DSV41_TS(10);
   const int sp = blockIdx.x, hg = blockIdx.y, r = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rw = wave & 3, half = wave >> 2;
   const int l16 = lane & 15, g = lane >> 4;
   const int h0 = hg * 16;
   const int H = a.H;
 
-  uint4 qf[KS];
-  {
-    const int h = h0 + l16 < H ? h0 + l16 : H - 1;  // rows of missing heads are never written
-    const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)h * DQK;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qrow + ks * 32 + g * 8);
-  }
   long slot, pos = 0, pmax = 0, plim = 0;
   const int W = a.n1;
   if (a.mode == 1) {
@@ -318,7 +326,6 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const AttnArgs a) {
   const uint16_t* base1 = a.kv1 + slot * a.kv1_sstride;
   const uint16_t* base2 = a.kv2 ? a.kv2 + slot * a.kv2_sstride : nullptr;
   const int* irow = a.t > 0 ? a.idx + (long)r * a.idx_rstride : nullptr;
-
   const int j0 = sp * a.chunk;
   const int j1 = min(a.L, j0 + a.chunk);
   const int ntiles = (j1 - j0 + TILE - 1) / TILE;
@@ -345,37 +352,47 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const AttnArgs a) {
       rptr[ti % 3][tid] = p;
     }
   };
-  // every thread issues U*TILE/256 direct-to-LDS 16-byte loads per tile; no VGPRs hold the data
-  auto issue = [&](int ti) {
+  auto issue = [&](int ti) {  // direct-to-LDS 16-byte loads; no VGPRs hold the data
     uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
     const uint16_t* const* rp = rptr[ti % 3];
 #pragma unroll 2
-    for (int rd = 0; rd < TILE * U / 256; ++rd) {  // fire-and-forget: a rolled loop keeps every load in flight
-      const int q = rd * 256 + wave * 64 + lane;  // LDS chunk position
+    for (int rd = 0; rd < TILE * U / 512; ++rd) {
+      const int q = rd * 512 + wave * 64 + lane;  // LDS chunk position
       const int j = q / U, cs = q - j * U;
       const int c = cs ^ (j & 7);
       const uint16_t* p = rp[j];
       const uint16_t* src = p ? p + c * 8 : g_zero_row;
-      __builtin_amdgcn_global_load_lds((const void*)src, (void*)(buf + (rd * 256 + wave * 64) * 8), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)src, (void*)(buf + (rd * 512 + wave * 64) * 8), 16, 0, 0);
     }
   };
 
-  float m_run = -1e30f, l_run = 0.0f;
-  f32x4_t o[CT];
-#pragma unroll
-  for (int c = 0; c < CT; ++c) o[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
 #pragma unroll 1
   for (int ti = 0; ti < 2 && ti < ntiles; ++ti) resolve(ti);
+  uint4 qf[KS];
+  {
+    const int h = h0 + l16 < H ? h0 + l16 : H - 1;  // rows of missing heads are never written
+    const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)h * DQK;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qrow + ks * 32 + g * 8);
+  }
   __syncthreads();
+  DSV41_TS(11);
   issue(0);
+
+  float m_ref = -1e30f, l_run = 0.0f;  // per head (lane's head l16), log2 units
+  f32x4_t o[CTH];
+#pragma unroll
+  for (int c = 0; c < CTH; ++c) o[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const float sl2 = a.scale * kLog2e;
+
   for (int ti = 0; ti < ntiles; ++ti) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    DSV41_TS(12 + 2 * (ti & 3));
     if (ti + 1 < ntiles) issue(ti + 1);
     const uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
     const uint16_t* const* rp = rptr[ti % 3];
-    const int rb = wave * 16;  // this wave's 16 key rows of the tile
+    const int rb = rw * 16;  // this wave's 16 key rows of the tile
     f32x4_t s = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     {
       const int j = rb + l16;
@@ -384,57 +401,62 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const AttnArgs a) {
       for (int ks = 0; ks < KS; ++ks)
         s = mfma_bf16_16x16x32(*(const uint4*)(krow + (((ks * 4 + g) ^ (j & 7)) * 8)), qf[ks], s);
     }
-    float p[4];
+    // s[i] = score of key row rb + 4g + i for head h0 + l16
+    float x[4];
     float tmax = -1e30f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x = rp[rb + 4 * g + i] ? s[i] * a.scale : -1e30f;
-      p[i] = x;
-      tmax = fmaxf(tmax, x);
+      x[i] = rp[rb + 4 * g + i] ? s[i] * sl2 : -1e30f;
+      tmax = fmaxf(tmax, x[i]);
     }
     tmax = fmaxf(tmax, wave_shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, wave_shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = exp2f((m_run - m_new) * kLog2e);
+    const bool bump = tmax > m_ref + kRescale;
+    if (__ballot(bump)) {  // wave-uniform: some head of this wave needs a new reference
+      const float m_new = bump ? tmax : m_ref;
+      const float alpha = exp2f(m_ref - m_new);
+      l_run *= alpha;
+      m_ref = m_new;
+      float al[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+      for (int ct = 0; ct < CTH; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[ct][i] *= al[i];
+    }
     float psum = 0.0f;
+    float p[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      p[i] = rp[rb + 4 * g + i] ? exp2f((p[i] - m_new) * kLog2e) : 0.0f;
+      p[i] = rp[rb + 4 * g + i] ? exp2f(x[i] - m_ref) : 0.0f;
       psum += p[i];
     }
     psum += wave_shfl_xor(psum, 16);
     psum += wave_shfl_xor(psum, 32);
-    l_run = alpha * l_run + psum;
-    m_run = m_new;
-    float al[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i, 64);
+    l_run += psum;
     const uint2 pa = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
-    const int jv = rb + 4 * g;  // rows jv..jv+3; jv % 4 == 0 so (jv + i) & 7 = (jv & 7) + i
-    const uint16_t* vr = buf + jv * DQK + (l16 & 7);
-    const int sw = jv & 7;
+    // V operand: lane (column l16 of the 16-column tile, rows rb + 4g .. +3) via the transpose read: input lane
+    // j of the 16-lane group reads row rb + 4g + j/4, columns 4*(j%4)..+3 of the tile
+    const int vj = rb + 4 * g + (l16 >> 2);
+    const uint16_t* vrow = buf + vj * DQK + ((l16 & 1) << 2);
+    const int vsw = vj & 7;
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[ct][i] *= al[i];
-      const int cch = ct * 2 + (l16 >> 3);  // chunk of column ct*16 + l16
-      const uint16_t v0 = vr[0 * DQK + ((cch ^ (sw + 0)) * 8)];
-      const uint16_t v1 = vr[1 * DQK + ((cch ^ (sw + 1)) * 8)];
-      const uint16_t v2 = vr[2 * DQK + ((cch ^ (sw + 2)) * 8)];
-      const uint16_t v3 = vr[3 * DQK + ((cch ^ (sw + 3)) * 8)];
-      const uint2 vb = make_uint2((uint32_t)v0 | ((uint32_t)v1 << 16), (uint32_t)v2 | ((uint32_t)v3 << 16));
+    for (int ct = 0; ct < CTH; ++ct) {
+      const int cch = ((half * (DV / 2) + ct * 16) >> 3) + ((l16 & 3) >> 1);  // chunk of column col0 + 4*(l16&3)
+      const uint2 vb = lds_read_tr16(vrow + ((cch ^ vsw) << 3));
       o[ct] = mfma_bf16_16x16x16(pa, vb, o[ct]);
     }
+    DSV41_TS(13 + 2 * (ti & 3));
     if (ti + 2 < ntiles) resolve(ti + 2);
   }
   __syncthreads();
+  DSV41_TS(20);
 
-  // ---- merge the 4 waves' states (per head): M = max m_w, factor_w = exp(m_w - M), L = sum factor_w * l_w.
-  // Every wave parks its scaled accumulator in LDS ([wave][16 heads][DV] fp32, aliasing the tile buffers), then the
-  // block sums the 4 copies with a rolled loop over column pairs.
-  if (g == 0) {
-    wm[wave][l16] = m_run;
-    wl[wave][l16] = l_run;
+  // ---- merge the 4 row-waves' states per head (both column halves hold identical m, l)
+  if (half == 0 && g == 0) {
+    wm[rw][l16] = m_ref;
+    wl[rw][l16] = l_run;
   }
   __syncthreads();
   {
@@ -443,36 +465,38 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const AttnArgs a) {
     for (int i = 0; i < 4; ++i) {
       const int hh = 4 * g + i;
       const float M = fmaxf(fmaxf(wm[0][hh], wm[1][hh]), fmaxf(wm[2][hh], wm[3][hh]));
-      fac[i] = exp2f((wm[wave][hh] - M) * kLog2e);
+      fac[i] = exp2f(wm[rw][hh] - M);
     }
-    float* xw = (float*)ktile + wave * 16 * DV;
+    float* xw = (float*)ktile + rw * 16 * DV + half * (DV / 2);
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
+    for (int ct = 0; ct < CTH; ++ct)
 #pragma unroll
       for (int i = 0; i < 4; ++i) xw[(4 * g + i) * DV + ct * 16 + l16] = o[ct][i] * fac[i];
   }
   __syncthreads();
+  DSV41_TS(21);
   const float* xb = (const float*)ktile;
   const bool final_out = a.nsplit == 1;
   const long pr = pos < 0 ? 0 : pos;
+  const float ln2 = 0.6931471805599453f;
 #pragma unroll 2
-  for (int e = tid; e < 16 * DV / 2; e += 256) {  // column pairs (2c, 2c + 1) of head hh
+  for (int e = tid; e < 16 * DV / 2; e += 512) {  // column pairs (2c, 2c + 1) of head hh
     const int hh = e / (DV / 2), c = 2 * (e - hh * (DV / 2));
     const int hout = h0 + hh;
     if (hout >= H) continue;
     const float M = fmaxf(fmaxf(wm[0][hh], wm[1][hh]), fmaxf(wm[2][hh], wm[3][hh]));
     float L = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) L += wl[w][hh] * exp2f((wm[w][hh] - M) * kLog2e);
+    for (int w = 0; w < 4; ++w) L += wl[w][hh] * exp2f(wm[w][hh] - M);
     float v0 = 0.0f, v1 = 0.0f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float2 x = *(const float2*)(xb + (w * 16 + hh) * DV + c);
-      v0 += x.x;
-      v1 += x.y;
+      const float2 xx = *(const float2*)(xb + (w * 16 + hh) * DV + c);
+      v0 += xx.x;
+      v1 += xx.y;
     }
     if (final_out) {
-      const float inv = 1.0f / (L + exp2f((a.sink[hout] - M) * kLog2e));
+      const float inv = 1.0f / (L + exp2f(a.sink[hout] * kLog2e - M));
       float re = round_bf16(v0 * inv), im = round_bf16(v1 * inv);
       if (a.rd > 0 && c >= DV - a.rd) {
         const int jj = (c - (DV - a.rd)) >> 1;
@@ -488,11 +512,12 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const AttnArgs a) {
       const long pi = ((long)r * H + hout) * a.nsplit + sp;
       *(uint32_t*)((uint16_t*)a.pacc + pi * DV + c) = pack_bf16x2(v0 * inv, v1 * inv);
       if (c == 0) {
-        a.pm[pi] = M;
+        a.pm[pi] = M * ln2;  // natural-log units, as the combine expects
         a.pl[pi] = L;
       }
     }
   }
+  DSV41_TS(22);
 }
 
 // Merge bf16-normalised partials: out = sum_s w_s l_s o_s / (sum_s w_s l_s + exp(sink - M)), w_s = exp(m_s - M).
@@ -568,7 +593,7 @@ template <int DQK, int DV>
 int launch_attn(AttnArgs& a, hipStream_t st) {
   if (use_decode_kernel(a.R, a.H)) {
     dim3 grid(a.nsplit, (a.H + 15) / 16, a.R);
-    attn_decode_kernel<DQK, DV><<<grid, 256, 0, st>>>(a);
+    attn_decode_kernel<DQK, DV><<<grid, 512, 0, st>>>(a);
     DSV41_CHECK_LAUNCH();
     if (a.nsplit > 1) {
       attn_decode_combine_kernel<DV><<<dim3((a.H + 3) / 4, a.R), 256, 0, st>>>(a);
@@ -647,6 +672,11 @@ int finish_plan(AttnArgs& a, int want_nsplit, void* ws, long ws_bytes, int dv) {
 }  // namespace
 
 extern "C" {
+
+#ifdef DSV41_TIMING
+int dsv41_read_ts_attn(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
+#endif
+
 
 long dsv41_attn_workspace_bytes(int R, int H, int L, int dv, int want_nsplit) {
   int ns, chunk;

@@ -101,6 +101,20 @@ DSV41_DEV f32x4_t mfma_fp8_16x16x128(i32x8_t a, i32x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
 }
 
+// Phase timestamps for development builds (-DDSV41_TIMING): thread 0 of block (0,0,0) records wall_clock64() (a
+// constant-rate clock) into g_dsv41_ts[i].  Compiled out otherwise.
+#ifdef DSV41_TIMING
+__device__ long long g_dsv41_ts[64];
+#define DSV41_TS(i)                                                                                       \
+  do {                                                                                                    \
+    if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) g_dsv41_ts[i] = wall_clock64(); \
+  } while (0)
+#else
+#define DSV41_TS(i) \
+  do {              \
+  } while (0)
+#endif
+
 #define DSV41_CHECK_LAUNCH()                          \
   do {                                                \
     hipError_t _e = hipGetLastError();                \

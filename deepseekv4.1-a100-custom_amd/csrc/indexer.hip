@@ -8,7 +8,7 @@
 //   dsv41_topk_indices   the k largest scores of each row, ascending index order, -1 padding / masking
 //                        (dsv41/fused3.py:65-75, dsv41/cuda/topk_select.cu); ties resolved lowest index first.
 //
-// Score kernel: 4 waves per workgroup, each wave owns 128 consecutive key positions of one query row (8 MFMA
+// Score kernel: 4 waves per workgroup, each wave owns 64 consecutive key positions of one query row (4 MFMA
 // column tiles of 16 keys, loads issued before the query preparation); the query fragments live in VGPRs.  MFMA output layout: lane l holds key (l & 15) and
 // heads 4*(l >> 4) + i, so the head reduction is 16 in-lane FMAs plus two cross-lane shuffles.
 // Keys at positions >= cl are never read: the scan is bounded by the valid count, not the allocated capacity.
@@ -46,7 +46,7 @@ DSV41_DEV long row_cl(const ScoreArgs& a, int r) {
 
 constexpr int kHT = 4;            // head tiles of 16 (up to 64 indexer heads)
 constexpr int kHistBins = 4096;   // top 12 bits of the order-preserving score key (8 bins per octave)
-constexpr int kKeysPerWave = 128;  // 8 column tiles of 16 keys
+constexpr int kKeysPerWave = 64;   // 4 column tiles of 16 keys (two or more waves per SIMD)
 constexpr int kKeysPerWG = 4 * kKeysPerWave;
 
 // One column tile (16 keys) against all head tiles; returns this lane's partial weighted relu sum for key l16.
@@ -80,6 +80,7 @@ DSV41_DEV float score_tile(const i32x8_t (&qa8)[kHT], const uint4 (&qa16)[kHT][4
 
 template <int KFMT, bool HIST>
 __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
+  DSV41_TS(30);
   __shared__ int lhist[HIST ? kHistBins : 1];
   const int r = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -103,7 +104,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
   const int lim = (int)cl;
 
   // ---- issue the key loads of the first column tiles before the query preparation
-  constexpr int NT = KFMT == 1 ? 8 : 4;  // column tiles prefetched per round
+  constexpr int NT = 4;  // column tiles prefetched per round
   uint4 k0[NT], k1[NT];
   uint4 kb16[NT][4];
   float ksc[NT];
@@ -149,6 +150,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
     wl[ht] = a.w[(long)r * a.w_rstride + hc];
     if (!hv) wl[ht] = 0.0f;
   }
+  DSV41_TS(31);
   float wr[kHT][4];  // weights of the heads this lane's accumulators hold: ht*16 + 4g + i
 #pragma unroll
   for (int ht = 0; ht < kHT; ++ht)
@@ -172,6 +174,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
     }
   }
   }  // kt0 < cl
+  DSV41_TS(32);
   if (HIST) {
     __syncthreads();
     int* gh = a.hist + (long)r * kHistBins;
@@ -419,6 +422,11 @@ int launch_score(ScoreArgs& a, hipStream_t st) {
 }  // namespace
 
 extern "C" {
+
+#ifdef DSV41_TIMING
+int dsv41_read_ts_idx(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
+#endif
+
 
 int dsv41_index_score(const void* q, long q_rstride, const float* w, long w_rstride, int R, int HI, int D, int kfmt,
                       const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,

@@ -183,6 +183,7 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
   __shared__ int tmp[40];
   __shared__ int pa[1024], pc[1024];  // per-chunk exclusive prefix of above / candidate counts (<= 1024 chunks)
   __shared__ int s_digit, s_rem;
+  DSV41_TS(0);
   const int r = blockIdx.x, tid = threadIdx.x;
   const int c = row_c(a, r), k = a.k;
   int* orow = a.out + (long)r * a.out_rstride;
@@ -203,6 +204,7 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
     na = cnt[0];
     nc = cnt[1];
   }
+  DSV41_TS(1);
   int tot_a, tot_c;
   const int ea = block_scan<kFinThreads>(na, tmp, &tot_a);
   const int ec = block_scan<kFinThreads>(nc, tmp, &tot_c);
@@ -213,6 +215,7 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
 #pragma unroll 1
   for (int i = tid; i < words; i += kFinThreads) bitmap[i] = 0u;
   __syncthreads();
+  DSV41_TS(2);
   const int need = k - tot_a;  // candidates to take (1 <= need <= tot_c)
   const bool staged = tot_c <= kCandCap;
   const long reg = (long)r * a.n;
@@ -242,6 +245,7 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
     atomicOr(&bitmap[i >> 5], 1u << (i & 31));
   }
   __syncthreads();
+  DSV41_TS(3);
   // candidate j (0 <= j < tot_c, index order) -> (key, position)
   auto cand = [&](int j, uint32_t* key, int* pos) {
     if (staged) {
@@ -285,6 +289,7 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
     remaining = s_rem;
     __syncthreads();
   }
+  DSV41_TS(4);
   // ---- take candidates with low bits > prefix, and the first `remaining` equal ones in index order
   int eq_seen = 0;
 #pragma unroll 1
@@ -302,6 +307,7 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
     eq_seen += tot_eq;
   }
   __syncthreads();
+  DSV41_TS(5);
   // ---- ordered emission from the bitmap: thread t owns words [t*wpt, (t+1)*wpt)
   const int wpt = (words + kFinThreads - 1) / kFinThreads;
   const int w0 = tid * wpt;
@@ -320,6 +326,7 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
       ++o;
     }
   }
+  DSV41_TS(6);
 #pragma unroll 1
   for (int i = tot + tid; i < k; i += kFinThreads) orow[i] = -1;
 #pragma unroll 1
@@ -329,6 +336,10 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
 }  // namespace
 
 extern "C" {
+
+#ifdef DSV41_TIMING
+int dsv41_read_ts(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
+#endif
 
 long dsv41_select_workspace_bytes(int R, int n) {
   const long nch = (n + kChunk - 1) / kChunk;

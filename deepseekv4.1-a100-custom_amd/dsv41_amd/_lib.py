@@ -5,11 +5,12 @@ tensors are not on a GPU, the entry points raise."""
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "libdsv41_hip.so"
+LIB_PATH = Path(os.environ.get("DSV41_HIP_LIB") or Path(__file__).resolve().parent / "libdsv41_hip.so")
 
 _P, _L, _I, _F = ctypes.c_void_p, ctypes.c_long, ctypes.c_int, ctypes.c_float
 

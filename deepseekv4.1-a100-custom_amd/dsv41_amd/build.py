@@ -21,29 +21,33 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Xclang", "-tar
          "-packed-fp32-ops", f"-I{INCLUDE}", f"-I{CSRC}"]
 
 
-def _compile(src: Path) -> Path:
-    obj = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, extra=(), tag: str = "") -> Path:
+    obj = OBJ / (src.stem + tag + ".o")
+    cmd = [HIPCC, *FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stderr}")
     return obj
 
 
-def build(verbose: bool = False) -> Path:
+def build(verbose: bool = False, out: Path | None = None, defines=()) -> Path:
+    """Compile and link; `out`/`defines` build a variant library (e.g. -DDSV41_TIMING phase timestamps)."""
     OBJ.mkdir(exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
+    extra = [f"-D{d}" for d in defines]
+    tag = "".join("_" + d.lower() for d in defines)
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda p: _compile(p, extra, tag), srcs))
+    target = Path(out) if out else LIB
+    tmp = target.with_suffix(".so.tmp")
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, target)
     if verbose:
-        print(f"built {LIB}", file=sys.stderr)
-    return LIB
+        print(f"built {target}", file=sys.stderr)
+    return target
 
 
 if __name__ == "__main__":
