@@ -156,6 +156,85 @@ def run_decode(args, dev):
     return dict(cfg=cfg, step_us=step_us, kern_us=kern_us, kern_bytes=kb, steps=replays * NL, sel_union=sel_union)
 
 
+def run_prefill(args, dev):
+    """Config C3: one layer's 2048-token chunk after 65536 prior tokens -- the chunk's cache appends (SWA rows,
+    compressed rows, index keys), the indexer (score + per-query causal top-2048) and the sparse attention over
+    [window history | chunk | compressed] with 128 + 2048 indices per query.  Eager launches, events on the launch
+    stream, median of the repetitions."""
+    import numpy as np
+    import torch
+    from dsv41_amd import cache as C
+    from dsv41_amd.indexer import index_topk
+    from dsv41_amd.kernels import sparse_attn
+    from dsv41_amd.workloads import PREFILL, make_prefill_inputs, DQK, DV, DI, H, HI, WIN
+    cfg = PREFILL["C3"]
+    x = make_prefill_inputs(cfg, dev)
+    g = torch.Generator(device=dev).manual_seed(7)
+    S = cfg.chunk
+    kv_raw = (torch.randn(1, S, DQK, generator=g, device=dev)).to(torch.bfloat16)
+    kvn = (torch.rand(DQK, generator=g, device=dev) + 0.5).to(torch.bfloat16)
+    lat = (torch.randn(1, S // cfg.ratio, DQK, generator=g, device=dev)).to(torch.bfloat16)
+    kraw = (torch.randn(1, S // cfg.ratio, DI, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (torch.rand(DI, generator=g, device=dev) + 0.5).to(torch.bfloat16)
+    ring = torch.zeros(1, WIN, DQK, dtype=torch.bfloat16, device=dev)
+    rd = 64
+    ang = torch.outer(torch.arange(cfg.end + 8, dtype=torch.float32),
+                      1.0 / (10000.0 ** (torch.arange(0, rd, 2, dtype=torch.float32) / rd)))
+    cos, sin = torch.cos(ang).to(dev), torch.sin(ang).to(dev)
+    ckv_tab = torch.zeros(1, cfg.n_c + 8, DQK, dtype=torch.bfloat16, device=dev)
+    ckv_tab[:, :x["ckv"].shape[1]] = x["ckv"]
+    kb_tab = torch.zeros(1, cfg.n_c + 8, DI, dtype=torch.bfloat16, device=dev)
+    k8_tab = torch.zeros(1, cfg.n_c + 8, DI, dtype=torch.float8_e4m3fn, device=dev)
+    ks_tab = torch.zeros(1, cfg.n_c + 8, dtype=torch.float32, device=dev)
+    k8_tab[:, :x["k8"].shape[1]] = x["k8"]
+    ks_tab[:, :x["ks"].shape[1]] = x["ks"]
+    sink = torch.zeros(H, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    E = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+
+    def step(ev=None):
+        if ev: ev[0].record(stream)
+        win_kv, widx = C.window_kv(kv_raw, kvn, 1e-6, cos, sin, rd, ring, cfg.prior)
+        C.write_compress_kv(ckv_tab, lat, cfg.prior, cfg.ratio, cos, sin, rd)
+        C.write_index_k(kb_tab, kraw, kn, 1e-6, cfg.prior, cfg.ratio, cos, sin, rd, k8=k8_tab.view(torch.uint8),
+                        k_scale=ks_tab)
+        if ev: ev[1].record(stream)
+        off = win_kv.shape[1]
+        cidx = index_topk(x["q_idx"], x["w_idx"], k8_tab, cfg.prior, cfg.ratio, cfg.topk, off, k_scale=ks_tab)
+        if ev: ev[2].record(stream)
+        kv = torch.cat([win_kv, ckv_tab[:, :cfg.n_c]], dim=1)
+        idx = torch.cat([widx, cidx], dim=-1)
+        if ev: ev[3].record(stream)
+        o = sparse_attn(x["q"], kv, sink, idx, DQK ** -0.5, d_v=DV)
+        if ev: ev[4].record(stream)
+        return o
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize(dev)
+    times = {"appends": [], "indexer": [], "glue": [], "attention": [], "total": []}
+    for _ in range(max(3, min(args.prefill_reps, 20))):
+        ev = [E() for _ in range(5)]
+        step(ev)
+        torch.cuda.synchronize(dev)
+        for i, k in enumerate(["appends", "indexer", "glue", "attention"]):
+            times[k].append(ev[i].elapsed_time(ev[i + 1]) * 1000.0)
+        times["total"].append(ev[0].elapsed_time(ev[4]) * 1000.0)
+    t = {k: float(np.median(v)) for k, v in times.items()}
+    T = cfg.n_c
+    idx_flops = sum(2 * HI * DI * ((cfg.prior + i + 1) // cfg.ratio) for i in range(S))
+    att_flops = S * (WIN + cfg.topk) * H * (DQK + DV) * 2
+    log(f"[bench] prefill C3 phases (us): {t}")
+    return {"config": f"{cfg.name}: {S}-token chunk after {cfg.prior} tokens, ratio {cfg.ratio}, top-k {cfg.topk}, "
+                      f"{T} compressed rows, 64 heads x 576",
+            "tok_per_s": round(S / (t["total"] * 1e-6), 1), "us_per_chunk": round(t["total"], 1),
+            "phase_us": {k: round(v, 1) for k, v in t.items()},
+            "mfma_frac": {"indexer_fp8": round(idx_flops / (t["indexer"] * 1e-6) / (MFMA_FP8_TFLOPS * 1e12), 4),
+                          "attention_bf16": round(att_flops / (t["attention"] * 1e-6) / (MFMA_BF16_TFLOPS * 1e12), 4),
+                          "combined": round((idx_flops / (MFMA_FP8_TFLOPS * 1e12) + att_flops /
+                                             (MFMA_BF16_TFLOPS * 1e12)) / (t["total"] * 1e-6), 4)}}
+
+
 def cpu_baseline(cfg, budget_s: float):
     """The oracle (numpy port of the reference's decode path) on the host: index score + top-k + sattn2 for one
     slot of the workload, repeated until the budget is spent; scaled to a full layer-step (x slots)."""
@@ -203,6 +282,8 @@ def main():
     ap.add_argument("--layers", type=int, default=8, help="independent cache copies rotated per step")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-reps", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the path shards by slot with no exchange; see the design "
@@ -220,6 +301,7 @@ def main():
     achieved = kb[dom] / (ku[dom] * 1e-6) / 1e9
     alg = survey_bytes(cfg)
     frac_step = alg / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS
+    pre = None if args.no_prefill else run_prefill(args, dev)
     cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_budget)
     out = {
         "metric": "attn decode us/layer-step + % HBM roofline @128Kx4 slots; prefill tok/s @2K chunk",
@@ -243,6 +325,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes": kb[dom]},
+        "prefill": pre,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -520,6 +520,206 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   DSV41_TS(22);
 }
 
+// ------------------------------------------------------------------------------------------------ prefill kernel
+// Many query rows (prefill chunk): one workgroup per (query row, 64 heads), whole key list, no split.  4 waves:
+// wave (hh, ch) = (head half of 32, column half of DV/2 / row half of the 64-key tile).
+//   S^T[32 rows x 32 heads] = K Q^T for the wave's row half: 32x32x16 bf16 MFMA (Q held in VGPRs);
+//   the two row halves exchange their per-head tile maxima (common lazy reference) and their P tiles (bf16, stored
+//   in MFMA-fragment order, so the PV A operand is one 16-byte LDS read);
+//   O[32 heads x DV/2] += P[32 x 64] V[64 x DV/2]: V fragments from the transpose read (two per 16-deep k block).
+// 32x32 accumulator layout: lane l holds column l % 32 and rows 8*(i/4) + 4*(l/32) + (i%4), i = 0..15.
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+
+DSV41_DEV f32x16_t mfma_bf16_32x32x16(uint4 a, uint4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+template <int DQK, int DV>
+__global__ void __launch_bounds__(256) attn_prefill_kernel(const AttnArgs a) {
+  constexpr int KS = DQK / 16;  // 16-deep k steps of QK^T
+  constexpr int CB = DV / 64;   // 32-column output blocks per wave
+  constexpr int U = DQK / 8;    // 16-byte chunks per row; chunk c of row j at j*U + (c ^ (j & 7))
+  static_assert(U % 8 == 0 && CB >= 1, "row widths");
+  constexpr int TILE = 64;
+  constexpr int TILE_ELEMS = TILE * DQK;
+  constexpr float kRescale = 8.0f;
+  __shared__ __align__(16) uint16_t ktile[2 * TILE_ELEMS];
+  __shared__ const uint16_t* rptr[3][TILE];
+  __shared__ uint4 pfrag[2][2][2][64];  // [head half][row half][k block][lane]
+  __shared__ float smax[2][2][32];      // [head half][row half][head]
+  __shared__ float sl[2][2][32];
+
+  const int hb = blockIdx.y, r = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hh = wave & 1, ch = wave >> 1;
+  const int n32 = lane & 31, half = lane >> 5;
+  const int H = a.H;
+  const int hq = hb * 64 + hh * 32 + n32;  // this lane's head in the S^T orientation
+
+  long slot, pos = 0, pmax = 0, plim = 0;
+  const int W = a.n1;
+  if (a.mode == 1) {
+    slot = a.seq[r];
+    pos = a.pos[r];
+    pmax = a.pmax[r];
+    plim = a.plim ? a.plim[r] : pos;
+  } else {
+    slot = r / a.rows_per_slot;
+  }
+  const uint16_t* base1 = a.kv1 + slot * a.kv1_sstride;
+  const uint16_t* base2 = a.kv2 ? a.kv2 + slot * a.kv2_sstride : nullptr;
+  const int* irow = a.t > 0 ? a.idx + (long)r * a.idx_rstride : nullptr;
+  const int L = a.L;
+  const int ntiles = (L + TILE - 1) / TILE;
+
+  auto resolve = [&](int ti) {
+    if (tid < TILE) {
+      const int j = ti * TILE + tid;
+      const uint16_t* p = nullptr;
+      if (j < L) {
+        if (a.mode == 1 && j < W) {
+          int m = (int)(pmax - j) % W;
+          m = m < 0 ? m + W : m;
+          const long held = pmax - m;
+          if (held >= 0 && held <= plim && pos - held < W) p = base1 + (long)j * DQK;
+        } else {
+          const int ix = irow[a.mode == 1 ? j - W : j];
+          if (a.mode == 1) {
+            if (ix >= 0 && ix < a.n2) p = base2 + (long)ix * DQK;
+          } else if (ix >= 0 && ix < a.n1 + a.n2) {
+            p = ix < a.n1 ? base1 + (long)ix * DQK : base2 + (long)(ix - a.n1) * DQK;
+          }
+        }
+      }
+      rptr[ti % 3][tid] = p;
+    }
+  };
+  auto issue = [&](int ti) {
+    uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
+    const uint16_t* const* rp = rptr[ti % 3];
+#pragma unroll 2
+    for (int rd = 0; rd < TILE * U / 256; ++rd) {
+      const int q = rd * 256 + wave * 64 + lane;
+      const int j = q / U, cs = q - j * U;
+      const int c = cs ^ (j & 7);
+      const uint16_t* p = rp[j];
+      __builtin_amdgcn_global_load_lds((const void*)(p ? p + c * 8 : g_zero_row),
+                                       (void*)(buf + (rd * 256 + wave * 64) * 8), 16, 0, 0);
+    }
+  };
+
+#pragma unroll 1
+  for (int ti = 0; ti < 2 && ti < ntiles; ++ti) resolve(ti);
+  uint4 qf[KS];
+  {
+    const int h = hq < H ? hq : H - 1;
+    const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)h * DQK + half * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qrow + ks * 16);
+  }
+  __syncthreads();
+  issue(0);
+
+  float m_ref = -1e30f, l_lane = 0.0f;  // reference max (log2 units) of head hq; partial sum of this lane's p
+  f32x16_t o[CB];
+#pragma unroll
+  for (int c = 0; c < CB; ++c)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[c][i] = 0.0f;
+  const float sl2 = a.scale * kLog2e;
+  const int rb = ch * 32;
+
+  for (int ti = 0; ti < ntiles; ++ti) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (ti + 1 < ntiles) issue(ti + 1);
+    const uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
+    const uint16_t* const* rp = rptr[ti % 3];
+    f32x16_t s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+    {
+      const int j = rb + n32;
+      const uint16_t* krow = buf + j * DQK;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        s = mfma_bf16_32x32x16(*(const uint4*)(krow + (((2 * ks + half) ^ (j & 7)) << 3)), qf[ks], s);
+    }
+    float tmax = -1e30f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {  // s becomes the scaled, masked logits (log2 units)
+      const int j = rb + 8 * (i >> 2) + 4 * half + (i & 3);
+      s[i] = rp[j] ? s[i] * sl2 : -1e30f;
+      tmax = fmaxf(tmax, s[i]);
+    }
+    tmax = fmaxf(tmax, wave_shfl_xor(tmax, 32));
+    if (half == 0) smax[hh][ch][n32] = tmax;
+    __syncthreads();
+    tmax = fmaxf(smax[hh][0][n32], smax[hh][1][n32]);
+    const bool bump = tmax > m_ref + kRescale;
+    if (__ballot(bump)) {
+      const float m_new = bump ? tmax : m_ref;
+      const float alpha = exp2f(m_ref - m_new);
+      l_lane *= alpha;
+      m_ref = m_new;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float al = __shfl(alpha, 8 * (i >> 2) + 4 * half + (i & 3), 64);
+#pragma unroll
+        for (int c = 0; c < CB; ++c) o[c][i] *= al;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {  // s becomes p
+      s[i] = s[i] > -1e29f ? exp2f(s[i] - m_ref) : 0.0f;
+      l_lane += s[i];
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+      pfrag[hh][ch][m][lane] = make_uint4(pack_bf16x2(s[8 * m + 0], s[8 * m + 1]), pack_bf16x2(s[8 * m + 2], s[8 * m + 3]),
+                                          pack_bf16x2(s[8 * m + 4], s[8 * m + 5]), pack_bf16x2(s[8 * m + 6], s[8 * m + 7]));
+    __syncthreads();
+    // PV over the 4 k blocks of 16 rows: rows 32*src + 16*m + {4*half + e, 8 + 4*half + e}
+    const int j16 = lane & 15, colsub = ((lane >> 4) & 1) * 16;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int src = kb >> 1, m = kb & 1;
+      const uint4 pa = pfrag[hh][src][m][lane];
+      const int r0 = 32 * src + 16 * m + 4 * half + (j16 >> 2);  // row of this lane's transpose-read input
+      const int r1 = r0 + 8;
+      const uint16_t* v0 = buf + r0 * DQK;
+      const uint16_t* v1 = buf + r1 * DQK;
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const int col = ch * (DV / 2) + cb * 32 + colsub + 4 * (j16 & 3);  // first of the 4 columns read
+        const int cc = col >> 3, co = col & 7;
+        const uint2 b0 = lds_read_tr16(v0 + ((cc ^ (r0 & 7)) << 3) + co);
+        const uint2 b1 = lds_read_tr16(v1 + ((cc ^ (r1 & 7)) << 3) + co);
+        o[cb] = mfma_bf16_32x32x16(pa, make_uint4(b0.x, b0.y, b1.x, b1.y), o[cb]);
+      }
+    }
+    if (ti + 2 < ntiles) resolve(ti + 2);
+  }
+  // ---- normaliser: l over both lane halves and both row halves, sink term; O rows are heads 8*(i/4)+4*half+(i%4)
+  float lh = l_lane + wave_shfl_xor(l_lane, 32);
+  if (half == 0) sl[hh][ch][n32] = lh;
+  __syncthreads();
+  const int hs = hq < H ? hq : H - 1;
+  const float den_lane = sl[hh][0][n32] + sl[hh][1][n32] + exp2f(a.sink[hs] * kLog2e - m_ref);
+  float inv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) inv[i] = 1.0f / __shfl(den_lane, 8 * (i >> 2) + 4 * half + (i & 3), 64);
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    const int c = ch * (DV / 2) + cb * 32 + n32;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int h = hb * 64 + hh * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
+      if (h < H) a.out[(long)r * a.out_rstride + (long)h * DV + c] = f2bf(o[cb][i] * inv[i]);
+    }
+  }
+}
+
 // Merge bf16-normalised partials: out = sum_s w_s l_s o_s / (sum_s w_s l_s + exp(sink - M)), w_s = exp(m_s - M).
 // One workgroup per (row, 4 heads); thread -> (head, 8 consecutive columns); all split loads are independent.
 template <int DV>
@@ -602,6 +802,11 @@ int launch_attn(AttnArgs& a, hipStream_t st) {
     return 0;
   }
   dim3 grid(a.nsplit, (a.H + 63) / 64, a.R);
+  if (a.nsplit == 1 && a.rd == 0) {
+    attn_prefill_kernel<DQK, DV><<<grid, 256, 0, st>>>(a);
+    DSV41_CHECK_LAUNCH();
+    return 0;
+  }
   attn_split_kernel<DQK, DV><<<grid, 256, 0, st>>>(a);
   DSV41_CHECK_LAUNCH();
   if (a.nsplit > 1) {
@@ -637,7 +842,7 @@ void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
     if (per < 2) per = 2;
   } else {
     const long wgs = (long)R * ((H + 63) / 64);
-    const long target = wgs >= 512 ? 1 : (512 + wgs - 1) / wgs;
+    const long target = wgs >= 256 ? 1 : (512 + wgs - 1) / wgs;
     per = (int)((tiles + target - 1) / target);
     if (per < 2 && target > 1) per = 2;
   }

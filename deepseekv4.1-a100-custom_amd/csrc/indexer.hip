@@ -186,9 +186,114 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
   }
 }
 
+// Prefill score kernel (many query rows of one sequence; e4m3 keys + prepared e4m3 queries): a workgroup owns 8
+// consecutive query rows (2 per wave) and a range of key positions, streamed through LDS in 256-key chunks
+// (direct-to-LDS loads, double buffered) and shared by the 4 waves.  Per 16-key column tile a wave runs
+// 2 rows x 4 head tiles 16x16x128 fp8 MFMAs on one B fragment.  Key tiles past a row's causal limit are skipped.
+constexpr int kPQ = 8;       // query rows per workgroup
+constexpr int kPChunk = 256;  // keys per LDS chunk (32 KB)
+
+__global__ void __launch_bounds__(256) index_score_prefill_kernel(const ScoreArgs a, int key_split) {
+  __shared__ __align__(16) uint8_t kbuf[2][kPChunk * 128];
+  __shared__ float sbuf[2][kPChunk];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int r0 = blockIdx.y * kPQ;
+  const int slot = r0 / a.rows_per_slot;  // all rows of a block belong to one sequence (host-checked)
+  // causal limits of the block's rows (increasing with the row)
+  long cl_lo = row_cl(a, r0), cl_hi = row_cl(a, min(r0 + kPQ, a.R) - 1);
+  if (cl_hi > a.n_pos) cl_hi = a.n_pos;
+  const int span = (a.n_pos + key_split - 1) / key_split;
+  const int kb0 = blockIdx.x * span;
+  const int kb1 = min((long)(kb0 + span), cl_hi);
+  if (kb0 >= kb1) return;
+  const uint8_t* kbase = (const uint8_t*)a.keys + (long)slot * a.k_sstride;
+  const float* sbase = a.kscale + (long)slot * a.ks_sstride;
+  const int nchunks = (kb1 - kb0 + kPChunk - 1) / kPChunk;
+  auto issue = [&](int ci) {  // 256 keys x 128 B = 2048 chunks of 16 B: 8 per thread; + 256 scales
+    const int c0 = kb0 + ci * kPChunk;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      // LDS unit q holds key q / 8, 16-byte part (q % 8) ^ (key % 8) (XOR swizzle against bank conflicts)
+      const int q = u * 256 + threadIdx.x;
+      const int kl = q >> 3;
+      int key = c0 + kl;
+      key = key < kb1 ? key : kb1 - 1;
+      __builtin_amdgcn_global_load_lds((const void*)(kbase + (long)key * 128 + ((q & 7) ^ (kl & 7)) * 16),
+                                       (void*)(kbuf[ci & 1] + (u * 256 + wave * 64) * 16), 16, 0, 0);
+    }
+    int key = c0 + threadIdx.x;
+    key = key < kb1 ? key : kb1 - 1;
+    __builtin_amdgcn_global_load_lds((const void*)(sbase + key), (void*)(sbuf[ci & 1] + wave * 64), 4, 0, 0);
+  };
+  issue(0);
+  // query fragments of this wave's 2 rows and their head weights
+  i32x8_t qa[2][kHT];
+  float wr[2][kHT][4];
+  const int nht = (a.HI + 15) / 16;
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq) {
+    const int r = min(r0 + wave * 2 + qq, a.R - 1);
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht) {
+      const int h = ht * 16 + l16;
+      const bool hv = ht < nht && h < a.HI;
+      const uint4* qrow = (const uint4*)((const uint8_t*)a.q + (long)r * a.q_rstride + (long)(hv ? h : 0) * 128 + g * 32);
+      const uint4 u0 = qrow[0], u1 = qrow[1];
+      qa[qq][ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+      const float wv = hv ? a.w[(long)r * a.w_rstride + h] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wr[qq][ht][i] = __shfl(wv, 4 * g + i, 64);
+    }
+  }
+  int rows[2];
+  long clr[2];
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq) {
+    rows[qq] = r0 + wave * 2 + qq;
+    clr[qq] = rows[qq] < a.R ? row_cl(a, rows[qq]) : 0;
+    if (clr[qq] > a.n_pos) clr[qq] = a.n_pos;
+  }
+  for (int ci = 0; ci < nchunks; ++ci) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (ci + 1 < nchunks) issue(ci + 1);
+    const int c0 = kb0 + ci * kPChunk;
+    const uint8_t* kb = kbuf[ci & 1];
+    const float* sb = sbuf[ci & 1];
+    const long wave_lim = clr[1] > clr[0] ? clr[1] : clr[0];
+#pragma unroll 2
+    for (int kt = 0; kt < kPChunk / 16; ++kt) {
+      const int t0 = c0 + kt * 16;
+      if (t0 >= kb1 || t0 >= wave_lim) break;  // wave-uniform
+      const int kl = kt * 16 + l16;
+      const uint4 k0 = *(const uint4*)(kb + kl * 128 + (((2 * g) ^ (kl & 7)) << 4));
+      const uint4 k1 = *(const uint4*)(kb + kl * 128 + (((2 * g + 1) ^ (kl & 7)) << 4));
+      const i32x8_t bfrag = i32x8_t{(int)k0.x, (int)k0.y, (int)k0.z, (int)k0.w, (int)k1.x, (int)k1.y, (int)k1.z,
+                                    (int)k1.w};
+      const float ksc = sb[kt * 16 + l16];
+      const int t = t0 + l16;
+#pragma unroll
+      for (int qq = 0; qq < 2; ++qq) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int ht = 0; ht < kHT; ++ht) {
+          if (ht < nht) {
+            const f32x4_t acc = mfma_fp8_16x16x128(qa[qq][ht], bfrag, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum += wr[qq][ht][i] * fmaxf(acc[i], 0.0f);
+          }
+        }
+        sum += wave_shfl_xor(sum, 16);
+        sum += wave_shfl_xor(sum, 32);
+        if (g == 0 && rows[qq] < a.R && t < clr[qq] && t < kb1)
+          a.out[(long)rows[qq] * a.out_rstride + t] = sum * ksc;
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------------------ top-k
-constexpr int kTopkThreads = 1024;
-constexpr int kTopkCache = 32768;  // rows up to this many valid positions are staged in LDS once
 
 struct TopkArgs {
   const float* score;
@@ -203,8 +308,10 @@ struct TopkArgs {
   int offset;
 };
 
-// Block-wide exclusive scan of one int per thread (1024 threads = 16 waves).  Returns the prefix; *total = sum.
+// Block-wide exclusive scan of one int per thread (NT threads = NT/64 waves).  Returns the prefix; *total = sum.
+template <int NT>
 DSV41_DEV int block_excl_scan(int v, int* tmp, int* total) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int x = v;
 #pragma unroll
@@ -215,17 +322,17 @@ DSV41_DEV int block_excl_scan(int v, int* tmp, int* total) {
   if (lane == 63) tmp[wave] = x;
   __syncthreads();
   if (wave == 0) {
-    int w = lane < 16 ? tmp[lane] : 0;
+    int w = lane < NW ? tmp[lane] : 0;
 #pragma unroll
-    for (int d = 1; d < 16; d <<= 1) {
+    for (int d = 1; d < NW; d <<= 1) {
       const int y = __shfl_up(w, d, 64);
       if (lane >= d) w += y;
     }
-    if (lane < 16) tmp[16 + lane] = w;  // inclusive wave prefix
+    if (lane < NW) tmp[16 + lane] = w;  // inclusive wave prefix
   }
   __syncthreads();
   const int before = wave ? tmp[16 + wave - 1] : 0;
-  *total = tmp[31];
+  *total = tmp[16 + NW - 1];
   const int r = before + x - v;
   __syncthreads();
   return r;
@@ -235,13 +342,17 @@ DSV41_DEV int block_excl_scan(int v, int* tmp, int* total) {
 // first histogram already spreads the scores over 2048 bins whatever their magnitude; then an ordered emission in
 // which every wave owns a contiguous chunk and places its selected indices with ballots (ascending order, ties at
 // the threshold taken lowest index first).  Rows with <= kTopkCache valid positions are staged in LDS once.
-__global__ void __launch_bounds__(kTopkThreads) topk_kernel(const TopkArgs a) {
+template <int NT, int CACHE>
+__global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
+  constexpr int kTopkThreads = NT;
+  constexpr int kTopkCache = CACHE;
+  constexpr int NW = NT / 64;
   constexpr int B = 8;  // independent loads in flight per thread per batch
   __shared__ uint32_t keys[kTopkCache];
   __shared__ int hist[2048];
   __shared__ int scan_tmp[32];
-  __shared__ uint32_t red_min[16], red_max[16];
-  __shared__ int w_gt[16], w_eq[16], w_take[16], w_base[16];
+  __shared__ uint32_t red_min[NW], red_max[NW];
+  __shared__ int w_gt[NW], w_eq[NW], w_take[NW], w_base[NW];
   __shared__ int s_digit, s_rem;
   const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* row = a.score + (long)r * a.ld;
@@ -258,21 +369,52 @@ __global__ void __launch_bounds__(kTopkThreads) topk_kernel(const TopkArgs a) {
   auto key_at = [&](int i) -> uint32_t { return cached ? keys[i] : score_key(row[i]); };
 
   uint32_t kmin = 0xffffffffu, kmax = 0u;
-  for (int i0 = tid; i0 < c; i0 += B * kTopkThreads) {
-    float v[B];
+  if ((((uintptr_t)row) & 15) == 0) {  // 16-byte aligned row: float4 loads, 4 x B elements per thread per batch
+    for (int i0 = 4 * tid; i0 < c; i0 += 4 * B * kTopkThreads) {
+      float4 v[B];
 #pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const int i = i0 + u * kTopkThreads;
-      v[u] = row[i < c ? i : 0];
+      for (int u = 0; u < B; ++u) {
+        const int i = i0 + 4 * u * kTopkThreads;
+        v[u] = *(const float4*)(row + (i + 3 < c ? i : 0));
+        if (i + 3 >= c) {  // tail: element-wise
+          v[u].x = row[i < c ? i : 0];
+          v[u].y = row[i + 1 < c ? i + 1 : 0];
+          v[u].z = row[i + 2 < c ? i + 2 : 0];
+          v[u].w = row[0];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const float vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = i0 + 4 * u * kTopkThreads + e;
+          if (i < c) {
+            const uint32_t key = score_key(vv[e]);
+            if (cached) keys[i] = key;
+            kmin = min(kmin, key);
+            kmax = max(kmax, key);
+          }
+        }
+      }
     }
+  } else {
+    for (int i0 = tid; i0 < c; i0 += B * kTopkThreads) {
+      float v[B];
 #pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const int i = i0 + u * kTopkThreads;
-      if (i < c) {
-        const uint32_t key = score_key(v[u]);
-        if (cached) keys[i] = key;
-        kmin = min(kmin, key);
-        kmax = max(kmax, key);
+      for (int u = 0; u < B; ++u) {
+        const int i = i0 + u * kTopkThreads;
+        v[u] = row[i < c ? i : 0];
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int i = i0 + u * kTopkThreads;
+        if (i < c) {
+          const uint32_t key = score_key(v[u]);
+          if (cached) keys[i] = key;
+          kmin = min(kmin, key);
+          kmax = max(kmax, key);
+        }
       }
     }
   }
@@ -293,7 +435,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_kernel(const TopkArgs a) {
   kmin = red_min[0];
   kmax = red_max[0];
 #pragma unroll
-  for (int w = 1; w < 16; ++w) {
+  for (int w = 1; w < NW; ++w) {
     kmin = min(kmin, red_min[w]);
     kmax = max(kmax, red_max[w]);
   }
@@ -319,19 +461,25 @@ __global__ void __launch_bounds__(kTopkThreads) topk_kernel(const TopkArgs a) {
         if (i0 + u * kTopkThreads < c && (d[u] & pmask) == prefix) atomicAdd(&hist[(d[u] >> shift) & (nb - 1)], 1);
     }
     __syncthreads();
-    // descending suffix counts: thread t owns bins 2u, 2u+1 with u = 1023 - t (the scan runs high -> low)
+    // descending suffix counts: thread t owns BPT consecutive bins starting at BPT*u, u = NT-1-t (high -> low)
+    constexpr int BPT = 2048 / NT;
     const int u = kTopkThreads - 1 - tid;
-    const int hlo = 2 * u < nb ? hist[2 * u] : 0, hhi = 2 * u + 1 < nb ? hist[2 * u + 1] : 0;
-    int total;
-    const int greater_hi = block_excl_scan(hlo + hhi, scan_tmp, &total);  // elements in bins > 2u+1
-    if (2 * u + 1 < nb && greater_hi < remaining && remaining <= greater_hi + hhi) {
-      s_digit = 2 * u + 1;
-      s_rem = remaining - greater_hi;
+    int hb[BPT];
+    int local = 0;
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      hb[i] = BPT * u + i < nb ? hist[BPT * u + i] : 0;
+      local += hb[i];
     }
-    const int greater_lo = greater_hi + hhi;
-    if (2 * u < nb && greater_lo < remaining && remaining <= greater_lo + hlo) {
-      s_digit = 2 * u;
-      s_rem = remaining - greater_lo;
+    int total;
+    int greater = block_excl_scan<NT>(local, scan_tmp, &total);  // elements in bins above this thread's range
+#pragma unroll
+    for (int i = BPT - 1; i >= 0; --i) {
+      if (BPT * u + i < nb && greater < remaining && remaining <= greater + hb[i]) {
+        s_digit = BPT * u + i;
+        s_rem = remaining - greater;
+      }
+      greater += hb[i];
     }
     __syncthreads();
     prefix |= (uint32_t)s_digit << shift;
@@ -341,7 +489,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_kernel(const TopkArgs a) {
   }
   const uint32_t thr = kmin + prefix;  // the k-th largest key; `remaining` elements equal to it are taken
   // ---- ordered emission: wave w owns [w*chunk, (w+1)*chunk) of the row, 64 positions per step
-  const int chunk = ((c + 16 * 64 - 1) / (16 * 64)) * 64;
+  const int chunk = ((c + NW * 64 - 1) / (NW * 64)) * 64;
   const int i0 = min(c, wave * chunk), i1 = min(c, i0 + chunk);
   int gt = 0, eq = 0;
   for (int b0 = i0; b0 < i1; b0 += 64 * B) {
@@ -367,7 +515,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_kernel(const TopkArgs a) {
   __syncthreads();
   if (tid == 0) {
     int eq_before = 0, sel_before = 0;
-    for (int w = 0; w < 16; ++w) {
+    for (int w = 0; w < NW; ++w) {
       int take = remaining - eq_before;
       take = take < 0 ? 0 : (take > w_eq[w] ? w_eq[w] : take);
       w_take[w] = take;
@@ -407,6 +555,15 @@ __global__ void __launch_bounds__(kTopkThreads) topk_kernel(const TopkArgs a) {
 int launch_score(ScoreArgs& a, hipStream_t st) {
   if (a.R <= 0 || a.n_pos <= 0) return 0;
   if (a.HI <= 0 || a.HI > 64) return (int)hipErrorInvalidValue;
+  if (a.kfmt == 1 && !a.seq && !a.hist && !a.write_masked && !a.cl && a.R >= 64 && a.rows_per_slot % kPQ == 0) {
+    // prefill: causal rows of one sequence per block of kPQ rows; positions >= the row's limit are not written
+    const int qblocks = (a.R + kPQ - 1) / kPQ;
+    int split = (512 + qblocks - 1) / qblocks;
+    split = split < 1 ? 1 : (split > 16 ? 16 : split);
+    index_score_prefill_kernel<<<dim3(split, qblocks), 256, 0, st>>>(a, split);
+    DSV41_CHECK_LAUNCH();
+    return 0;
+  }
   dim3 grid((a.n_pos + kKeysPerWG - 1) / kKeysPerWG, a.R);
   if (a.hist) {
     if (a.kfmt == 1) index_score_kernel<1, true><<<grid, 256, 0, st>>>(a);
@@ -474,7 +631,8 @@ int dsv41_topk_indices(const float* score, long ld, int R, int n, int k, const l
   a.out = out;
   a.out_rstride = out_rstride;
   a.offset = offset;
-  topk_kernel<<<R, kTopkThreads, 0, (hipStream_t)stream>>>(a);
+  if (R >= 512 && n <= 17408) topk_kernel<256, 17408><<<R, 256, 0, (hipStream_t)stream>>>(a);  // many short rows
+  else topk_kernel<1024, 32768><<<R, 1024, 0, (hipStream_t)stream>>>(a);
   DSV41_CHECK_LAUNCH();
   return 0;
 }

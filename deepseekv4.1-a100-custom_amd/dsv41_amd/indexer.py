@@ -36,11 +36,11 @@ def index_topk(q: torch.Tensor, weights: torch.Tensor, index_k: torch.Tensor, st
         wf = torch.empty(b * s, 64, dtype=torch.float32, device=dev)
         call("dsv41_index_qprep", ptr(qc), ptr(w), b * s, H, ptr(q8), ptr(wf), st)
         call("dsv41_index_score", ptr(q8), 64 * 128, ptr(wf), 64, b * s, H, D, 1, ptr(index_k), index_k.stride(0),
-             ptr(ks), ks.stride(0), None, s, None, start_pos, ratio, T, 1, ptr(score), T, None, st)
+             ptr(ks), ks.stride(0), None, s, None, start_pos, ratio, T, 0, ptr(score), T, None, st)
     else:
         call("dsv41_index_score", ptr(qc), H * D, ptr(w), H, b * s, H, D, 0, ptr(index_k), index_k.stride(0), None, 0,
-             None, s, None, start_pos, ratio, T, 1, ptr(score), T, None, st)
+             None, s, None, start_pos, ratio, T, 0, ptr(score), T, None, st)
     call("dsv41_topk_indices", ptr(score), T, b * s, T, kk, None, start_pos, ratio, s, int(offset), ptr(out), kk, st)
-    if return_score:
+    if return_score:  # positions at or past a row's causal limit are not written (the top-k never reads them)
         return out, score.view(b, s, T)
     return out

@@ -118,3 +118,47 @@ def make_decode_inputs(cfg: DecodeConfig, device, seed: int = 0, cache_copies: i
         pmax=torch.tensor(pmax, dtype=torch.int64, device=device),
     )
     return layers, step
+
+
+@dataclass
+class PrefillConfig:
+    name: str = "C3"
+    chunk: int = 2048        # query tokens in the chunk
+    prior: int = 65536       # tokens before the chunk
+    ratio: int = 4
+    topk: int = 2048
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def end(self):
+        return self.prior + self.chunk
+
+    @property
+    def n_c(self):  # compressed rows visible to the last query
+        return self.end // self.ratio
+
+
+PREFILL = {"C3": PrefillConfig()}
+
+
+def make_prefill_inputs(cfg: PrefillConfig, device, seed: int = 1):
+    """One layer's chunked-prefill inputs: queries, index queries/weights, the compressed-KV table and e4m3 index keys
+    covering the prior context plus the chunk's own groups, the SWA history + chunk rows, and the per-query index
+    lists in the reference's layout (window indices into [history | chunk] followed by compressed indices + offset,
+    dsv41/model.py:1442-1443)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    S, T = cfg.chunk, cfg.n_c
+    hist = min(cfg.prior, WIN - 1)
+    q = (torch.randn(1, S, H, DQK, generator=g, device=device) * 0.1).to(torch.bfloat16)
+    q_idx = fp4_round(torch.randn(1, S, HI, DI, generator=g, device=device))
+    w_idx = (torch.randn(1, S, HI, generator=g, device=device) * (DI ** -0.5 * HI ** -0.5)).to(torch.bfloat16)
+    kk = torch.randn(1, T, DI, generator=g, device=device) * 0.1
+    kk[..., list(OUTLIER_CH)] *= 8
+    kbf = fp4_round(kk)
+    k8, ks = encode_e4m3_rows(kbf)
+    ckv = (torch.randn(1, T, DQK, generator=g, device=device) * 0.1).to(torch.bfloat16)
+    win = (torch.randn(1, hist + S, DQK, generator=g, device=device) * 0.1).to(torch.bfloat16)
+    qq = hist + torch.arange(S, device=device).unsqueeze(1)
+    widx = (qq - WIN + 1).clamp_min(0) + torch.arange(WIN, device=device).unsqueeze(0)
+    widx = torch.where(widx <= qq, widx, -1).to(torch.int32).unsqueeze(0)
+    return dict(q=q, q_idx=q_idx, w_idx=w_idx, kbf=kbf, k8=k8, ks=ks, ckv=ckv, win=win, widx=widx, hist=hist)

@@ -419,3 +419,40 @@ def test_decode_selector_end_to_end(cls):
             continue
         err = np.abs(sc[b, :c] - want[b, :c]).max() / np.abs(want[b, :c]).max()
         assert err <= 1e-2, (b, err)
+
+
+def test_topk_many_rows_bit_exact():
+    """Prefill-shaped selection (many rows of <= 17408 positions: the 256-thread top-k), causal limits per row."""
+    import dsv41_amd
+    from dsv41_amd._lib import call, ptr
+    r = rng(16)
+    R, n, k = 600, 16896, 2048
+    sc = r.standard_normal((R, n)).astype(np.float32)
+    sc[::7] = np.round(sc[::7] * 3) / 3  # tie-heavy rows
+    start, ratio = 65536 - 4 * 600 + 4 * 16896 - 65536, 4  # rows see (start + i + 1) // 4 positions
+    cls = [(start + i + 1) // ratio for i in range(R)]
+    out = torch.empty(R, k, dtype=torch.int32, device=DEV)
+    call("dsv41_topk_indices", ptr(f32(sc)), n, R, n, k, None, start, ratio, R, 7, ptr(out), k,
+         torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    want = O.topk_indices(sc, k, cls)
+    np.testing.assert_array_equal(out.cpu().numpy(), np.where(want >= 0, want + 7, -1))
+
+
+@pytest.mark.parametrize("dqk,dv,h", [(576, 512, 64), (512, 512, 64), (576, 512, 40)])
+def test_sparse_attn_prefill_shape(dqk, dv, h):
+    """Many query rows (the prefill kernel): per-query index lists of window rows + compressed rows with -1 holes
+    and out-of-range entries, against the reference's prefill rounding (bf16 QK and PV einsums)."""
+    import dsv41_amd
+    r = rng(17)
+    b, s, n, t = 1, 320, 3000, 700
+    q = O.bf16(r.standard_normal((b, s, h, dqk)).astype(np.float32))
+    kv = O.bf16(r.standard_normal((b, n, dqk)).astype(np.float32) * 0.1)
+    sink = r.standard_normal(h).astype(np.float32)
+    idx = r.integers(0, n, (b, s, t)).astype(np.int32)
+    idx[:, ::3, 100:180] = -1
+    idx[:, 5, :] = -1  # a query with no valid key: output 0
+    idx[:, 7, 3] = n + 11
+    scale = dqk ** -0.5
+    o = host(dsv41_amd.sparse_attn(bf(q), bf(kv), f32(sink), torch.from_numpy(idx).to(DEV), scale, d_v=dv))
+    attn_close(o, O.sparse_attn(q, kv, sink, idx, scale, dv=dv), f"prefill {dqk}/{dv} h={h}")
