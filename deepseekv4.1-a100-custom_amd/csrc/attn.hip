@@ -293,6 +293,7 @@ DSV41_DEV uint2 lds_read_tr16(const uint16_t* p) {
 // limits, and the final normalisation uses the same reference, so the result is the exact softmax.
 template <int DQK, int DV>
 __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
+  DSV41_WG_TS(0);
   constexpr int KS = DQK / 32;
   constexpr int CTH = DV / 32;  // 16-column output tiles per wave (half of DV)
   constexpr int U = DQK / 8;    // 16-byte chunks per row; chunk c of row j stored at j*U + (c ^ (j & 7))
@@ -518,6 +519,7 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
     }
   }
   DSV41_TS(22);
+  DSV41_WG_TS(1);
 }
 
 // ------------------------------------------------------------------------------------------------ prefill kernel
@@ -880,6 +882,7 @@ extern "C" {
 
 #ifdef DSV41_TIMING
 int dsv41_read_ts_attn(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
+int dsv41_read_wg_attn(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_wg), sizeof(g_dsv41_wg)); }
 #endif
 
 

@@ -109,9 +109,19 @@ __device__ long long g_dsv41_ts[64];
   do {                                                                                                    \
     if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) g_dsv41_ts[i] = wall_clock64(); \
   } while (0)
+// Per-workgroup start / end stamps (first 4096 workgroups of a launch, linear block id).
+__device__ long long g_dsv41_wg[4096][2];
+#define DSV41_WG_TS(k)                                                                                     \
+  do {                                                                                                     \
+    const int _b = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);                         \
+    if (threadIdx.x == 0 && _b < 4096) g_dsv41_wg[_b][k] = wall_clock64();                                 \
+  } while (0)
 #else
 #define DSV41_TS(i) \
   do {              \
+  } while (0)
+#define DSV41_WG_TS(k) \
+  do {                 \
   } while (0)
 #endif
 

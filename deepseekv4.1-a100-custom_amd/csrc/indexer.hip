@@ -81,6 +81,7 @@ DSV41_DEV float score_tile(const i32x8_t (&qa8)[kHT], const uint4 (&qa16)[kHT][4
 template <int KFMT, bool HIST>
 __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
   DSV41_TS(30);
+  DSV41_WG_TS(0);
   __shared__ int lhist[HIST ? kHistBins : 1];
   const int r = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -184,6 +185,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
       if (v) atomicAdd(&gh[i], v);
     }
   }
+  DSV41_WG_TS(1);
 }
 
 // Prefill score kernel (many query rows of one sequence; e4m3 keys + prepared e4m3 queries): a workgroup owns 8
@@ -582,6 +584,7 @@ extern "C" {
 
 #ifdef DSV41_TIMING
 int dsv41_read_ts_idx(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
+int dsv41_read_wg_idx(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_wg), sizeof(g_dsv41_wg)); }
 #endif
 
 
