@@ -94,7 +94,7 @@ def run_decode(args, dev):
     torch.cuda.synchronize(dev)
 
     # ---- per-phase durations (eager, events around each launch on the launch stream): appends (1 kernel),
-    # index_score (the score kernel alone), topk (select + finalize), sattn (attention + combine)
+    # index_score (the score kernel alone), topk (selection), sattn (attention, splits merged in-kernel)
     E = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     phases = {"appends": [], "index_score": [], "topk": [], "sattn": []}
     reps = max(2, min(args.steps, 20))
@@ -112,8 +112,9 @@ def run_decode(args, dev):
             ev[2].record(stream)
             idx = sel.select(cl)
             ev[3].record(stream)
+            ws = lay.attn_workspace(st["q"].shape[0], st["q"].shape[2], lay.ring.shape[1] + idx.shape[-1], dev)
             o = sattn2(st["q"], lay.ring, lay.ckv, idx, pos, lay.sink, lay.cos, lay.sin, 0, lay.scale, seq, pmax,
-                       plim=pos, d_v=512)
+                       plim=pos, d_v=512, ws=ws)
             ev[4].record(stream)
             torch.cuda.synchronize(dev)
             for i, k in enumerate(phases):

@@ -48,6 +48,9 @@ struct AttnArgs {
   float* pm;  // [R, H, nsplit]
   float* pl;
   float* pacc;  // [R, H, nsplit, DV]
+  int* arrive;  // decode kernel: [R * head groups] split arrival counters (zero between launches), or null
+  int units;    // with arrive: (row, 16-head group) units, placed upx per XCD (1-D grid of kXcds * upx * nsplit)
+  int upx;
   const float* cos_t;
   const float* sin_t;
   int rd;
@@ -286,6 +289,73 @@ DSV41_DEV uint2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
+// Merge the split partials of heads h0..h0+15 of row r (512 threads, nsplit <= 32): weights w_s = l_s e^(m_s - M)
+// normalised by sum_s w_s + e^(sink - M), then out = sum_s w_s o_s (o_s bf16-normalised), bf16 round, inverse rope
+// on the last rd columns.
+template <int DV>
+DSV41_DEV void merge_splits(const AttnArgs& a, int r, int h0, long pr, float (*wts)[33]) {
+  const int tid = threadIdx.x, H = a.H, ns = a.nsplit;
+  {
+    const int hh = tid >> 5, sp = tid & 31, h = h0 + hh;
+    const bool ok = h < H && sp < ns;
+    const long pi = ((long)r * H + h) * ns + sp;
+    // pm/pl lines can hold entries of other units: agent-scope loads do not use the CU cache
+    const float m = ok ? __hip_atomic_load(a.pm + pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -1e30f;
+    const float l = ok ? __hip_atomic_load(a.pl + pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+    float M = m;
+#pragma unroll
+    for (int d = 1; d < 32; d <<= 1) M = fmaxf(M, __shfl_xor(M, d, 64));
+    const float w = ok ? l * exp2f((m - M) * kLog2e) : 0.0f;
+    float den = w;
+#pragma unroll
+    for (int d = 1; d < 32; d <<= 1) den += __shfl_xor(den, d, 64);
+    den += exp2f((a.sink[h < H ? h : H - 1] - M) * kLog2e);
+    wts[hh][sp] = w / den;
+  }
+  __syncthreads();
+  const uint16_t* pb = (const uint16_t*)a.pacc;
+  constexpr int CG = DV / 8;  // 8-column groups per head
+#pragma unroll 1
+  for (int e = tid; e < 16 * CG; e += 512) {
+    const int hh = e / CG, c = (e - hh * CG) * 8, h = h0 + hh;
+    if (h >= H) continue;
+    const long base = ((long)r * H + h) * ns;
+    float num[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll 1
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      uint4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = *(const uint4*)(pb + (base + min(s0 + u, ns - 1)) * DV + c);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float wg = s0 + u < ns ? wts[hh][s0 + u] : 0.0f;
+        const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          num[2 * q] += wg * __uint_as_float(vv[q] << 16);
+          num[2 * q + 1] += wg * __uint_as_float(vv[q] & 0xffff0000u);
+        }
+      }
+    }
+    uint32_t pk[4];
+#pragma unroll
+    for (int q = 0; q < 8; q += 2) {
+      float re = round_bf16(num[q]), im = round_bf16(num[q + 1]);
+      const int cc = c + q;
+      if (a.rd > 0 && cc >= DV - a.rd) {
+        const int jj = (cc - (DV - a.rd)) >> 1;
+        const float cs = a.cos_t[pr * (a.rd / 2) + jj];
+        const float sn = -a.sin_t[pr * (a.rd / 2) + jj];
+        const float yr = re * cs - im * sn, yi = re * sn + im * cs;
+        re = yr;
+        im = yi;
+      }
+      pk[q / 2] = pack_bf16x2(re, im);
+    }
+    *(uint4*)(a.out + (long)r * a.out_rstride + (long)h * DV + c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  }
+}
+
 // Decode attention, 8 waves per workgroup (2 per SIMD): wave w handles key rows 16*(w&3)..+15 of every 64-key tile
 // and output columns [(w>>2)*DV/2, +DV/2) (QK^T and the softmax are computed by both column halves, identically).
 // The softmax keeps a reference maximum per head and rescales the accumulators only when the tile maximum exceeds
@@ -307,7 +377,22 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   __shared__ float wm[4][16], wl[4][16];
 
   DSV41_TS(10);
-  const int sp = blockIdx.x, hg = blockIdx.y, r = blockIdx.z;
+  DSV41_PH(0);
+  int sp, hg, r, home = -1;
+  if (a.arrive) {  // the nsplit workgroups of a unit share XCD `home` and merge through its L2
+    const int x = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+    const int unit = x * a.upx + j / a.nsplit;
+    if (unit >= a.units) return;
+    const int HG = (a.H + 15) / 16;
+    sp = j % a.nsplit;
+    hg = unit % HG;
+    r = unit / HG;
+    home = x;
+  } else {
+    sp = blockIdx.x;
+    hg = blockIdx.y;
+    r = blockIdx.z;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rw = wave & 3, half = wave >> 2;
   const int l16 = lane & 15, g = lane >> 4;
@@ -327,8 +412,9 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   const uint16_t* base1 = a.kv1 + slot * a.kv1_sstride;
   const uint16_t* base2 = a.kv2 ? a.kv2 + slot * a.kv2_sstride : nullptr;
   const int* irow = a.t > 0 ? a.idx + (long)r * a.idx_rstride : nullptr;
-  const int j0 = sp * a.chunk;
-  const int j1 = min(a.L, j0 + a.chunk);
+  const int all_tiles = (a.L + TILE - 1) / TILE;  // split sp takes tiles [sp*T/ns, (sp+1)*T/ns)
+  const int j0 = (int)((long)sp * all_tiles / a.nsplit) * TILE;
+  const int j1 = min(a.L, (int)((long)(sp + 1) * all_tiles / a.nsplit) * TILE);
   const int ntiles = (j1 - j0 + TILE - 1) / TILE;
 
   auto resolve = [&](int ti) {  // threads 0..63: row pointer of key position j0 + ti*TILE + tid
@@ -378,6 +464,7 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   }
   __syncthreads();
   DSV41_TS(11);
+  DSV41_PH(1);
   issue(0);
 
   float m_ref = -1e30f, l_run = 0.0f;  // per head (lane's head l16), log2 units
@@ -453,6 +540,7 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   }
   __syncthreads();
   DSV41_TS(20);
+  DSV41_PH(2);
 
   // ---- merge the 4 row-waves' states per head (both column halves hold identical m, l)
   if (half == 0 && g == 0) {
@@ -519,6 +607,25 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
     }
   }
   DSV41_TS(22);
+  DSV41_PH(3);
+  if (final_out || !a.arrive) {
+    DSV41_WG_TS(1);
+    return;
+  }
+  // ---- the last split workgroup of the unit to finish merges all splits' partials
+  __shared__ int s_slot;
+  __shared__ float wts[16][33];
+  int* cnt = a.arrive + (long)r * ((H + 15) / 16) + hg;
+  const int old = group_arrive(cnt, home, &s_slot);
+  if ((old & (kMisplaced - 1)) != a.nsplit - 1) {
+    DSV41_WG_TS(1);
+    return;
+  }
+  DSV41_PH(4);
+  group_acquire(old, home);
+  if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  merge_splits<DV>(a, r, h0, pr, wts);
+  DSV41_PH(5);
   DSV41_WG_TS(1);
 }
 
@@ -794,10 +901,10 @@ bool use_decode_kernel(int R, int H) { return (long)R * ((H + 63) / 64) < 128; }
 template <int DQK, int DV>
 int launch_attn(AttnArgs& a, hipStream_t st) {
   if (use_decode_kernel(a.R, a.H)) {
-    dim3 grid(a.nsplit, (a.H + 15) / 16, a.R);
+    const dim3 grid = a.arrive ? dim3(kXcds * a.upx * a.nsplit) : dim3(a.nsplit, (a.H + 15) / 16, a.R);
     attn_decode_kernel<DQK, DV><<<grid, 512, 0, st>>>(a);
     DSV41_CHECK_LAUNCH();
-    if (a.nsplit > 1) {
+    if (a.nsplit > 1 && !a.arrive) {
       attn_decode_combine_kernel<DV><<<dim3((a.H + 3) / 4, a.R), 256, 0, st>>>(a);
       DSV41_CHECK_LAUNCH();
     }
@@ -838,10 +945,14 @@ void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
   if (want > 0) {
     per = (tiles + want - 1) / want;
   } else if (dec) {
+    // ~256 workgroups, >= 2 tiles per split; the decode kernel balances the tiles over the splits
     const long wgs = (long)R * ((H + 15) / 16);
-    const long target = wgs >= 256 ? 1 : (256 + wgs - 1) / wgs;
-    per = (int)((tiles + target - 1) / target);
-    if (per < 2) per = 2;
+    const int cap = tiles / 2 < 1 ? 1 : tiles / 2;
+    int ns = (int)(wgs >= 256 ? 1 : (256 + wgs - 1) / wgs);
+    if (ns > cap) ns = cap;
+    *nsplit = ns;
+    *chunk = (tiles + ns - 1) / ns * tile;
+    return;
   } else {
     const long wgs = (long)R * ((H + 63) / 64);
     const long target = wgs >= 256 ? 1 : (512 + wgs - 1) / wgs;
@@ -854,9 +965,16 @@ void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
   *nsplit = (tiles + per - 1) / per;
 }
 
+// The decode kernel merges its own splits (XCD-local units) when there are enough units to occupy every XCD.
+constexpr int kFuseMaxSplits = 32;
+bool fuse_merge(int R, int H, int ns) { return ns > 1 && ns <= kFuseMaxSplits && (long)R * ((H + 15) / 16) >= kXcds; }
+
 long workspace_bytes(int R, int H, int ns, int dv) {
   if (ns <= 1) return 0;
-  if (use_decode_kernel(R, H)) return (long)R * H * ns * (8 + 2L * dv);
+  if (use_decode_kernel(R, H)) {  // m, l (fp32), bf16 partials, then the arrival counters
+    const long part = (long)R * H * ns * (8 + 2L * dv);
+    return fuse_merge(R, H, ns) ? part + (long)R * ((H + 15) / 16) * 4 : part;
+  }
   return (long)R * H * ns * (2 + dv) * 4;
 }
 
@@ -872,6 +990,11 @@ int finish_plan(AttnArgs& a, int want_nsplit, void* ws, long ws_bytes, int dv) {
     a.pm = f;
     a.pl = f + (long)a.R * a.H * ns;
     a.pacc = f + 2L * a.R * a.H * ns;
+    if (use_decode_kernel(a.R, a.H) && fuse_merge(a.R, a.H, ns)) {
+      a.arrive = (int*)((char*)ws + (long)a.R * a.H * ns * (8 + 2L * dv));
+      a.units = a.R * ((a.H + 15) / 16);
+      a.upx = (a.units + kXcds - 1) / kXcds;
+    }
   }
   return 0;
 }
@@ -882,6 +1005,7 @@ extern "C" {
 
 #ifdef DSV41_TIMING
 int dsv41_read_ts_attn(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
+int dsv41_read_ph_attn(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ph), sizeof(g_dsv41_ph)); }
 int dsv41_read_wg_attn(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_wg), sizeof(g_dsv41_wg)); }
 #endif
 

@@ -116,7 +116,20 @@ __device__ long long g_dsv41_wg[4096][2];
     const int _b = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);                         \
     if (threadIdx.x == 0 && _b < 4096) g_dsv41_wg[_b][k] = wall_clock64();                                 \
   } while (0)
+// Per-workgroup phase stamps (1-D grids, first 1024 workgroups).
+__device__ long long g_dsv41_ph[1024][8];
+__device__ long long g_dsv41_ck[1024][8];  // shader clock at the same points
+#define DSV41_PH(k)                                                  \
+  do {                                                               \
+    if (threadIdx.x == 0 && blockIdx.x < 1024) {                     \
+      g_dsv41_ph[blockIdx.x][k] = wall_clock64();                    \
+      g_dsv41_ck[blockIdx.x][k] = clock64();                         \
+    }                                                                \
+  } while (0)
 #else
+#define DSV41_PH(k) \
+  do {              \
+  } while (0)
 #define DSV41_TS(i) \
   do {              \
   } while (0)
@@ -124,6 +137,74 @@ __device__ long long g_dsv41_wg[4096][2];
   do {                 \
   } while (0)
 #endif
+
+// ---- scans
+// Inclusive prefix sum over the 64 lanes of a wave with DPP lane moves (no LDS traffic): shifts of 1, 2, 4, 8
+// within each row of 16 lanes, then the row totals are carried by row_bcast:15 (into rows 1, 3) and row_bcast:31
+// (into rows 2, 3).  Lanes a move does not reach add 0.
+DSV41_DEV int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
+}
+
+// Exclusive prefix sum over the NT threads of a workgroup (tmp: NT/64 ints), with the workgroup total; two barriers.
+template <int NT>
+DSV41_DEV int block_scan_dpp(int v, int* tmp, int* total) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int x = wave_incl_scan(v);
+  if (lane == 63) tmp[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int s = tmp[w];
+    before += w < wave ? s : 0;
+    all += s;
+  }
+  *total = all;
+  __syncthreads();
+  return before + x - v;
+}
+
+// ---- workgroup groups that exchange data through one XCD's L2
+// The 8 XCDs of an MI355X each have their own L2; a device-scope release/acquire writes back / invalidates a whole
+// L2, which costs tens of microseconds when every workgroup of a launch does it.  Workgroups that cooperate are
+// therefore placed on one XCD (workgroups of a 1-D grid are dealt to the XCDs round-robin: workgroup b runs on XCD
+// b % 8), where the shared L2 makes their stores visible to each other once they have left the CU (the CU caches are
+// write-through, and only lines read after the exchange are cached).  Each workgroup checks its hardware XCD id;
+// one that finds itself elsewhere publishes with a device-scope fence and flags the group, and a reader that sees
+// the flag (or is misplaced itself) acquires with a device-scope fence, so results never depend on the placement.
+constexpr int kXcds = 8;
+constexpr int kMisplaced = 1 << 16;  // flag added to a group arrival counter by a misplaced workgroup
+
+DSV41_DEV int xcd_id() { return __builtin_amdgcn_s_getreg(0x1814) & 15; }  // hwreg(HW_REG_XCC_ID, 0, 4)
+
+// Arrive at the group counter after this workgroup's stores (call from every thread); returns the previous counter
+// value to every thread.  `home` is the XCD the group was placed on.
+DSV41_DEV int group_arrive(int* counter, int home, int* s_slot) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have reached the L2
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool away = xcd_id() != home;
+    if (away) __threadfence();
+    *s_slot = __hip_atomic_fetch_add(counter, away ? 1 + kMisplaced : 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  return *s_slot;
+}
+
+// After the group is complete (`seen` = a counter value that includes every member): make the members' stores
+// visible to this workgroup's loads.  Call from every thread; ends with a barrier.
+DSV41_DEV void group_acquire(int seen, int home) {
+  if (threadIdx.x == 0 && (seen >= kMisplaced || xcd_id() != home)) __threadfence();
+  __syncthreads();
+}
 
 #define DSV41_CHECK_LAUNCH()                          \
   do {                                                \

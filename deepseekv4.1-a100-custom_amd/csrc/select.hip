@@ -29,9 +29,10 @@ struct SelArgs {
   int n, k, R;
   int* hist;         // [R, kBins]
   int* counts;       // [R, nchunks, 2]
-  int* above;        // [R, n]   (chunk-owned regions)
-  int* cand_idx;     // [R, n]
-  uint32_t* cand_key;  // [R, n]
+  int* above;        // [R, rs]   (chunk-owned regions; rs = n rounded up to 32: rows never share a cache line)
+  int* cand_idx;     // [R, rs]
+  uint32_t* cand_key;  // [R, rs]
+  long rs;
   int nchunks;
   int* out;          // [R, k]
   long out_rstride;
@@ -156,7 +157,7 @@ __global__ void __launch_bounds__(256) select_chunks_kernel(const SelArgs a) {
     cnt[0] = wa[0] + wa[1] + wa[2] + wa[3];
     cnt[1] = wc[0] + wc[1] + wc[2] + wc[3];
   }
-  const long reg = (long)r * a.n + (long)ch * kChunk;
+  const long reg = (long)r * a.rs + (long)ch * kChunk;
   const unsigned long long lt = (1ull << lane) - 1ull;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -218,7 +219,7 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
   DSV41_TS(2);
   const int need = k - tot_a;  // candidates to take (1 <= need <= tot_c)
   const bool staged = tot_c <= kCandCap;
-  const long reg = (long)r * a.n;
+  const long reg = (long)r * a.rs;
   // ---- stage candidates (index order) and mark the above positions: flat loops, every load independent
   auto chunk_of = [&](const int* pre, int j) {  // last chunk q with pre[q] <= j
     int lo = 0, hi = nch - 1;
@@ -333,17 +334,326 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
   for (int i = tid; i < kBins; i += kFinThreads) gh[i] = 0;
 }
 
+// ------------------------------------------------------------------------------------------------ one launch
+// Rows of at most kGroupPerXcd chunks: the chunks of a row form one group of workgroups on one XCD (row r on XCD
+// r / rpx; workgroup b runs on XCD b % 8), all resident at once, that meet once at a per-row barrier:
+//   A. scores of the chunk (4 positions per thread), the row's histogram and length: one round trip
+//   B. threshold bin B (where the running count from the top reaches k); need = k - (entries above B)
+//   C. classify: entries above B are counted; bin-B candidates are stored as key << 32 | ~position (a larger value
+//      is the better candidate: higher key, then lower position) in the chunk's slot region, with the counts
+//   D. barrier: a 64-bit arrival counter per row that only grows (launch e waits for (e + 1) * slots arrivals)
+//   E. the counts of every chunk and the first kGroupSpec candidates of each chunk in one round trip
+//   F. unless all of bin B is taken: T = the candidate of rank need - 1 (rank = candidates larger than it)
+//   G. the chunk's taken positions (above B, or candidates >= T) at offset sum over earlier chunks of
+//      (above + taken candidates) plus the in-chunk prefix.
+// A workgroup that finds itself off its XCD publishes with a device-scope fence and adds kAwayFlag to its arrival;
+// readers that see any such flag (or are misplaced themselves) acquire with a device-scope fence, so results never
+// depend on placement (a workspace that ever saw a misplaced workgroup keeps taking the fenced exchange).
+constexpr int kGroupPerXcd = 64;   // 2 per CU of a 32-CU XCD: every chunk of a row is resident at the barrier
+constexpr int kGroupSpec = 32;     // candidates per chunk read together with the counts
+constexpr int kGroupCand = 2048;   // candidates staged in LDS (more: read from the workspace)
+constexpr int kRankDirect = 64;    // up to this many candidates: direct ranks; more: radix passes
+constexpr int kSpinLimit = 1 << 22;
+constexpr unsigned long long kAwayFlag = 1ull << 48, kArriveMask = kAwayFlag - 1;
+
+struct GroupArgs {
+  SelArgs s;
+  unsigned long long* cand;   // [R, rs] (chunk ch: slots ch * kChunk ..)
+  unsigned long long* epoch;  // [R] arrival counters (bits 0..47: arrivals; 48..: misplaced arrivals)
+  int* err;                   // set when a barrier wait gives up (kSpinLimit polls)
+  int rpx;                    // rows per XCD
+};
+
+__global__ void __launch_bounds__(256) select_group_kernel(const GroupArgs g) {
+  const SelArgs& a = g.s;
+  const int home = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+  const int ch = j % a.nchunks, r = home * g.rpx + j / a.nchunks;
+  if (r >= a.R) return;
+  __shared__ int tmp[4];
+  __shared__ int s_bin, s_need, s_cnt, s_selb;
+  __shared__ int wcnt[4][2];
+  __shared__ int pc[kGroupPerXcd + 1];
+  __shared__ int na_q[kGroupPerXcd], nc_q[kGroupPerXcd];
+  __shared__ unsigned long long lc[kGroupCand + 2];  // (+ a zero pad after the last candidate)
+  __shared__ int rh[1024];
+  __shared__ int s_over, s_digit, s_rem, s_eq;
+  __shared__ unsigned long long s_T, s_ep;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int nslots = a.nchunks;
+  DSV41_PH(0);
+  // ---- A. loads
+  const long cl = a.cl[r];
+  const int p = ch * kChunk + 4 * t;
+  const float4 v = p < a.n ? *(const float4*)(a.score + (long)r * a.ld + p) : make_float4(0.f, 0.f, 0.f, 0.f);
+  int* gh = a.hist + (long)r * kBins;
+  int4 h4[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) h4[u] = *(const int4*)(gh + kBins - 16 * (t + 1) + 4 * u);
+  const int c = (int)(cl < 0 ? 0 : (cl > a.n ? a.n : cl)), k = a.k;
+  int* orow = a.out + (long)r * a.out_rstride;
+  unsigned long long* ep = g.epoch + r;
+  const int zb = (kBins + nslots - 1) / nslots, z0 = ch * zb, z1 = min(kBins, z0 + zb);  // histogram slice to clear
+  if (c <= k) {  // everything is selected; arrive without waiting (keeps the epoch count)
+    if (ch == 0) {
+#pragma unroll 1
+      for (int i = t; i < k; i += 256) orow[i] = i < c ? i + a.offset : -1;
+    }
+#pragma unroll 1
+    for (int i = z0 + t; i < z1; i += 256) gh[i] = 0;
+    if (t == 0) __hip_atomic_fetch_add(ep, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  // ---- B. threshold bin (thread t: bins 4095-16t down to 4080-16t)
+  if (t == 0) {  // (a histogram holding fewer than k entries of a row longer than k is a caller error)
+    s_bin = 0;
+    s_need = k;
+    s_cnt = 0;
+  }
+  {
+    const int h[16] = {h4[3].w, h4[3].z, h4[3].y, h4[3].x, h4[2].w, h4[2].z, h4[2].y, h4[2].x,
+                       h4[1].w, h4[1].z, h4[1].y, h4[1].x, h4[0].w, h4[0].z, h4[0].y, h4[0].x};
+    int local = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) local += h[i];
+    int total;
+    int above = block_scan_dpp<256>(local, tmp, &total);
+    if (above < k && k <= above + local) {
+#pragma unroll 1
+      for (int i = 0; i < 16; ++i) {
+        if (k <= above + h[i]) {
+          s_bin = kBins - 1 - 16 * t - i;
+          s_need = k - above;
+          s_cnt = h[i];
+          break;
+        }
+        above += h[i];
+      }
+    }
+    __syncthreads();
+  }
+  DSV41_PH(1);
+  const uint32_t lo = (uint32_t)s_bin << 20, hi = (uint32_t)(s_bin + 1) << 20;  // bin B = [lo, hi)
+  const int need = s_need, cnt = s_cnt;
+  // ---- C. classify
+  const uint32_t key[4] = {score_key(v.x), score_key(v.y), score_key(v.z), score_key(v.w)};
+  int na = 0, nc = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const bool ok = p + e < c;
+    na += ok && key[e] >= hi;
+    nc += ok && key[e] >= lo && key[e] < hi;
+  }
+  const int ia = wave_incl_scan(na), ic = wave_incl_scan(nc);
+  if (lane == 63) {
+    wcnt[wave][0] = ia;
+    wcnt[wave][1] = ic;
+  }
+  __syncthreads();
+  int cbase = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) cbase += w < wave ? wcnt[w][1] : 0;
+  unsigned long long* crow = g.cand + (long)r * a.rs;
+  if (nc > 0) {
+    int o = ch * kChunk + cbase + ic - nc;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (p + e < c && key[e] >= lo && key[e] < hi)
+        crow[o++] = (unsigned long long)key[e] << 32 | (uint32_t)~(uint32_t)(p + e);
+  }
+  if (t == 0) {
+    const int ta = wcnt[0][0] + wcnt[1][0] + wcnt[2][0] + wcnt[3][0];
+    const int tc = wcnt[0][1] + wcnt[1][1] + wcnt[2][1] + wcnt[3][1];
+    *(int2*)(a.counts + ((long)r * nslots + ch) * 2) = make_int2(ta, tc);
+  }
+  // ---- D. row barrier
+  DSV41_PH(2);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) {
+    const bool away = xcd_id() != home;
+    if (away) __threadfence();
+    const unsigned long long old =
+        __hip_atomic_fetch_add(ep, away ? 1ull + kAwayFlag : 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long target = ((old & kArriveMask) / nslots + 1) * nslots;
+    unsigned long long cur;
+    int spins = 0;
+    while (((cur = __hip_atomic_load(ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) & kArriveMask) < target &&
+           spins < kSpinLimit) {
+      __builtin_amdgcn_s_sleep(2);
+      ++spins;
+    }
+    if (spins >= kSpinLimit) __hip_atomic_store(g.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (away || cur >= kAwayFlag) __threadfence();  // some workgroup of this workspace ever ran off its XCD
+  }
+  __syncthreads();
+  DSV41_PH(3);
+  // the histogram is consumed (every chunk read it before arriving)
+#pragma unroll 1
+  for (int i = z0 + t; i < z1; i += 256) gh[i] = 0;
+  // ---- E. counts of all chunks + speculative candidate prefixes
+  if (t < nslots) {
+    const long long cv = __hip_atomic_load((long long*)(a.counts + ((long)r * nslots + t) * 2), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    na_q[t] = (int)(cv & 0xffffffff);
+    nc_q[t] = (int)(cv >> 32);
+  }
+  constexpr int kSpecPer = kGroupPerXcd * kGroupSpec / 256;
+  unsigned long long sv[kSpecPer];
+#pragma unroll
+  for (int u = 0; u < kSpecPer; ++u) {
+    const int idx = u * 256 + t, q = idx / kGroupSpec, e = idx % kGroupSpec;
+    sv[u] = q < nslots ? crow[q * kChunk + e] : 0ull;
+  }
+  __syncthreads();
+  if (wave == 0) {  // prefix of the candidate counts; entries above B in earlier chunks; largest chunk count
+    const int x = lane < nslots ? nc_q[lane] : 0;
+    const int ix = wave_incl_scan(x);
+    pc[lane + 1] = ix;
+    if (lane == 0) pc[0] = 0;
+    const int y = lane < ch ? na_q[lane] : 0;
+    const int iy = wave_incl_scan(y);
+    if (lane == 63) s_selb = iy;
+    const bool over = __ballot(x > kGroupSpec) != 0;
+    if (lane == 0) s_over = over;
+    const int mtot = __shfl(ix, 63, 64);
+    if (lane == 0 && mtot <= kGroupCand) lc[mtot] = 0ull;  // pad for pairwise reads
+  }
+  __syncthreads();
+  const int m = pc[nslots];
+  const bool staged = m <= kGroupCand;
+#pragma unroll
+  for (int u = 0; u < kSpecPer; ++u) {
+    const int idx = u * 256 + t, q = idx / kGroupSpec, e = idx % kGroupSpec;
+    if (staged && q < nslots && e < nc_q[q]) lc[pc[q] + e] = sv[u];
+  }
+  if (staged && s_over) {  // chunks with more than kGroupSpec candidates
+#pragma unroll 1
+    for (int q = 0; q < nslots; ++q)
+      for (int e = kGroupSpec + t; e < nc_q[q]; e += 256) lc[pc[q] + e] = crow[q * kChunk + e];
+  }
+  __syncthreads();
+  auto cand_at = [&](int i) -> unsigned long long {
+    if (staged) return lc[i];
+    int q = 0;
+    while (pc[q + 1] <= i) ++q;
+    return crow[q * kChunk + (i - pc[q])];
+  };
+  DSV41_PH(4);
+  // ---- F. threshold candidate
+  if (t == 0) s_T = 0ull;  // every candidate is taken
+  __syncthreads();
+  if (cnt != need || m != need) {
+    if (staged && m <= kRankDirect) {  // direct ranks, two candidates per LDS read
+      const uint4* l4 = (const uint4*)lc;
+      const int m2 = (m + 1) / 2;
+#pragma unroll 1
+      for (int i = t; i < m; i += 256) {
+        const unsigned long long me = lc[i];
+        int rk = 0;
+#pragma unroll 8
+        for (int q = 0; q < m2; ++q) {
+          const uint4 w = l4[q];
+          rk += ((unsigned long long)w.y << 32 | w.x) > me;
+          rk += ((unsigned long long)w.w << 32 | w.z) > me;
+        }
+        if (rk == need - 1) s_T = me;
+      }
+    } else {
+      // two 10-bit histogram passes over key bits 19..10 and 9..0 give the exact key Tk and the number rem of
+      // candidates with key Tk that are taken; among those, the one whose position ranks rem - 1 is T
+      uint32_t prefix = lo, mask = 0xfff00000u;
+      int rem = need;
+#pragma unroll 1
+      for (int pass = 0; pass < 2; ++pass) {
+        const int shift = pass == 0 ? 10 : 0;
+        *(int4*)(rh + 4 * t) = make_int4(0, 0, 0, 0);
+        __syncthreads();
+#pragma unroll 1
+        for (int i = t; i < m; i += 256) {
+          const uint32_t kk = (uint32_t)(cand_at(i) >> 32);
+          if ((kk & mask) == prefix) atomicAdd(&rh[(kk >> shift) & 1023], 1);
+        }
+        __syncthreads();
+        const int4 hv = *(const int4*)(rh + 1020 - 4 * t);  // digits 1023-4t .. 1020-4t
+        const int h[4] = {hv.w, hv.z, hv.y, hv.x};
+        int tot;
+        int greater = block_scan_dpp<256>(h[0] + h[1] + h[2] + h[3], tmp, &tot);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (greater < rem && rem <= greater + h[i]) {
+            s_digit = 1023 - 4 * t - i;
+            s_rem = rem - greater;
+            s_eq = h[i];
+          }
+          greater += h[i];
+        }
+        __syncthreads();
+        prefix |= (uint32_t)s_digit << shift;
+        mask |= 1023u << shift;
+        rem = s_rem;
+      }
+      if (t == 0 && s_eq == rem) s_T = (unsigned long long)prefix << 32;  // every candidate with key Tk is taken
+#pragma unroll 1
+      for (int i = t; i < m && s_eq != rem; i += 256) {
+        const unsigned long long me = cand_at(i);
+        if ((uint32_t)(me >> 32) != prefix) continue;
+        int rk = 0;  // candidates of the same key at lower positions (larger values)
+#pragma unroll 1
+        for (int q = 0; q < m; ++q) {
+          const unsigned long long o = cand_at(q);
+          rk += (uint32_t)(o >> 32) == prefix && o > me;
+        }
+        if (rk == rem - 1) s_T = me;
+      }
+    }
+    __syncthreads();
+  }
+  const unsigned long long T = s_T;
+  int sb = 0;  // taken candidates of earlier chunks
+#pragma unroll 1
+  for (int i = t; i < pc[ch]; i += 256) sb += cand_at(i) >= T;
+  int tot;
+  block_scan_dpp<256>(sb, tmp, &tot);
+  const int base = s_selb + tot;
+  DSV41_PH(5);
+  // ---- G. ordered emission of this chunk
+  bool take[4];
+  int nt = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const bool ok = p + e < c;
+    take[e] = ok && (key[e] >= hi ||
+                     (key[e] >= lo && ((unsigned long long)key[e] << 32 | (uint32_t)~(uint32_t)(p + e)) >= T));
+    nt += take[e];
+  }
+  int o = base + block_scan_dpp<256>(nt, tmp, &tot);
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (take[e]) orow[o++] = p + e + a.offset;
+  DSV41_PH(6);
+}
+
+// Workspace: histograms [R, kBins] | chunk counts [R, nch, 2] | above, candidate positions, candidate keys [R, rs]
+// each (rs = n rounded up to 32, so rows never share a cache line; the one-launch path uses the first two as 64-bit
+// candidate slots [R, rs]) | arrival counters [R] (64-bit) | timeout flag.
+long row_stride(int n) { return ((long)n + 31) / 32 * 32; }
+long select_base_bytes(int R, int n) {
+  const long nch = (n + kChunk - 1) / kChunk;
+  return ((long)R * kBins + (long)R * nch * 2 + 3L * R * row_stride(n)) * 4;
+}
+
 }  // namespace
 
 extern "C" {
 
 #ifdef DSV41_TIMING
 int dsv41_read_ts(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
+int dsv41_read_ph_sel(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ph), sizeof(g_dsv41_ph)); }
+int dsv41_read_ck_sel(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ck), sizeof(g_dsv41_ck)); }
 #endif
 
 long dsv41_select_workspace_bytes(int R, int n) {
-  const long nch = (n + kChunk - 1) / kChunk;
-  return (long)R * (kBins + nch * 2 + 3L * n) * 4;
+  return select_base_bytes(R, n) + (R + 2L) * 8;  // + per-row arrival counters, timeout flag
 }
 
 int dsv41_select_topk(const float* score, long ld, int R, int n, int k, const long* cl, int offset, void* ws,
@@ -363,14 +673,25 @@ int dsv41_select_topk(const float* score, long ld, int R, int n, int k, const lo
   a.R = R;
   a.hist = w;
   a.counts = w + (long)R * kBins;
+  a.rs = row_stride(n);
   a.above = a.counts + (long)R * nch * 2;
-  a.cand_idx = a.above + (long)R * n;
-  a.cand_key = (uint32_t*)(a.cand_idx + (long)R * n);
+  a.cand_idx = a.above + (long)R * a.rs;
+  a.cand_key = (uint32_t*)(a.cand_idx + (long)R * a.rs);
   a.nchunks = nch;
   a.out = out;
   a.out_rstride = out_rstride;
   a.offset = offset;
   hipStream_t st = (hipStream_t)stream;
+  const int rpx = (R + kXcds - 1) / kXcds;
+  if (rpx * nch <= kGroupPerXcd && ld % 4 == 0 && ((uintptr_t)score & 15) == 0) {  // one launch
+    GroupArgs g{a, (unsigned long long*)a.above, nullptr, nullptr, rpx};
+    unsigned long long* ctl = (unsigned long long*)((char*)ws + select_base_bytes(R, n));
+    g.epoch = ctl;
+    g.err = (int*)(ctl + R);
+    select_group_kernel<<<kXcds * rpx * nch, 256, 0, st>>>(g);
+    DSV41_CHECK_LAUNCH();
+    return 0;
+  }
   select_chunks_kernel<<<dim3(nch, R), 256, 0, st>>>(a);
   DSV41_CHECK_LAUNCH();
   finalize_kernel<<<R, kFinThreads, 0, st>>>(a);

@@ -27,6 +27,7 @@ class DecodeLayer:
         self.scale = ckv.shape[-1] ** -0.5
         self._selectors = {}
         self._qbufs = {}
+        self._attn_ws = {}
         self._prepared = None
 
     def _qbuf(self, B, dev):
@@ -59,9 +60,20 @@ class DecodeLayer:
             sel = self._selectors[rows] = DecodeSelector(rows, self.k8.shape[1], self.topk, device)
         return sel
 
+    def attn_workspace(self, B: int, h: int, L: int, device) -> torch.Tensor:
+        """Persistent zero-initialised attention workspace for B rows (split partials + arrival counters, which
+        every launch leaves at zero); allocate it before graph capture.  Calls sharing it must be stream-ordered."""
+        ws = self._attn_ws.get(B)
+        if ws is None:
+            from ._lib import lib
+            n = lib().dsv41_attn_workspace_bytes(B, h, L, self.dv, 0)
+            ws = self._attn_ws[B] = torch.zeros(max(n, 4) // 4, device=device, dtype=torch.float32)
+        return ws
+
     def attend(self, q, idx, pos, seq, pmax, plim=None):
+        ws = self.attn_workspace(q.shape[0], q.shape[2], self.ring.shape[1] + idx.shape[-1], q.device)
         return sattn2(q, self.ring, self.ckv, idx, pos, self.sink, self.cos, self.sin, 0 if self.dv < q.shape[-1]
-                      else self.rd, self.scale, seq, pmax, plim=plim, d_v=self.dv)
+                      else self.rd, self.scale, seq, pmax, plim=plim, d_v=self.dv, ws=ws)
 
     def step(self, q, q_idx, w_idx, pos, seq, pmax, plim=None):
         idx = self.select(q_idx, w_idx, pos, seq)

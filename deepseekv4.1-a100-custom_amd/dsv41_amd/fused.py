@@ -76,7 +76,8 @@ def rope_dev_(x: torch.Tensor, rd: int, cos: torch.Tensor, sin: torch.Tensor, po
 def _workspace(dev, R, H, L, dv, nsplit):
     from ._lib import lib
     n = lib().dsv41_attn_workspace_bytes(R, H, L, dv, nsplit)
-    return (torch.empty(max(n, 4) // 4, device=dev, dtype=torch.float32), n) if n > 0 else (None, 0)
+    # zero-filled: the split-arrival counters at the end must start at zero (the library leaves them at zero)
+    return (torch.zeros(max(n, 4) // 4, device=dev, dtype=torch.float32), n) if n > 0 else (None, 0)
 
 
 def sparse_attn_decode(q: torch.Tensor, kv: torch.Tensor, attn_sink: torch.Tensor, topk_idxs: torch.Tensor,

@@ -24,7 +24,7 @@ def kv_write(x: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch.Ten
 
 
 def sattn2(q, kv_win, kv_c, idx, pos, attn_sink, cos, sin, rd, softmax_scale, seq, pmax, block_t: int = 64,
-           plim=None, d_v: int | None = None, nsplit: int = 0):
+           plim=None, d_v: int | None = None, nsplit: int = 0, ws=None):
     """dsv41/fused2.py:417-446.  q: [B, 1, h, d] bf16 (row b at position pos[b] of sequence seq[b]); kv_win:
     [S, win, d] rings; pmax [B]: newest position written to the row's ring; kv_c: [S, n, d] compressed caches (may be
     an as_strided view) or None; idx: [B, 1, t] int32 rows of kv_c (-1 = none) or None; plim [B] (default pos):
@@ -51,7 +51,10 @@ def sattn2(q, kv_win, kv_c, idx, pos, attn_sink, cos, sin, rd, softmax_scale, se
     sink = attn_sink.float().contiguous()
     o = torch.empty(b, 1, h, dv, device=dev, dtype=q.dtype)
     nbytes = lib().dsv41_attn_workspace_bytes(b, h, win + t, dv, nsplit)
-    ws = torch.empty(max(nbytes, 4) // 4, device=dev, dtype=torch.float32) if nbytes > 0 else None
+    if ws is None:  # the split-arrival counters at its end must start at zero; the library leaves them at zero
+        ws = torch.zeros(max(nbytes, 4) // 4, device=dev, dtype=torch.float32) if nbytes > 0 else None
+    else:
+        assert ws.numel() * ws.element_size() >= nbytes, "workspace too small"
     call("dsv41_sattn2", ptr(qc), ptr(kv_win), kv_win.stride(0), win, ptr(kvc), c_stride, n_c, ptr(ix), t, ptr(pos),
          ptr(seq), ptr(pmax), ptr(plim), ptr(sink), ptr(cos), ptr(sin), int(rd), float(softmax_scale), ptr(o), b, h, d,
          dv, nsplit, ptr(ws), nbytes, stream(dev))

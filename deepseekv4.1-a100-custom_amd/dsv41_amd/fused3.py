@@ -68,8 +68,8 @@ def topk_indices(score: torch.Tensor, k: int, cl: torch.Tensor) -> torch.Tensor:
 
 class DecodeSelector:
     """index_score + topk_indices of the graph decode (dsv41/decode.py:289-294) for a fixed (rows, n_pos, k): the
-    score kernel also builds a 4096-bin histogram of the score keys, from which the top-k needs one compaction pass
-    over many workgroups plus one small finalize per row.  Holds the score buffer and the zero-initialised
+    score kernel also builds a 4096-bin histogram of the score keys, from which the top-k is one workgroup per row
+    (rows up to 36864 positions; longer rows: a compaction pass over many workgroups plus a finalize per row).  Holds the score buffer and the zero-initialised
     workspace (the finalize leaves the histogram zeroed, so the object is reusable and graph-capturable)."""
 
     def __init__(self, rows: int, n_pos: int, k: int, device):
@@ -77,7 +77,8 @@ class DecodeSelector:
         nbytes = lib().dsv41_select_workspace_bytes(rows, n_pos)
         self.ws = torch.zeros(nbytes // 4, dtype=torch.int32, device=device)
         self.nbytes = nbytes
-        self.score = torch.empty(rows, n_pos, dtype=torch.float32, device=device)
+        ld = (n_pos + 3) // 4 * 4  # 16-byte aligned rows: the one-workgroup-per-row selection reads float4
+        self.score = torch.empty(rows, ld, dtype=torch.float32, device=device)[:, :n_pos]
         self.out = torch.empty(rows, 1, k, dtype=torch.int32, device=device)
 
     def score_into(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None) -> None:
@@ -89,9 +90,9 @@ class DecodeSelector:
         _score(q, index_k, weights, seq, cl, k_scale, self.score, False, self.ws, prepared)
 
     def select(self, cl) -> torch.Tensor:
-        """Top-k from the buffered scores + histogram (two launches); leaves the histogram zeroed."""
-        call("dsv41_select_topk", ptr(self.score), self.n_pos, self.rows, self.n_pos, self.k, ptr(cl), 0, ptr(self.ws),
-             self.nbytes, ptr(self.out), self.k, stream(self.score.device))
+        """Top-k from the buffered scores + histogram; leaves the histogram zeroed."""
+        call("dsv41_select_topk", ptr(self.score), self.score.stride(0), self.rows, self.n_pos, self.k, ptr(cl), 0,
+             ptr(self.ws), self.nbytes, ptr(self.out), self.k, stream(self.score.device))
         return self.out
 
     def __call__(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None) -> torch.Tensor:

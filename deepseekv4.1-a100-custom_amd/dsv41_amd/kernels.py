@@ -28,7 +28,7 @@ def sparse_attn(q: torch.Tensor, kv: torch.Tensor, attn_sink: torch.Tensor, topk
         return out
     from ._lib import lib
     nbytes = lib().dsv41_attn_workspace_bytes(b * s, h, t, dv, 0)
-    ws = torch.empty(max(nbytes, 4) // 4, device=dev, dtype=torch.float32) if nbytes > 0 else None
+    ws = torch.zeros(max(nbytes, 4) // 4, device=dev, dtype=torch.float32) if nbytes > 0 else None
     call("dsv41_sparse_attn", ptr(qc), ptr(kvc), ptr(sink), ptr(idx), ptr(out), b, s, h, d, dv, n_kv, kvc.stride(0),
          t, float(softmax_scale), 0, ptr(ws), nbytes, stream(dev))
     return out
