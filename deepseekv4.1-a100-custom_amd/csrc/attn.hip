@@ -370,11 +370,15 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   static_assert(U % 8 == 0, "row width must be a multiple of 64 elements");
   constexpr int TILE = 64;
   constexpr int TILE_ELEMS = TILE * DQK;
+  constexpr int kLoadsPerTile = TILE * U / 512;  // 16-byte direct-to-LDS loads per wave per tile
+  static_assert(kLoadsPerTile < 16, "vmcnt immediate");
   constexpr float kRescale = 8.0f;
-  constexpr int KT_ELEMS = 2 * TILE_ELEMS > 4 * 16 * DV * 2 ? 2 * TILE_ELEMS : 4 * 16 * DV * 2;
+  constexpr int KT_ELEMS = 2 * TILE_ELEMS > 4 * 16 * (DV + 4) * 2 ? 2 * TILE_ELEMS : 4 * 16 * (DV + 4) * 2;
   __shared__ __align__(16) uint16_t ktile[KT_ELEMS];  // two tile buffers; the merge buffer aliases them
   __shared__ const uint16_t* rptr[3][TILE];            // resolved row pointers of tiles i, i+1, i+2 (null: invalid)
-  __shared__ float wm[4][16], wl[4][16];
+  __shared__ float wm[4][16], wl[4][16], wf[4][16], hM[16], hL[16];
+  constexpr int kIxPre = 512;  // index entries prefetched (8 tiles); later tiles load theirs when resolved
+  __shared__ int ixs[kIxPre];
 
   DSV41_TS(10);
   DSV41_PH(0);
@@ -399,8 +403,27 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   const int h0 = hg * 16;
   const int H = a.H;
 
-  long slot, pos = 0, pmax = 0, plim = 0;
+  // the index rows of the first two tiles and Q are loaded before the row's position data (independent loads)
   const int W = a.n1;
+  const int* irow = a.t > 0 ? a.idx + (long)r * a.idx_rstride : nullptr;
+  const int all_tiles = (a.L + TILE - 1) / TILE;  // split sp takes tiles [sp*T/ns, (sp+1)*T/ns)
+  const int j0 = (int)((long)sp * all_tiles / a.nsplit) * TILE;
+  const int j1 = min(a.L, (int)((long)(sp + 1) * all_tiles / a.nsplit) * TILE);
+  const int ntiles = (j1 - j0 + TILE - 1) / TILE;
+  auto load_ix = [&](int jo) {  // index-list entry of key position j0 + jo (or -1)
+    const int j = j0 + jo;
+    const int jj = a.mode == 1 ? j - W : j;
+    return j < j1 && jj >= 0 && irow ? irow[jj] : -1;
+  };
+  ixs[tid] = load_ix(tid);  // the first kIxPre entries of the split, kept in LDS
+  uint4 qf[KS];
+  {
+    const int h = h0 + l16 < H ? h0 + l16 : H - 1;  // rows of missing heads are never written
+    const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)h * DQK;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qrow + ks * 32 + g * 8);
+  }
+  long slot, pos = 0, pmax = 0, plim = 0;
   if (a.mode == 1) {
     slot = a.seq[r];
     pos = a.pos[r];
@@ -411,15 +434,12 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   }
   const uint16_t* base1 = a.kv1 + slot * a.kv1_sstride;
   const uint16_t* base2 = a.kv2 ? a.kv2 + slot * a.kv2_sstride : nullptr;
-  const int* irow = a.t > 0 ? a.idx + (long)r * a.idx_rstride : nullptr;
-  const int all_tiles = (a.L + TILE - 1) / TILE;  // split sp takes tiles [sp*T/ns, (sp+1)*T/ns)
-  const int j0 = (int)((long)sp * all_tiles / a.nsplit) * TILE;
-  const int j1 = min(a.L, (int)((long)(sp + 1) * all_tiles / a.nsplit) * TILE);
-  const int ntiles = (j1 - j0 + TILE - 1) / TILE;
 
   auto resolve = [&](int ti) {  // threads 0..63: row pointer of key position j0 + ti*TILE + tid
     if (tid < TILE) {
-      const int j = j0 + ti * TILE + tid;
+      const int jo = ti * TILE + tid;
+      const int ix = jo < kIxPre ? ixs[jo] : load_ix(jo);
+      const int j = j0 + jo;
       const uint16_t* p = nullptr;
       if (j < j1) {
         if (a.mode == 1 && j < W) {
@@ -428,7 +448,6 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
           const long held = pmax - m;
           if (held >= 0 && held <= plim && pos - held < W) p = base1 + (long)j * DQK;
         } else {
-          const int ix = irow[a.mode == 1 ? j - W : j];
           if (a.mode == 1) {
             if (ix >= 0 && ix < a.n2) p = base2 + (long)ix * DQK;
           } else if (ix >= 0 && ix < a.n1 + a.n2) {
@@ -439,33 +458,29 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
       rptr[ti % 3][tid] = p;
     }
   };
-  auto issue = [&](int ti) {  // direct-to-LDS 16-byte loads; no VGPRs hold the data
+  auto issue = [&](int ti) {  // direct-to-LDS 16-byte loads (inline assembly: no compiler waits around them)
     uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
     const uint16_t* const* rp = rptr[ti % 3];
-#pragma unroll 2
-    for (int rd = 0; rd < TILE * U / 512; ++rd) {
+#pragma unroll 1
+    for (int rd = 0; rd < kLoadsPerTile; ++rd) {
       const int q = rd * 512 + wave * 64 + lane;  // LDS chunk position
       const int j = q / U, cs = q - j * U;
       const int c = cs ^ (j & 7);
       const uint16_t* p = rp[j];
-      const uint16_t* src = p ? p + c * 8 : g_zero_row;
-      __builtin_amdgcn_global_load_lds((const void*)src, (void*)(buf + (rd * 512 + wave * 64) * 8), 16, 0, 0);
+      lds_dma16(p ? p + c * 8 : g_zero_row, buf + (rd * 512 + wave * 64) * 8);
     }
   };
 
-#pragma unroll 1
-  for (int ti = 0; ti < 2 && ti < ntiles; ++ti) resolve(ti);
-  uint4 qf[KS];
-  {
-    const int h = h0 + l16 < H ? h0 + l16 : H - 1;  // rows of missing heads are never written
-    const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)h * DQK;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qrow + ks * 32 + g * 8);
-  }
+  __builtin_amdgcn_s_waitcnt(0);  // Q has arrived too: no wait for it is left inside the tile loop
+  DSV41_PH(1);
+  __syncthreads();
+  if (ntiles > 0) resolve(0);
+  if (ntiles > 1) resolve(1);
   __syncthreads();
   DSV41_TS(11);
-  DSV41_PH(1);
-  issue(0);
+  DSV41_PH(2);
+  if (ntiles > 0) issue(0);
+  if (ntiles > 1) issue(1);
 
   float m_ref = -1e30f, l_run = 0.0f;  // per head (lane's head l16), log2 units
   f32x4_t o[CTH];
@@ -474,10 +489,13 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   const float sl2 = a.scale * kLog2e;
 
   for (int ti = 0; ti < ntiles; ++ti) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    // tile ti is complete once at most one tile's loads of this wave remain (loads complete in order)
+    if (ti + 1 < ntiles)
+      __builtin_amdgcn_s_waitcnt(kLoadsPerTile | (0x7 << 4) | (0xf << 8));  // vmcnt(kLoadsPerTile)
+    else
+      __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
     DSV41_TS(12 + 2 * (ti & 3));
-    if (ti + 1 < ntiles) issue(ti + 1);
     const uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
     const uint16_t* const* rp = rptr[ti % 3];
     const int rb = rw * 16;  // this wave's 16 key rows of the tile
@@ -536,78 +554,101 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
       o[ct] = mfma_bf16_16x16x16(pa, vb, o[ct]);
     }
     DSV41_TS(13 + 2 * (ti & 3));
-    if (ti + 2 < ntiles) resolve(ti + 2);
+    if (ti + 2 < ntiles) {
+      resolve(ti + 2);
+      lds_barrier();  // buffer ti & 1 is free, the pointers of tile ti + 2 are visible
+      issue(ti + 2);
+    }
   }
   __syncthreads();
   DSV41_TS(20);
-  DSV41_PH(2);
+  DSV41_PH(3);
 
-  // ---- merge the 4 row-waves' states per head (both column halves hold identical m, l)
+  // ---- merge the 4 row-waves' states per head (both column halves hold identical m, l): per-head maximum M, sum L
+  // and the waves' factors once, then the waves' accumulators scaled into LDS (row stride DVP: the 4 heads a
+  // 16-lane row group writes fall on different banks) and summed
+  constexpr int DVP = DV + 4;
   if (half == 0 && g == 0) {
     wm[rw][l16] = m_ref;
     wl[rw][l16] = l_run;
   }
   __syncthreads();
+  if (tid < 16) {
+    const float M = fmaxf(fmaxf(wm[0][tid], wm[1][tid]), fmaxf(wm[2][tid], wm[3][tid]));
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = exp2f(wm[w][tid] - M);
+      wf[w][tid] = f;
+      L += wl[w][tid] * f;
+    }
+    hM[tid] = M;
+    hL[tid] = L;
+  }
+  __syncthreads();
   {
-    float fac[4];  // this wave's factor for the heads 4g + i its accumulators hold
+    float* xw = (float*)ktile + rw * 16 * DVP + half * (DV / 2);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int hh = 4 * g + i;
-      const float M = fmaxf(fmaxf(wm[0][hh], wm[1][hh]), fmaxf(wm[2][hh], wm[3][hh]));
-      fac[i] = exp2f(wm[rw][hh] - M);
+      const float fac = wf[rw][4 * g + i];
+#pragma unroll
+      for (int ct = 0; ct < CTH; ++ct) xw[(4 * g + i) * DVP + ct * 16 + l16] = o[ct][i] * fac;
     }
-    float* xw = (float*)ktile + rw * 16 * DV + half * (DV / 2);
-#pragma unroll
-    for (int ct = 0; ct < CTH; ++ct)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xw[(4 * g + i) * DV + ct * 16 + l16] = o[ct][i] * fac[i];
   }
   __syncthreads();
   DSV41_TS(21);
+  DSV41_PH(4);
   const float* xb = (const float*)ktile;
   const bool final_out = a.nsplit == 1;
   const long pr = pos < 0 ? 0 : pos;
   const float ln2 = 0.6931471805599453f;
-#pragma unroll 2
-  for (int e = tid; e < 16 * DV / 2; e += 512) {  // column pairs (2c, 2c + 1) of head hh
-    const int hh = e / (DV / 2), c = 2 * (e - hh * (DV / 2));
+  constexpr int CG = DV / 8;  // 8-column groups per head: one 16-byte store each
+#pragma unroll 1
+  for (int e = tid; e < 16 * CG; e += 512) {
+    const int hh = e / CG, c = (e - hh * CG) * 8;
     const int hout = h0 + hh;
     if (hout >= H) continue;
-    const float M = fmaxf(fmaxf(wm[0][hh], wm[1][hh]), fmaxf(wm[2][hh], wm[3][hh]));
-    float L = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) L += wl[w][hh] * exp2f(wm[w][hh] - M);
-    float v0 = 0.0f, v1 = 0.0f;
+    const float M = hM[hh], L = hL[hh];
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float2 xx = *(const float2*)(xb + (w * 16 + hh) * DV + c);
-      v0 += xx.x;
-      v1 += xx.y;
+      const float4 x0 = *(const float4*)(xb + (w * 16 + hh) * DVP + c);
+      const float4 x1 = *(const float4*)(xb + (w * 16 + hh) * DVP + c + 4);
+      v[0] += x0.x, v[1] += x0.y, v[2] += x0.z, v[3] += x0.w;
+      v[4] += x1.x, v[5] += x1.y, v[6] += x1.z, v[7] += x1.w;
     }
+    uint32_t pk[4];
     if (final_out) {
       const float inv = 1.0f / (L + exp2f(a.sink[hout] * kLog2e - M));
-      float re = round_bf16(v0 * inv), im = round_bf16(v1 * inv);
-      if (a.rd > 0 && c >= DV - a.rd) {
-        const int jj = (c - (DV - a.rd)) >> 1;
-        const float cs = a.cos_t[pr * (a.rd / 2) + jj];
-        const float sn = -a.sin_t[pr * (a.rd / 2) + jj];
-        const float yr = re * cs - im * sn, yi = re * sn + im * cs;
-        re = yr;
-        im = yi;
+#pragma unroll
+      for (int q = 0; q < 8; q += 2) {
+        float re = round_bf16(v[q] * inv), im = round_bf16(v[q + 1] * inv);
+        const int cc = c + q;
+        if (a.rd > 0 && cc >= DV - a.rd) {
+          const int jj = (cc - (DV - a.rd)) >> 1;
+          const float cs = a.cos_t[pr * (a.rd / 2) + jj];
+          const float sn = -a.sin_t[pr * (a.rd / 2) + jj];
+          const float yr = re * cs - im * sn, yi = re * sn + im * cs;
+          re = yr;
+          im = yi;
+        }
+        pk[q / 2] = pack_bf16x2(re, im);
       }
-      *(uint32_t*)(a.out + (long)r * a.out_rstride + (long)hout * DV + c) = pack_bf16x2(re, im);
+      *(uint4*)(a.out + (long)r * a.out_rstride + (long)hout * DV + c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
     } else {
       const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+      for (int q = 0; q < 8; q += 2) pk[q / 2] = pack_bf16x2(v[q] * inv, v[q + 1] * inv);
       const long pi = ((long)r * H + hout) * a.nsplit + sp;
-      *(uint32_t*)((uint16_t*)a.pacc + pi * DV + c) = pack_bf16x2(v0 * inv, v1 * inv);
+      *(uint4*)((uint16_t*)a.pacc + pi * DV + c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
       if (c == 0) {
-        a.pm[pi] = M * ln2;  // natural-log units, as the combine expects
+        a.pm[pi] = M * ln2;  // natural-log units, as the merge expects
         a.pl[pi] = L;
       }
     }
   }
   DSV41_TS(22);
-  DSV41_PH(3);
+  DSV41_PH(5);
   if (final_out || !a.arrive) {
     DSV41_WG_TS(1);
     return;
@@ -621,11 +662,11 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
     DSV41_WG_TS(1);
     return;
   }
-  DSV41_PH(4);
+  DSV41_PH(6);
   group_acquire(old, home);
   if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   merge_splits<DV>(a, r, h0, pr, wts);
-  DSV41_PH(5);
+  DSV41_PH(7);
   DSV41_WG_TS(1);
 }
 

@@ -138,6 +138,22 @@ __device__ long long g_dsv41_ck[1024][8];  // shader clock at the same points
   } while (0)
 #endif
 
+// Workgroup execution barrier that waits for this wave's LDS operations but not for its outstanding global loads
+// (e.g. direct-to-LDS tile loads still in flight, waited for separately with a counted vmcnt).  __syncthreads()
+// would wait for every outstanding memory operation.  The memory clobber keeps the compiler from moving memory
+// accesses across it.
+DSV41_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// 16-byte direct-to-LDS load: lane i writes lds_dst + 16 i (lds_dst is wave-uniform).  Issued as inline assembly
+// so the compiler does not treat later LDS reads as dependent on it (it would wait for every outstanding load
+// before them); callers wait for these loads with explicit vmcnt counts.  Compiler-tracked loads are unaffected:
+// loads complete in order, so the compiler's own waits only become stricter.
+DSV41_DEV void lds_dma16(const void* src, void* lds_dst) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds_dst);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+}
+
 // ---- scans
 // Inclusive prefix sum over the 64 lanes of a wave with DPP lane moves (no LDS traffic): shifts of 1, 2, 4, 8
 // within each row of 16 lanes, then the row totals are carried by row_bcast:15 (into rows 1, 3) and row_bcast:31

@@ -227,12 +227,15 @@ def test_sattn2_reference_geometry(p):
         attn_close(host(o), want, f"sattn2 ref pos={p} c={with_c}")
 
 
-def test_sattn2_absorbed_mla_ragged_with_drafts():
+@pytest.mark.parametrize("H", [64, 40])
+def test_sattn2_absorbed_mla_ragged_with_drafts(H):
     """576/512 absorbed MLA, k = 2048, 4 slots at ragged positions, plus 6 draft rows of one sequence with plim
-    causal masking (the MTP verify shape, dsv41/fused2.py:351-360)."""
+    causal masking (the MTP verify shape, dsv41/fused2.py:351-360), at 64 and 40 heads.  Two calls share one
+    workspace (its split counters must be left ready)."""
     import dsv41_amd
+    from dsv41_amd._lib import lib
     r = rng(9)
-    H, dqk, dv, win, k = 64, 576, 512, 128, 2048
+    dqk, dv, win, k = 576, 512, 128, 2048
     S, n_c = 4, 4096
     q = O.bf16(r.standard_normal((10, 1, H, dqk)).astype(np.float32))
     sink = r.standard_normal(H).astype(np.float32)
@@ -247,10 +250,13 @@ def test_sattn2_absorbed_mla_ragged_with_drafts():
         nv = min(k, cl)
         idx[b, 0, :nv] = np.sort(r.choice(cl, nv, replace=False))
     cos = np.zeros((1, 1), np.float32)
-    o = dsv41_amd.sattn2(bf(q), bf(ring), bf(ckv), torch.from_numpy(idx).to(DEV), i64(pos), f32(sink), f32(cos),
-                         f32(cos), 0, dqk ** -0.5, i64(seq), i64(pmax), plim=i64(pos), d_v=dv)
     want = O.sattn2(q, ring, ckv, idx, pos, seq, pmax, pos, sink, cos, cos, 0, dqk ** -0.5, dv=dv)
-    attn_close(host(o), want, "sattn2 mla ragged+drafts")
+    nbytes = lib().dsv41_attn_workspace_bytes(10, H, win + k, dv, 0)
+    ws = torch.zeros(max(nbytes, 4) // 4, dtype=torch.float32, device=DEV)
+    for call_no in range(2):
+        o = dsv41_amd.sattn2(bf(q), bf(ring), bf(ckv), torch.from_numpy(idx).to(DEV), i64(pos), f32(sink), f32(cos),
+                             f32(cos), 0, dqk ** -0.5, i64(seq), i64(pmax), plim=i64(pos), d_v=dv, ws=ws)
+        attn_close(host(o), want, f"sattn2 mla ragged+drafts H={H} call {call_no}")
 
 
 # ------------------------------------------------------------------------------------------------ indexer
