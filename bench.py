@@ -6,7 +6,8 @@ compressed-KV and index-key appends, the indexer score over the e4m3 keys, the t
 ring + top-k rows.  Inputs are resident in HBM; NL independent copies of the layer's caches are rotated so every
 step misses the 256 MB last-level cache.  The timed region replays a HIP graph of NL layer-steps K/NL times
 (rounded up) with events on the launch stream; the per-kernel durations behind `roofline` come from an eager pass
-with events around each launch, on the same stream.
+with events around each launch, on the same stream; each heavy kernel is also replayed alone from a graph of NL
+launches for its average launch duration.
 
 Prints ONE JSON line (rank 0, N = 1)."""
 from __future__ import annotations
@@ -31,18 +32,18 @@ def log(*a):
 
 
 def decode_bytes(cfg, idx_sets=None):
-    """Algorithmic HBM bytes of one decode layer-step: per slot the valid index keys (128 B + 4 B scale each), the
-    union of the selected compressed rows, the ring, plus per query row q, index q, output and indices."""
+    """Algorithmic HBM bytes per launch of the decode kernels.  indexer: per slot the valid index keys (128 B + 4 B
+    scale each), per query row the prepared e4m3 query and weights and the k indices written.  sattn: per slot the
+    union of the selected compressed rows and the ring rows (576 x bf16 each), per query row q, output and indices."""
     from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN
-    per_kernel = {"index_score": 0, "topk": 0, "sattn": 0}
+    per_kernel = {"indexer": 0, "sattn": 0}
     R = cfg.slots * cfg.rows_per_slot
     for s in range(cfg.slots):
         n = cfg.n_c(s)
-        per_kernel["index_score"] += n * (DI + 4) + cfg.rows_per_slot * n * 4  # keys + scores written
-        per_kernel["topk"] += cfg.rows_per_slot * n * 4 + cfg.rows_per_slot * cfg.topk * 4
+        per_kernel["indexer"] += n * (DI + 4)
         sel = min(cfg.topk, n) if idx_sets is None else idx_sets[s]
         per_kernel["sattn"] += (sel + WIN) * DQK * 2
-    per_kernel["index_score"] += R * (HI * DI * 2 + HI * 2)
+    per_kernel["indexer"] += R * (64 * DI + 64 * 4 + cfg.topk * 4)
     per_kernel["sattn"] += R * (H * DQK * 2 + H * DV * 2 + cfg.topk * 4)
     return per_kernel
 
@@ -93,29 +94,23 @@ def run_decode(args, dev):
             layer_step(lay)
     torch.cuda.synchronize(dev)
 
-    # ---- per-phase durations (eager, events around each launch on the launch stream): appends (1 kernel),
-    # index_score (the score kernel alone), topk (selection), sattn (attention, splits merged in-kernel)
+    # ---- per-phase durations (eager, events around each launch on the launch stream): appends (1 kernel), indexer
+    # (scores + top-k: one launch), sattn (attention, splits merged in-kernel)
     E = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    phases = {"appends": [], "index_score": [], "topk": [], "sattn": []}
+    phases = {"appends": [], "indexer": [], "sattn": []}
     reps = max(2, min(args.steps, 20))
-    from dsv41_amd.fused2 import sattn2
     sel_union = None
     for rep in range(reps):
         for lay in L:
-            ev = [E() for _ in range(5)]
+            ev = [E() for _ in range(4)]
             ev[0].record(stream)
             lay.appends(st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos, seq, st["q_idx"],
                         st["w_idx"])
             ev[1].record(stream)
-            sel = lay.selector(st["q_idx"].shape[0], st["q_idx"].device)
-            sel.score_into(st["q_idx"], lay.k8, st["w_idx"], seq, cl, k_scale=lay.ks, prepared=lay._prepared)
+            idx = lay.select(st["q_idx"], st["w_idx"], pos, seq, cl)
             ev[2].record(stream)
-            idx = sel.select(cl)
+            lay.attend(st["q"], idx, pos, seq, pmax, plim=pos)
             ev[3].record(stream)
-            ws = lay.attn_workspace(st["q"].shape[0], st["q"].shape[2], lay.ring.shape[1] + idx.shape[-1], dev)
-            o = sattn2(st["q"], lay.ring, lay.ckv, idx, pos, lay.sink, lay.cos, lay.sin, 0, lay.scale, seq, pmax,
-                       plim=pos, d_v=512, ws=ws)
-            ev[4].record(stream)
             torch.cuda.synchronize(dev)
             for i, k in enumerate(phases):
                 phases[k].append(ev[i].elapsed_time(ev[i + 1]) * 1000.0)
@@ -153,35 +148,36 @@ def run_decode(args, dev):
     step_us = e0.elapsed_time(e1) * 1000.0 / (replays * NL)
     log(f"[bench] graph: {replays} replays x {NL} layer-steps: {step_us:.2f} us/layer-step (wall {wall*1e3:.1f} ms)")
 
-    # ---- the dominant kernel alone: a graph of NL index-score launches (one per cache copy), replayed; its average
-    # launch duration is the roofline denominator
-    gs = torch.cuda.CUDAGraph()
-    sels = [lay.selector(st["q_idx"].shape[0], dev) for lay in L]
-    with torch.cuda.stream(s2):
-        for lay, sel in zip(L, sels):
-            sel.score_into(st["q_idx"], lay.k8, st["w_idx"], seq, cl, k_scale=lay.ks, prepared=lay._prepared)
-            sel.select(cl)  # keeps the histograms zeroed
+    # ---- each heavy kernel alone: a graph of NL launches of it (one per cache copy), replayed; the average launch
+    # duration (events on the launch stream around the replays) is the roofline denominator
+    idxs = [lay.select(st["q_idx"], st["w_idx"], pos, seq, cl) for lay in L]
     torch.cuda.synchronize(dev)
-    with torch.cuda.graph(gs, stream=s2):
-        for lay, sel in zip(L, sels):
-            sel.score_into(st["q_idx"], lay.k8, st["w_idx"], seq, cl, k_scale=lay.ks, prepared=lay._prepared)
-    # histogram accumulation is harmless here (the score values are what is timed); re-zero afterwards
-    gs.replay()
-    torch.cuda.synchronize(dev)
-    e2, e3 = E(), E()
-    e2.record(stream)
-    for _ in range(replays):
-        gs.replay()
-    e3.record(stream)
-    torch.cuda.synchronize(dev)
-    for sel in sels:
-        sel.ws.zero_()
-    score_us = e2.elapsed_time(e3) * 1000.0 / (replays * NL)
-    log(f"[bench] index_score kernel alone: {score_us:.2f} us/launch")
+    only = {"indexer": lambda lay, i: lay.select(st["q_idx"], st["w_idx"], pos, seq, cl),
+            "sattn": lambda lay, i: lay.attend(st["q"], idxs[i], pos, seq, pmax, plim=pos)}
+    alone_us = {}
+    for name, fn in only.items():
+        gk = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s2):
+            for i, lay in enumerate(L):
+                fn(lay, i)
+        torch.cuda.synchronize(dev)
+        with torch.cuda.graph(gk, stream=s2):
+            for i, lay in enumerate(L):
+                fn(lay, i)
+        gk.replay()
+        torch.cuda.synchronize(dev)
+        e2, e3 = E(), E()
+        e2.record(stream)
+        for _ in range(replays):
+            gk.replay()
+        e3.record(stream)
+        torch.cuda.synchronize(dev)
+        alone_us[name] = e2.elapsed_time(e3) * 1000.0 / (replays * NL)
+        log(f"[bench] {name} kernel alone: {alone_us[name]:.2f} us/launch")
     log(f"[bench] eager per-kernel medians (us): {kern_us}")
     kb = decode_bytes(cfg, sel_union)
     return dict(cfg=cfg, step_us=step_us, kern_us=kern_us, kern_bytes=kb, steps=replays * NL, sel_union=sel_union,
-                score_us=score_us)
+                alone_us=alone_us)
 
 
 def run_prefill(args, dev):
@@ -331,13 +327,20 @@ def main():
     r = run_decode(args, dev)
     cfg = r["cfg"]
     kb, ku = r["kern_bytes"], r["kern_us"]
-    dom = "index_score"  # single-launch kernel with the most algorithmic bytes (the e4m3 key scan)
-    achieved = kb[dom] / (r["score_us"] * 1e-6) / 1e9
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", "index_score_C2_traffic.json")
-    if os.path.exists(tf):  # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
-        with open(tf) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+    kernel_names = {"indexer": "index_select_kernel (scores + top-k, one launch)",
+                    "sattn": "attn_decode_kernel<576, 512> (splits merged in-kernel)"}
+    roof = {}
+    for name, us in r["alone_us"].items():
+        achieved = kb[name] / (us * 1e-6) / 1e9
+        traffic = None
+        tf = os.path.join(ROOT, "profiles", f"{name}_C2_traffic.json")
+        if os.path.exists(tf):  # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+            with open(tf) as f:
+                traffic = json.load(f).get("bytes_per_launch")
+        roof[name] = {"bound": "hbm", "kernel": kernel_names[name], "achieved": round(achieved, 1),
+                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                      "traffic": traffic, "algorithmic_bytes": kb[name], "kernel_us": round(us, 3)}
+    dom = max(r["alone_us"], key=r["alone_us"].get)  # the kernel with the longest launch
     alg = survey_bytes(cfg)
     frac_step = alg / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS
     pre = None if args.no_prefill else run_prefill(args, dev)
@@ -361,9 +364,8 @@ def main():
         "hbm_roofline_pct": round(100.0 * frac_step, 2),
         "algorithmic_bytes_per_step": alg,
         "kernel_us": {k: round(v, 3) for k, v in ku.items()},
-        "roofline": {"bound": "hbm", "kernel": "index_score_kernel (e4m3 keys, histogram)", "achieved":
-                     round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "algorithmic_bytes": kb[dom], "kernel_us": round(r["score_us"], 3)},
+        "roofline": roof[dom],
+        "roofline_other": {k: v for k, v in roof.items() if k != dom},
         "prefill": pre,
         "cpu_baseline": cpu,
     }

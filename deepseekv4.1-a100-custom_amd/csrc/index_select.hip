@@ -1,0 +1,402 @@
+// Decode lightning indexer in one launch: the scores of a row's compressed positions, their histogram and the top-k
+// selection (dsv41/decode.py:284-294, index_score followed by topk_indices; scores as dsv41/fused3.py:20-62, the
+// k largest of score[r, 0..cl) in ascending index order with -1 padding as dsv41/fused3.py:65-75, ties lowest index
+// first).
+//
+// Grid: R x nslots workgroups of 512 threads (chunk ch of row r is workgroup ch * R + r, so a row's chunks spread
+// over the XCDs), all resident at once (at most kIsMaxWG: 2 per CU).  Each workgroup:
+//   A. scores its 512 positions (8 waves x 64 keys, every key load issued up front, e4m3 keys against the prepared e4m3 queries, fp8 MFMA), keeps
+//      them in LDS, builds their 4096-bin histogram (top 12 bits of the order-preserving key) in LDS and adds it to
+//      the row's histogram with device-scope atomics
+//   B. row barrier 1; reads the row histogram: threshold bin B (where the running count from the top reaches k) and
+//      need = k - (entries above B)
+//   C. classifies its positions (one per thread): entries above B are counted, bin-B candidates
+//      (key << 32 | ~position) stored in the chunk's slots, with the counts
+//   D. row barrier 2; clears its slice of the row histogram
+//   E. gathers every chunk's counts and candidates (the first kIsSpec of each chunk with the counts, in one round
+//      trip), threshold candidate T (exact ranks / radix passes over the candidates)
+//   F. writes its taken positions (above B, or candidates >= T) at their global offset.
+// Data exchanged between workgroups (histogram, counts, candidates) is written and read with device-scope atomic
+// operations, which the hardware keeps coherent across the XCDs' L2 caches, so no cache maintenance is needed.  The
+// row barriers use one flag word per chunk (see row_wait); a wait gives up after kIsSpinLimit polls and sets the
+// error word, so every wave exits.
+#include "score_core.h"
+#include "select_core.h"
+
+namespace {
+
+constexpr int kIsThreads = 512;                // 8 waves: two per SIMD
+constexpr int kIsChunk = 512;                  // positions per workgroup
+constexpr int kIsKeysPerWave = kIsChunk / 8;   // 4 column tiles of 16 keys
+constexpr int kIsPer = kIsChunk / kIsThreads;  // positions per thread in the selection
+constexpr int kIsSpec = 16;                    // candidates per chunk read together with the counts
+constexpr int kIsCand = 2048;                  // candidates staged in LDS (more: read from the workspace)
+constexpr int kIsMaxChunks = 128;              // chunks per row (rows up to 65536 positions)
+constexpr int kIsMaxWG = 512;                  // resident workgroups: 2 per CU
+constexpr int kIsSpinLimit = 1 << 20;
+
+struct IsArgs {
+  ScoreArgs s;                // prepared e4m3 queries, folded weights, e4m3 keys + scales, seq, cl, n_pos; out or null
+  int k, offset;
+  int* idx;
+  long idx_rstride;
+  int nslots;                 // chunks per row
+  int* hist;                  // [R, kHistBins], zero between launches
+  unsigned long long* cnt;    // [R, nslots]: above | candidates << 32
+  unsigned long long* cand;   // [R, nslots * kIsChunk]
+  unsigned long long* flags;  // [R, nslots] barrier flags
+  int* err;
+};
+
+// Row barrier on flag words: chunk ch of row r owns flag[r][ch], which only grows (2e after launch e - 1).  At
+// phase ph (1, 2) of launch e a workgroup stores 2e + ph into its flag and waits until every flag of the row is
+// >= 2e + ph: threads 0..nslots-1 read the row's flags each poll (one round trip, no same-address contention).
+DSV41_DEV void row_wait(const unsigned long long* flags, int ns, unsigned long long target, int* done, int* err) {
+  const int t = threadIdx.x;
+  int spins = 0;
+#pragma unroll 1
+  while (true) {
+    const bool ok = t >= ns || __hip_atomic_load(flags + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target;
+    const int all = __syncthreads_and(ok);
+    if (all || ++spins >= kIsSpinLimit) break;
+    __builtin_amdgcn_s_sleep(4);
+  }
+  if (t == 0 && spins >= kIsSpinLimit) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  (void)done;
+}
+
+__global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArgs g) {
+  const ScoreArgs& a = g.s;
+  const int R = a.R, ns = g.nslots;
+  const int r = blockIdx.x % R, ch = blockIdx.x / R;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  __shared__ int lhist[kHistBins];
+  __shared__ float sc[kIsChunk];
+  __shared__ int tmp[8];
+  __shared__ int wcnt[8][2];
+  __shared__ int s_bin, s_need, s_cnt, s_selb, s_over;
+  __shared__ int pc[kIsMaxChunks + 1], na_q[kIsMaxChunks], nc_q[kIsMaxChunks];
+  __shared__ __align__(16) unsigned long long lc[kIsCand + 2];
+  __shared__ RankScratch rs;
+
+  // ---- A. row data (independent loads), scores, histogram
+  DSV41_PH(0);
+  DSV41_TS(48);
+  const long clr = row_cl(a, r);
+  const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
+  // this chunk's flag is 2e after launch e - 1 (earlier launches have completed): e is this launch's epoch
+  const unsigned long long e0 =
+      __hip_atomic_load(g.flags + (long)r * ns + ch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) / 2;
+  const int c = (int)(clr < 0 ? 0 : (clr > a.n_pos ? a.n_pos : clr)), k = g.k;
+  const int nht = (a.HI + 15) / 16;
+  i32x8_t qa8[kHT];
+  uint4 qa16[kHT][4];  // (bf16 queries: unused here)
+  float wl[kHT];
+#pragma unroll
+  for (int ht = 0; ht < kHT; ++ht) {
+    const int h = ht * 16 + l16;
+    const bool hv = ht < nht && h < a.HI;
+    const int hc = hv ? h : 0;
+    const uint4* qrow = (const uint4*)((const uint8_t*)a.q + (long)r * a.q_rstride + (long)hc * 128 + g4 * 32);
+    const uint4 u0 = qrow[0], u1 = qrow[1];
+    qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+    wl[ht] = hv ? a.w[(long)r * a.w_rstride + hc] : 0.0f;
+  }
+#ifdef DSV41_TIMING
+  __builtin_amdgcn_s_waitcnt(0);
+  DSV41_TS(49);
+#endif
+#pragma unroll 1
+  for (int i = t; i < kHistBins; i += kIsThreads) lhist[i] = 0;
+  constexpr int NT = kIsKeysPerWave / 16;  // column tiles of 16 keys per wave, all loads issued up front
+  uint4 k0[NT], k1[NT];
+  float ksc[NT];
+  const int pw = ch * kIsChunk + wave * kIsKeysPerWave;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int p = pw + nt * 16 + l16;
+    const bool pv = p < c;
+    const uint8_t* krow = (const uint8_t*)a.keys + slot * a.k_sstride + (long)p * 128 + g4 * 32;
+    k0[nt] = pv ? *(const uint4*)krow : make_uint4(0, 0, 0, 0);
+    k1[nt] = pv ? *(const uint4*)(krow + 16) : make_uint4(0, 0, 0, 0);
+    ksc[nt] = pv ? a.kscale[slot * a.ks_sstride + p] : 0.0f;
+  }
+#ifdef DSV41_TIMING
+  DSV41_TS(50);
+  __builtin_amdgcn_s_waitcnt(0);
+  DSV41_TS(51);
+#endif
+  float wr[kHT][4];  // weights of the heads this lane's accumulators hold: ht*16 + 4g + i
+#pragma unroll
+  for (int ht = 0; ht < kHT; ++ht)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[ht], 4 * g4 + i, 64);
+  __syncthreads();  // histogram cleared
+  DSV41_TS(52);
+  const bool sel = c > k;  // (otherwise every valid position is taken)
+  float* orow = a.out ? a.out + (long)r * a.out_rstride : nullptr;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int p = pw + nt * 16 + l16;
+    const float sum = score_tile<1>(qa8, qa16, wr, nht, k0[nt], k1[nt], nullptr);
+    if (g4 == 0) {
+      const float v = p < c ? sum * ksc[nt] : 0.0f;
+      sc[p - ch * kIsChunk] = v;
+      if (p < c && sel) atomicAdd(&lhist[score_key(v) >> 20], 1);
+      if (orow && p < a.n_pos) orow[p] = p < c ? v : -__builtin_inff();
+    }
+  }
+  DSV41_TS(53);
+  __syncthreads();
+  DSV41_PH(1);
+  DSV41_TS(54);
+  int* gh = g.hist + (long)r * kHistBins;
+  unsigned long long* rflags = g.flags + (long)r * ns;
+  int* oidx = g.idx + (long)r * g.idx_rstride;
+  if (!sel) {  // everything is selected: arrive twice without waiting (keeps the row's arrival count)
+    if (ch == 0) {
+#pragma unroll 1
+      for (int i = t; i < k; i += kIsThreads) oidx[i] = i < c ? i + g.offset : -1;
+    }
+    if (t == 0) __hip_atomic_store(rflags + ch, 2 * e0 + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+#pragma unroll 1
+  for (int i = t; i < kHistBins; i += kIsThreads) {
+    const int v = lhist[i];
+    if (v) atomicAdd(&gh[i], v);
+  }
+  // ---- B. row barrier 1, threshold bin
+  __builtin_amdgcn_s_waitcnt(0);
+  DSV41_PH(2);
+  __syncthreads();
+  if (t == 0) {
+    __hip_atomic_store(rflags + ch, 2 * e0 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_bin = 0;  // (a histogram holding fewer than k entries is a caller error)
+    s_need = k;
+    s_cnt = 0;
+  }
+  row_wait(rflags, ns, 2 * e0 + 1, nullptr, g.err);
+  DSV41_PH(3);
+  {
+    constexpr int BP = kHistBins / kIsThreads;  // bins per thread: 4095 - BP*t (h[0]) down to 4096 - BP*(t+1)
+    int h[BP];
+#pragma unroll
+    for (int u = 0; u < BP / 2; ++u) {
+      const unsigned long long v = __hip_atomic_load(
+          (unsigned long long*)(gh + kHistBins - BP * (t + 1) + 2 * u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      h[BP - 1 - 2 * u] = (int)(v & 0xffffffffu);
+      h[BP - 2 - 2 * u] = (int)(v >> 32);
+    }
+    int local = 0;
+#pragma unroll
+    for (int i = 0; i < BP; ++i) local += h[i];
+    int total;
+    int above = block_scan_dpp<kIsThreads>(local, tmp, &total);
+    if (above < k && k <= above + local) {
+#pragma unroll 1
+      for (int i = 0; i < BP; ++i) {
+        if (k <= above + h[i]) {
+          s_bin = kHistBins - 1 - BP * t - i;
+          s_need = k - above;
+          s_cnt = h[i];
+          break;
+        }
+        above += h[i];
+      }
+    }
+    __syncthreads();
+  }
+  const uint32_t lo = (uint32_t)s_bin << 20, hi = (uint32_t)(s_bin + 1) << 20;  // bin B = [lo, hi)
+  const int need = s_need;
+  // ---- C. classify this thread's positions
+  const int p0 = ch * kIsChunk + kIsPer * t;
+  uint32_t key[kIsPer];
+  int na = 0, nc = 0;
+#pragma unroll
+  for (int e = 0; e < kIsPer; ++e) {
+    key[e] = score_key(sc[kIsPer * t + e]);
+    const bool ok = p0 + e < c;
+    na += ok && key[e] >= hi;
+    nc += ok && key[e] >= lo && key[e] < hi;
+  }
+  const int ia = wave_incl_scan(na), ic = wave_incl_scan(nc);
+  if (lane == 63) {
+    wcnt[wave][0] = ia;
+    wcnt[wave][1] = ic;
+  }
+  __syncthreads();
+  int cbase = 0;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) cbase += w < wave ? wcnt[w][1] : 0;
+  unsigned long long* crow = g.cand + (long)r * ns * kIsChunk;
+  if (nc > 0) {
+    int o = ch * kIsChunk + cbase + ic - nc;
+#pragma unroll
+    for (int e = 0; e < kIsPer; ++e)
+      if (p0 + e < c && key[e] >= lo && key[e] < hi)
+        __hip_atomic_store(crow + o++, (unsigned long long)key[e] << 32 | (uint32_t)~(uint32_t)(p0 + e),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (t == 0) {
+    unsigned ta = 0, tc = 0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) ta += wcnt[w][0], tc += wcnt[w][1];
+    __hip_atomic_store(g.cnt + (long)r * ns + ch, (unsigned long long)ta | (unsigned long long)tc << 32,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // ---- D. row barrier 2; the histogram has been read by every chunk
+  __builtin_amdgcn_s_waitcnt(0);
+  DSV41_PH(4);
+  __syncthreads();
+  if (t == 0) __hip_atomic_store(rflags + ch, 2 * e0 + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  row_wait(rflags, ns, 2 * e0 + 2, nullptr, g.err);
+  DSV41_PH(5);
+  {
+    const int zb = (kHistBins + ns - 1) / ns, z0 = ch * zb, z1 = min(kHistBins, z0 + zb);
+#pragma unroll 1
+    for (int i = z0 + t; i < z1; i += kIsThreads) gh[i] = 0;
+  }
+  // ---- E. counts of all chunks + speculative candidate prefixes
+  if (t < ns) {
+    const unsigned long long cv = __hip_atomic_load(g.cnt + (long)r * ns + t, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+    na_q[t] = (int)(cv & 0xffffffffu);
+    nc_q[t] = (int)(cv >> 32);
+  }
+  constexpr int kSpecPer = kIsMaxChunks * kIsSpec / kIsThreads;
+  unsigned long long sv[kSpecPer];
+#pragma unroll
+  for (int u = 0; u < kSpecPer; ++u) {
+    const int id = u * kIsThreads + t, q = id / kIsSpec, e = id % kIsSpec;
+    sv[u] = q < ns ? __hip_atomic_load(crow + q * kIsChunk + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+  }
+  __syncthreads();
+  if (wave < 2) {  // prefix of the candidate counts (2 x 64 chunks); entries above B in earlier chunks
+    const int q = wave * 64 + lane;
+    const int x = q < ns ? nc_q[q] : 0;
+    const int ix = wave_incl_scan(x);
+    pc[q + 1] = ix;  // (wave 1 adds wave 0's total below)
+    const int y = q < ch ? na_q[q] : 0;
+    const int iy = wave_incl_scan(y);
+    if (lane == 63) wcnt[wave][0] = iy, wcnt[wave][1] = ix;
+    const bool over = __ballot(x > kIsSpec) != 0;
+    if (lane == 0) tmp[wave] = over;
+  }
+  __syncthreads();
+  if (t >= 64 && t < 128) pc[t + 1] += wcnt[0][1];
+  if (t == 0) {
+    pc[0] = 0;
+    s_selb = wcnt[0][0] + wcnt[1][0];
+    s_over = tmp[0] | tmp[1];
+  }
+  __syncthreads();
+  const int m = pc[ns];
+  const bool staged = m <= kIsCand;
+  if (t == 0 && staged) lc[m] = 0ull;  // pad for pairwise reads
+#pragma unroll
+  for (int u = 0; u < kSpecPer; ++u) {
+    const int id = u * kIsThreads + t, q = id / kIsSpec, e = id % kIsSpec;
+    if (staged && q < ns && e < nc_q[q]) lc[pc[q] + e] = sv[u];
+  }
+  if (staged && s_over) {  // chunks with more than kIsSpec candidates
+#pragma unroll 1
+    for (int q = 0; q < ns; ++q)
+      for (int e = kIsSpec + t; e < nc_q[q]; e += kIsThreads)
+        lc[pc[q] + e] = __hip_atomic_load(crow + q * kIsChunk + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  auto cand_at = [&](int i) -> unsigned long long {
+    if (staged) return lc[i];
+    int q = 0;
+    while (pc[q + 1] <= i) ++q;
+    return __hip_atomic_load(crow + q * kIsChunk + (i - pc[q]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  DSV41_PH(6);
+  const unsigned long long T = threshold_candidate<kIsThreads>(cand_at, lc, staged, m, need, lo, rs);
+  int sb = 0;  // taken candidates of earlier chunks
+#pragma unroll 1
+  for (int i = t; i < pc[ch]; i += kIsThreads) sb += cand_at(i) >= T;
+  int tot;
+  block_scan_dpp<kIsThreads>(sb, tmp, &tot);
+  const int base = s_selb + tot;
+  // ---- F. ordered emission of this chunk
+  bool take[kIsPer];
+  int nt = 0;
+#pragma unroll
+  for (int e = 0; e < kIsPer; ++e) {
+    const bool ok = p0 + e < c;
+    take[e] = ok && (key[e] >= hi ||
+                     (key[e] >= lo && ((unsigned long long)key[e] << 32 | (uint32_t)~(uint32_t)(p0 + e)) >= T));
+    nt += take[e];
+  }
+  int o = base + block_scan_dpp<kIsThreads>(nt, tmp, &tot);
+#pragma unroll
+  for (int e = 0; e < kIsPer; ++e)
+    if (take[e]) oidx[o++] = p0 + e + g.offset;
+  DSV41_PH(7);
+}
+
+int is_slots(int n_pos) { return (n_pos + kIsChunk - 1) / kIsChunk; }
+
+}  // namespace
+
+extern "C" {
+
+#ifdef DSV41_TIMING
+int dsv41_read_ph_is(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ph), sizeof(g_dsv41_ph)); }
+int dsv41_read_ts_is(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
+#endif
+
+long dsv41_index_select_workspace_bytes(int R, int n_pos) {
+  const long ns = is_slots(n_pos);
+  return (long)R * kHistBins * 4 + (long)R * ns * 8 + (long)R * ns * kIsChunk * 8 + (long)R * ns * 8 + 16;
+}
+
+int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_rstride, int R, int HI,
+                       const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
+                       const long* cl, int n_pos, int k, int offset, void* ws, long ws_bytes, float* score_out,
+                       long score_rstride, int* out, long out_rstride, void* stream) {
+  if (R <= 0 || k <= 0) return 0;
+  const int ns = is_slots(n_pos);
+  if (n_pos <= 0 || HI <= 0 || HI > 64 || !cl || !kscale || ns > kIsMaxChunks || (long)R * ns > kIsMaxWG)
+    return (int)hipErrorInvalidValue;
+  if (!ws || ws_bytes < dsv41_index_select_workspace_bytes(R, n_pos)) return (int)hipErrorInvalidValue;
+  IsArgs g{};
+  ScoreArgs& a = g.s;
+  a.q = (const uint16_t*)q8;
+  a.q_rstride = q_rstride;
+  a.w = wf;
+  a.w_rstride = w_rstride;
+  a.HI = HI;
+  a.R = R;
+  a.kfmt = 1;
+  a.keys = keys;
+  a.k_sstride = k_sstride;
+  a.kscale = kscale;
+  a.ks_sstride = ks_sstride;
+  a.seq = seq;
+  a.rows_per_slot = 1;
+  a.cl = cl;
+  a.n_pos = n_pos;
+  a.write_masked = 1;
+  a.out = score_out;
+  a.out_rstride = score_rstride;
+  g.k = k;
+  g.offset = offset;
+  g.idx = out;
+  g.idx_rstride = out_rstride;
+  g.nslots = ns;
+  char* w = (char*)ws;
+  g.hist = (int*)w;
+  g.cnt = (unsigned long long*)(w + (long)R * kHistBins * 4);
+  g.cand = g.cnt + (long)R * ns;
+  g.flags = g.cand + (long)R * ns * kIsChunk;
+  g.err = (int*)(g.flags + (long)R * ns);
+  index_select_kernel<<<R * ns, kIsThreads, 0, (hipStream_t)stream>>>(g);
+  DSV41_CHECK_LAUNCH();
+  return 0;
+}
+
+}  // extern "C"

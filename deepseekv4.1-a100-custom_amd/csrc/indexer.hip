@@ -12,76 +12,15 @@
 // column tiles of 16 keys, loads issued before the query preparation); the query fragments live in VGPRs.  MFMA output layout: lane l holds key (l & 15) and
 // heads 4*(l >> 4) + i, so the head reduction is 16 in-lane FMAs plus two cross-lane shuffles.
 // Keys at positions >= cl are never read: the scan is bounded by the valid count, not the allocated capacity.
-#include "common.h"
+#include "score_core.h"
 
 namespace {
-
-struct ScoreArgs {
-  const uint16_t* q;  // bf16 [R, HI, 128] (bf16 keys) or prepared e4m3 [R, 64, 128] bytes (e4m3 keys)
-  long q_rstride;     // elements (bf16) or bytes (e4m3) between rows
-  const float* w;  // [R, HI] fp32
-  long w_rstride;
-  int HI, R;
-  int kfmt;  // 0: bf16 keys; 1: e4m3 keys + fp32 per-row scale
-  const void* keys;
-  long k_sstride;  // elements (bf16) or bytes (e4m3) between slots
-  const float* kscale;
-  long ks_sstride;
-  const long* seq;  // slot = seq[r], or r / rows_per_slot when null
-  int rows_per_slot;
-  const long* cl;  // valid count per row, or (cl_start + (r % rows_per_slot) + 1) / cl_ratio when null
-  long cl_start;
-  int cl_ratio;
-  int n_pos;         // columns of the output row
-  int write_masked;  // write -inf for cl <= t < n_pos
-  float* out;
-  long out_rstride;
-  int* hist;  // optional [R, kHistBins]: counts of score_key(score) >> 20 over t < cl (decode selection)
-};
-
-DSV41_DEV long row_cl(const ScoreArgs& a, int r) {
-  if (a.cl) return a.cl[r];
-  return (a.cl_start + (long)(r % a.rows_per_slot) + 1) / a.cl_ratio;
-}
-
-constexpr int kHT = 4;            // head tiles of 16 (up to 64 indexer heads)
-constexpr int kHistBins = 4096;   // top 12 bits of the order-preserving score key (8 bins per octave)
-constexpr int kKeysPerWave = 64;   // 4 column tiles of 16 keys (two or more waves per SIMD)
-constexpr int kKeysPerWG = 4 * kKeysPerWave;
-
-// One column tile (16 keys) against all head tiles; returns this lane's partial weighted relu sum for key l16.
-template <int KFMT>
-DSV41_DEV float score_tile(const i32x8_t (&qa8)[kHT], const uint4 (&qa16)[kHT][4], const float (&wr)[kHT][4],
-                           int nht, uint4 k0, uint4 k1, const uint4* kb16) {
-  f32x4_t acc[kHT];
-#pragma unroll
-  for (int ht = 0; ht < kHT; ++ht) acc[ht] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  if (KFMT == 1) {
-    const i32x8_t kb = i32x8_t{(int)k0.x, (int)k0.y, (int)k0.z, (int)k0.w, (int)k1.x, (int)k1.y, (int)k1.z, (int)k1.w};
-#pragma unroll
-    for (int ht = 0; ht < kHT; ++ht)
-      if (ht < nht) acc[ht] = mfma_fp8_16x16x128(qa8[ht], kb, acc[ht]);
-  } else {
-#pragma unroll
-    for (int ht = 0; ht < kHT; ++ht)
-      if (ht < nht)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) acc[ht] = mfma_bf16_16x16x32(qa16[ht][ks], kb16[ks], acc[ht]);
-  }
-  float sum = 0.0f;
-#pragma unroll
-  for (int ht = 0; ht < kHT; ++ht)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sum += wr[ht][i] * fmaxf(acc[ht][i], 0.0f);
-  sum += wave_shfl_xor(sum, 16);
-  sum += wave_shfl_xor(sum, 32);
-  return sum;
-}
 
 template <int KFMT, bool HIST>
 __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
   DSV41_TS(30);
   DSV41_WG_TS(0);
+  if (blockIdx.y == 0) DSV41_PH(0);
   __shared__ int lhist[HIST ? kHistBins : 1];
   const int r = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -100,6 +39,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
       for (int t = kt0 + lane; t < kt0 + kKeysPerWave && t < a.n_pos; t += 64) orow[t] = -__builtin_inff();
     if (!HIST) return;
   } else {
+  if (blockIdx.y == 0) DSV41_PH(1);
   const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
   const int nht = (a.HI + 15) / 16;
   const int lim = (int)cl;
@@ -152,6 +92,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
     if (!hv) wl[ht] = 0.0f;
   }
   DSV41_TS(31);
+  if (blockIdx.y == 0) DSV41_PH(2);
   float wr[kHT][4];  // weights of the heads this lane's accumulators hold: ht*16 + 4g + i
 #pragma unroll
   for (int ht = 0; ht < kHT; ++ht)
@@ -176,6 +117,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
   }
   }  // kt0 < cl
   DSV41_TS(32);
+  if (blockIdx.y == 0) DSV41_PH(3);
   if (HIST) {
     __syncthreads();
     int* gh = a.hist + (long)r * kHistBins;
@@ -185,6 +127,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
       if (v) atomicAdd(&gh[i], v);
     }
   }
+  if (blockIdx.y == 0) DSV41_PH(4);
   DSV41_WG_TS(1);
 }
 
@@ -584,6 +527,7 @@ extern "C" {
 
 #ifdef DSV41_TIMING
 int dsv41_read_ts_idx(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
+int dsv41_read_ph_idx(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ph), sizeof(g_dsv41_ph)); }
 int dsv41_read_wg_idx(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_wg), sizeof(g_dsv41_wg)); }
 #endif
 

@@ -12,7 +12,7 @@
 //                   candidates in an LDS bitmap over the row and emits the set in index order from the bitmap's
 //                   popcount prefix.  It leaves hist[r] zeroed for the next step.
 // The row is read once (select) and never re-scanned; the finalize work is proportional to k plus the candidates.
-#include "common.h"
+#include "select_core.h"
 
 namespace {
 
@@ -352,7 +352,6 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
 constexpr int kGroupPerXcd = 64;   // 2 per CU of a 32-CU XCD: every chunk of a row is resident at the barrier
 constexpr int kGroupSpec = 32;     // candidates per chunk read together with the counts
 constexpr int kGroupCand = 2048;   // candidates staged in LDS (more: read from the workspace)
-constexpr int kRankDirect = 64;    // up to this many candidates: direct ranks; more: radix passes
 constexpr int kSpinLimit = 1 << 22;
 constexpr unsigned long long kAwayFlag = 1ull << 48, kArriveMask = kAwayFlag - 1;
 
@@ -375,9 +374,8 @@ __global__ void __launch_bounds__(256) select_group_kernel(const GroupArgs g) {
   __shared__ int pc[kGroupPerXcd + 1];
   __shared__ int na_q[kGroupPerXcd], nc_q[kGroupPerXcd];
   __shared__ unsigned long long lc[kGroupCand + 2];  // (+ a zero pad after the last candidate)
-  __shared__ int rh[1024];
-  __shared__ int s_over, s_digit, s_rem, s_eq;
-  __shared__ unsigned long long s_T, s_ep;
+  __shared__ RankScratch rs;
+  __shared__ int s_over;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int nslots = a.nchunks;
   DSV41_PH(0);
@@ -540,75 +538,7 @@ __global__ void __launch_bounds__(256) select_group_kernel(const GroupArgs g) {
   };
   DSV41_PH(4);
   // ---- F. threshold candidate
-  if (t == 0) s_T = 0ull;  // every candidate is taken
-  __syncthreads();
-  if (cnt != need || m != need) {
-    if (staged && m <= kRankDirect) {  // direct ranks, two candidates per LDS read
-      const uint4* l4 = (const uint4*)lc;
-      const int m2 = (m + 1) / 2;
-#pragma unroll 1
-      for (int i = t; i < m; i += 256) {
-        const unsigned long long me = lc[i];
-        int rk = 0;
-#pragma unroll 8
-        for (int q = 0; q < m2; ++q) {
-          const uint4 w = l4[q];
-          rk += ((unsigned long long)w.y << 32 | w.x) > me;
-          rk += ((unsigned long long)w.w << 32 | w.z) > me;
-        }
-        if (rk == need - 1) s_T = me;
-      }
-    } else {
-      // two 10-bit histogram passes over key bits 19..10 and 9..0 give the exact key Tk and the number rem of
-      // candidates with key Tk that are taken; among those, the one whose position ranks rem - 1 is T
-      uint32_t prefix = lo, mask = 0xfff00000u;
-      int rem = need;
-#pragma unroll 1
-      for (int pass = 0; pass < 2; ++pass) {
-        const int shift = pass == 0 ? 10 : 0;
-        *(int4*)(rh + 4 * t) = make_int4(0, 0, 0, 0);
-        __syncthreads();
-#pragma unroll 1
-        for (int i = t; i < m; i += 256) {
-          const uint32_t kk = (uint32_t)(cand_at(i) >> 32);
-          if ((kk & mask) == prefix) atomicAdd(&rh[(kk >> shift) & 1023], 1);
-        }
-        __syncthreads();
-        const int4 hv = *(const int4*)(rh + 1020 - 4 * t);  // digits 1023-4t .. 1020-4t
-        const int h[4] = {hv.w, hv.z, hv.y, hv.x};
-        int tot;
-        int greater = block_scan_dpp<256>(h[0] + h[1] + h[2] + h[3], tmp, &tot);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (greater < rem && rem <= greater + h[i]) {
-            s_digit = 1023 - 4 * t - i;
-            s_rem = rem - greater;
-            s_eq = h[i];
-          }
-          greater += h[i];
-        }
-        __syncthreads();
-        prefix |= (uint32_t)s_digit << shift;
-        mask |= 1023u << shift;
-        rem = s_rem;
-      }
-      if (t == 0 && s_eq == rem) s_T = (unsigned long long)prefix << 32;  // every candidate with key Tk is taken
-#pragma unroll 1
-      for (int i = t; i < m && s_eq != rem; i += 256) {
-        const unsigned long long me = cand_at(i);
-        if ((uint32_t)(me >> 32) != prefix) continue;
-        int rk = 0;  // candidates of the same key at lower positions (larger values)
-#pragma unroll 1
-        for (int q = 0; q < m; ++q) {
-          const unsigned long long o = cand_at(q);
-          rk += (uint32_t)(o >> 32) == prefix && o > me;
-        }
-        if (rk == rem - 1) s_T = me;
-      }
-    }
-    __syncthreads();
-  }
-  const unsigned long long T = s_T;
+  const unsigned long long T = threshold_candidate(cand_at, lc, staged, m, need, lo, rs);
   int sb = 0;  // taken candidates of earlier chunks
 #pragma unroll 1
   for (int i = t; i < pc[ch]; i += 256) sb += cand_at(i) >= T;

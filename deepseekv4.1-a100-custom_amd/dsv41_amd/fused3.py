@@ -67,19 +67,27 @@ def topk_indices(score: torch.Tensor, k: int, cl: torch.Tensor) -> torch.Tensor:
 
 
 class DecodeSelector:
-    """index_score + topk_indices of the graph decode (dsv41/decode.py:289-294) for a fixed (rows, n_pos, k): the
-    score kernel also builds a 4096-bin histogram of the score keys, from which the top-k is one workgroup per row
-    (rows up to 36864 positions; longer rows: a compaction pass over many workgroups plus a finalize per row).  Holds the score buffer and the zero-initialised
-    workspace (the finalize leaves the histogram zeroed, so the object is reusable and graph-capturable)."""
+    """index_score + topk_indices of the graph decode (dsv41/decode.py:289-294) for a fixed (rows, n_pos, k).  With
+    e4m3 keys and a grid that fits (rows * ceil(n_pos / 512) <= 512 workgroups, n_pos <= 65536) both run in one
+    launch (dsv41_index_select); otherwise the score kernel builds a 4096-bin histogram of the score keys and the
+    top-k follows from it (one workgroup per row up to 36864 positions, else a compaction pass plus a finalize).
+    Holds the score buffer and the zero-initialised workspaces, which every call leaves ready for the next
+    (reusable, graph-capturable).  keep_scores: also write the scores (self.score) on the one-launch path."""
 
-    def __init__(self, rows: int, n_pos: int, k: int, device):
+    def __init__(self, rows: int, n_pos: int, k: int, device, keep_scores: bool = False):
         self.rows, self.n_pos, self.k = rows, n_pos, k
         nbytes = lib().dsv41_select_workspace_bytes(rows, n_pos)
         self.ws = torch.zeros(nbytes // 4, dtype=torch.int32, device=device)
         self.nbytes = nbytes
-        ld = (n_pos + 3) // 4 * 4  # 16-byte aligned rows: the one-workgroup-per-row selection reads float4
+        ld = (n_pos + 3) // 4 * 4  # 16-byte aligned rows: the selection reads float4
         self.score = torch.empty(rows, ld, dtype=torch.float32, device=device)[:, :n_pos]
         self.out = torch.empty(rows, 1, k, dtype=torch.int32, device=device)
+        ns = (n_pos + 511) // 512
+        self.one_launch = ns <= 128 and rows * ns <= 512
+        self.keep_scores = keep_scores
+        if self.one_launch:
+            self.fnbytes = lib().dsv41_index_select_workspace_bytes(rows, n_pos)
+            self.fws = torch.zeros(self.fnbytes // 4, dtype=torch.int32, device=device)
 
     def score_into(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None) -> None:
         """The score kernel alone (scores + histogram into this object's buffers)."""
@@ -95,9 +103,24 @@ class DecodeSelector:
              ptr(self.ws), self.nbytes, ptr(self.out), self.k, stream(self.score.device))
         return self.out
 
+    def select_one_launch(self, q8, wf, H: int, index_k, k_scale, seq, cl) -> torch.Tensor:
+        """Scores + top-k in one launch from the prepared e4m3 queries (q8, wf)."""
+        ks = k_scale if k_scale.dtype == torch.float32 else k_scale.float()
+        call("dsv41_index_select", ptr(q8), 64 * 128, ptr(wf), 64, self.rows, H, ptr(index_k), index_k.stride(0),
+             ptr(ks), ks.stride(0), ptr(seq), ptr(cl), self.n_pos, self.k, 0, ptr(self.fws), self.fnbytes,
+             ptr(self.score) if self.keep_scores else None, self.score.stride(0), ptr(self.out), self.k,
+             stream(self.score.device))
+        return self.out
+
     def __call__(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None) -> torch.Tensor:
         dev = require_gpu(q, index_k, weights)
         seq = as_i64(seq.reshape(-1), dev)
         cl = as_i64(cl.reshape(-1), dev)
+        if self.one_launch and index_k.dtype == torch.float8_e4m3fn and k_scale is not None:
+            if q.shape[0] != self.rows or index_k.shape[1] != self.n_pos:
+                raise RuntimeError(f"DecodeSelector built for {self.rows} x {self.n_pos}, got {q.shape[0]} x "
+                                   f"{index_k.shape[1]}")
+            q8, wf = prepared if prepared is not None else qprep(q, weights)
+            return self.select_one_launch(q8, wf, q.shape[2], index_k, k_scale, seq, cl)
         self.score_into(q, index_k, weights, seq, cl, k_scale, prepared)
         return self.select(cl)

@@ -80,6 +80,24 @@ long dsv41_select_workspace_bytes(int R, int n);
 int dsv41_select_topk(const float* score, long ld, int R, int n, int k, const long* cl, int offset, void* ws,
                       long ws_bytes, int* out, long out_rstride, void* stream);
 
+/* Workspace of dsv41_index_select for R rows of n_pos positions.  Allocate it zeroed once: every call leaves its
+ * histogram zeroed and its arrival counters consistent for the next call (calls sharing it must be stream-ordered). */
+long dsv41_index_select_workspace_bytes(int R, int n_pos);
+
+/* The decode indexer in one launch: fused3.index_score followed by fused3.topk_indices (dsv41/decode.py:284-294;
+ * scores as dsv41/fused3.py:20-62, selection as dsv41/fused3.py:65-75).  q8/wf: the prepared e4m3 queries and folded
+ * weights of dsv41_index_qprep; keys: e4m3 [S, n_pos, 128] with fp32 per-row scales; row r uses slot seq[r] and
+ * positions 0..cl[r).  out [R, k]: the k largest scores' positions, ascending, + offset, -1 padding when cl[r] < k;
+ * ties lowest index first (the set of dsv41_topk_indices on the same scores).  score_out (may be null): the scores,
+ * -inf for cl[r] <= t < n_pos.  Needs R * ceil(n_pos / 512) <= 512 workgroups (resident together: the rows'
+ * workgroups meet at two barriers) and n_pos <= 65536; otherwise hipErrorInvalidValue (use dsv41_index_score +
+ * dsv41_select_topk).  A barrier wait that gives up (a workgroup never arrived) sets the workspace's last-but-three
+ * int32 to 1. */
+int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_rstride, int R, int HI,
+                       const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
+                       const long* cl, int n_pos, int k, int offset, void* ws, long ws_bytes, float* score_out,
+                       long score_rstride, int* out, long out_rstride, void* stream);
+
 /* fused3.topk_indices + cuda/topk_select.cu (dsv41/fused3.py:65-75, dsv41/cuda/topk_select.cu:94-168), also the
  * selection of Indexer.__call__ (dsv41/model.py:868-893): per row the k largest of score[r, 0..c) with c =
  * min(cl(r), n), ascending, + offset; positions past the selection (c < k) are -1.  Ties: lower index first. */

@@ -405,8 +405,8 @@ def test_select_topk_histogram_path(n, k, cls):
 
 @pytest.mark.parametrize("cls", [[32768, 32768, 20000, 1500], [2048, 100000, 3, 65000]])
 def test_decode_selector_end_to_end(cls):
-    """Fused decode selector (score kernel with histogram + select + finalize) == oracle top-k on the kernel's own
-    scores (bit-exact), and the scores match the oracle within 1e-2."""
+    """Decode selector (one launch: scores + histogram + selection; or the score kernel then the selection) ==
+    oracle top-k on the kernel's own scores (bit-exact), and the scores match the oracle within 1e-2."""
     from dsv41_amd.fused3 import DecodeSelector
     from dsv41_amd.workloads import encode_e4m3_rows, fp4_round
     g = torch.Generator(device=DEV).manual_seed(15)
@@ -416,12 +416,15 @@ def test_decode_selector_end_to_end(cls):
     q = fp4_round(torch.randn(R, 1, H, 128, generator=g, device=DEV))
     w = (torch.randn(R, H, generator=g, device=DEV) * 0.01).to(torch.bfloat16)
     seq = i64([0, 2, 1, 2])
-    sel = DecodeSelector(R, n, 2048, DEV)
+    sel = DecodeSelector(R, n, 2048, DEV, keep_scores=True)
+    assert sel.one_launch == (n <= 65536)  # one launch (score + select) for the first case, two kernels for the other
     for rep in range(2):  # the second call checks the workspace is reusable
         idx = sel(q, k8, w, seq, i64(cls), k_scale=ks)
         torch.cuda.synchronize()
         sc = sel.score.cpu().numpy()
         np.testing.assert_array_equal(idx.cpu().numpy()[:, 0], O.topk_indices(sc, 2048, cls))
+        if sel.one_launch:
+            assert int(sel.fws[-4].item()) == 0, "row barrier wait gave up"
     want = O.index_score(q.float().cpu().numpy(), k8.float().cpu().numpy(), w.float().cpu().numpy(),
                          [0, 2, 1, 2], cls, k_scale=ks.cpu().numpy())
     for b, c in enumerate(cls):
