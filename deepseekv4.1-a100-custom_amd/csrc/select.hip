@@ -12,6 +12,8 @@
 //                   candidates in an LDS bitmap over the row and emits the set in index order from the bitmap's
 //                   popcount prefix.  It leaves hist[r] zeroed for the next step.
 // The row is read once (select) and never re-scanned; the finalize work is proportional to k plus the candidates.
+// When a row's chunks fit one resident grid (at most 64 workgroups per XCD), select_group does both steps in one
+// launch: the chunks of a row run on one XCD and meet at a row barrier (see the kernel).
 #include "select_core.h"
 
 namespace {
