@@ -461,14 +461,17 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   auto issue = [&](int ti) {  // direct-to-LDS 16-byte loads (inline assembly: no compiler waits around them)
     uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
     const uint16_t* const* rp = rptr[ti % 3];
-#pragma unroll 1
+    const uint16_t* src[kLoadsPerTile];  // all row pointers read before the first load (the loads clobber memory)
+#pragma unroll
     for (int rd = 0; rd < kLoadsPerTile; ++rd) {
       const int q = rd * 512 + wave * 64 + lane;  // LDS chunk position
       const int j = q / U, cs = q - j * U;
       const int c = cs ^ (j & 7);
       const uint16_t* p = rp[j];
-      lds_dma16(p ? p + c * 8 : g_zero_row, buf + (rd * 512 + wave * 64) * 8);
+      src[rd] = p ? p + c * 8 : g_zero_row;
     }
+#pragma unroll
+    for (int rd = 0; rd < kLoadsPerTile; ++rd) lds_dma16(src[rd], buf + (rd * 512 + wave * 64) * 8);
   };
 
   __builtin_amdgcn_s_waitcnt(0);  // Q has arrived too: no wait for it is left inside the tile loop
@@ -764,14 +767,17 @@ __global__ void __launch_bounds__(512) attn_prefill_kernel(const AttnArgs a) {
   auto issue = [&](int ti) {  // direct-to-LDS 16-byte loads (inline assembly: no compiler waits around them)
     uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
     const uint16_t* const* rp = rptr[ti % 3];
-#pragma unroll 1
+    const uint16_t* src[kLoadsPerTile];  // all row pointers read before the first load (the loads clobber memory)
+#pragma unroll
     for (int rd = 0; rd < kLoadsPerTile; ++rd) {
       const int cc = rd * 512 + wave * 64 + lane;  // LDS chunk position
       const int j = cc / U, cs = cc - j * U;
       const int c = cs ^ (j & 7);
       const uint16_t* p = rp[j];
-      lds_dma16(p ? p + c * 8 : g_zero_row, buf + (rd * 512 + wave * 64) * 8);
+      src[rd] = p ? p + c * 8 : g_zero_row;
     }
+#pragma unroll
+    for (int rd = 0; rd < kLoadsPerTile; ++rd) lds_dma16(src[rd], buf + (rd * 512 + wave * 64) * 8);
   };
 
   __builtin_amdgcn_s_waitcnt(0);  // Q, the first index entries and the row's positions have arrived
