@@ -56,7 +56,9 @@ struct AttnArgs {
   int rd;
 };
 
-DSV41_DEV uint32_t pack_bf16x2(float a, float b) { return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16); }
+// Two floats to packed bf16 (round to nearest even), one v_cvt_pk_bf16_f32.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+DSV41_DEV uint32_t pack_bf16x2(float a, float b) { return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)a, (__bf16)b}); }
 
 template <int DQK, int DV>
 __global__ void __launch_bounds__(256) attn_split_kernel(const AttnArgs a) {
@@ -923,6 +925,294 @@ __global__ void __launch_bounds__(512) attn_prefill_kernel(const AttnArgs a) {
   }
 }
 
+// Many query rows, pipelined roles: the same work as attn_prefill_kernel (one workgroup per (query row, 64 heads),
+// whole key list) with 32-key tiles and the two halves of the tile work overlapped across waves:
+//   QK waves 0..3, w = (hb = w & 1: heads 32hb..32hb+31, kb = w >> 1: keys 16kb..16kb+15 of the tile): S for tile t
+//       (16x16x32 bf16 MFMA, Q of 32 heads in VGPRs, each K fragment used for two head blocks), the per-head tile
+//       maximum exchanged with the other key half, the probabilities (bf16, MFMA operand order) and the per-head
+//       rescale factor published through LDS.  These waves also gather the tiles (direct-to-LDS loads, two ahead).
+//   PV waves 4..7, cq = w - 4: O[64 heads x columns cq*DV/4 ..] += P V for tile t - 1 (16x16x16 bf16 MFMA, each
+//       transposed V fragment used for four head blocks).  Wave 4 also loads the index entries and resolves the
+//       row pointers three tiles ahead.
+// Four tile buffers: tile t (QK), t - 1 (PV), t + 1 and t + 2 (in flight).  Per tile two workgroup barriers:
+//   B0: tile t has landed, P / rescale of tile t - 1 and the pointers of tile t + 2 are visible;
+//   X:  both key halves' tile maxima of tile t are visible (and PV of tile t - 1 is done).
+template <int DQK, int DV>
+__global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) {
+  constexpr int KS = DQK / 32;  // 32-deep k steps of QK^T
+  constexpr int CT = DV / 64;   // 16-column output tiles per PV wave (a quarter of DV)
+  constexpr int U = DQK / 8;    // 16-byte chunks per row; chunk c of row j at j*U + (c ^ (j & 7))
+  static_assert(U % 8 == 0 && CT >= 1, "row widths");
+  constexpr int TILE = 32, NBUF = 4;
+  constexpr int TILE_ELEMS = TILE * DQK;
+  constexpr int kLd = TILE * U / 256;  // loads per QK-wave lane per tile
+  static_assert(TILE * U % 256 == 0 && kLd < 16, "vmcnt immediate");
+  static_assert(64 * DV * 4 <= NBUF * TILE_ELEMS * 2, "output staging fits the tile buffers");
+  constexpr float kRescale = 8.0f;
+  __shared__ __align__(16) uint16_t ktile[NBUF * TILE_ELEMS];
+  __shared__ const uint16_t* rptr[NBUF][TILE];
+  __shared__ uint2 pex[2][4][2][64];  // [tile parity][head block][key block][lane]
+  __shared__ float smax[2][4][64];    // [key half][lane group][head]; reused for the per-half sums at the end
+  __shared__ float salpha[2][64];     // [tile parity][head]: rescale factor (1 when the reference stays)
+  __shared__ float hfac[64];
+
+  const int hg64 = blockIdx.y;
+  const int per_xcd = (a.R + kXcds - 1) / kXcds, zb = blockIdx.z;
+  const int r = (zb % kXcds) * per_xcd + zb / kXcds;  // contiguous row ranges per XCD: shared rows hit its L2
+  if (r >= a.R) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool qk = wave < 4;
+  const int hb = wave & 1, kb = (wave >> 1) & 1;  // QK role
+  const int cq = wave & 3;                        // PV role
+  const int l16 = lane & 15, g = lane >> 4;
+  const int H = a.H;
+
+  const int W = a.n1;
+  const int* irow = a.t > 0 ? a.idx + (long)r * a.idx_rstride : nullptr;
+  const int L = a.L;
+  const int ntiles = (L + TILE - 1) / TILE;
+  const bool resolver = wave == 4 && lane < TILE;
+  auto load_ix = [&](int ti) {  // resolver lanes: index-list entry of key position ti*TILE + lane (or -1)
+    const int j = ti * TILE + lane;
+    const int jj = a.mode == 1 ? j - W : j;
+    return resolver && j < L && jj >= 0 && irow ? irow[jj] : -1;
+  };
+  long slot, pos = 0, pmax = 0, plim = 0;
+  if (a.mode == 1) {
+    slot = a.seq[r];
+    pos = a.pos[r];
+    pmax = a.pmax[r];
+    plim = a.plim ? a.plim[r] : pos;
+  } else {
+    slot = r / a.rows_per_slot;
+  }
+  const uint16_t* base1 = a.kv1 + slot * a.kv1_sstride;
+  const uint16_t* base2 = a.kv2 ? a.kv2 + slot * a.kv2_sstride : nullptr;
+  auto resolve = [&](int ti, int ix) {  // resolver lanes: row pointer of key position ti*TILE + lane
+    if (resolver) {
+      const int j = ti * TILE + lane;
+      const uint16_t* p = nullptr;
+      if (j < L) {
+        if (a.mode == 1 && j < W) {
+          int m = (int)(pmax - j) % W;
+          m = m < 0 ? m + W : m;
+          const long held = pmax - m;
+          if (held >= 0 && held <= plim && pos - held < W) p = base1 + (long)j * DQK;
+        } else if (a.mode == 1) {
+          if (ix >= 0 && ix < a.n2) p = base2 + (long)ix * DQK;
+        } else if (ix >= 0 && ix < a.n1 + a.n2) {
+          p = ix < a.n1 ? base1 + (long)ix * DQK : base2 + (long)(ix - a.n1) * DQK;
+        }
+      }
+      rptr[ti % NBUF][lane] = p;
+    }
+  };
+  auto issue = [&](int ti) {  // QK waves: direct-to-LDS 16-byte loads (inline assembly: no compiler waits)
+    uint16_t* buf = ktile + (ti % NBUF) * TILE_ELEMS;
+    const uint16_t* const* rp = rptr[ti % NBUF];
+    const uint16_t* src[kLd];  // all row pointers read before the first load (the loads clobber memory)
+#pragma unroll
+    for (int rd = 0; rd < kLd; ++rd) {
+      const int cc = rd * 256 + wave * 64 + lane;  // LDS chunk position
+      const int j = cc / U, cs = cc - j * U;
+      const int c = cs ^ (j & 7);
+      const uint16_t* p = rp[j];
+      src[rd] = p ? p + c * 8 : g_zero_row;
+    }
+#pragma unroll
+    for (int rd = 0; rd < kLd; ++rd) lds_dma16(src[rd], buf + (rd * 256 + wave * 64) * 8);
+  };
+
+  {
+    const int i0 = load_ix(0), i1 = load_ix(1), i2 = load_ix(2);
+    resolve(0, i0);
+    resolve(1, i1);
+    resolve(2, i2);
+  }
+  const float sl2 = a.scale * kLog2e;
+  float* stg = (float*)ktile;  // output staging [64 heads][DV] once the tiles are done
+  // The two roles run separate loops (so Q and the O accumulators never share registers) with the same barrier
+  // sequence: one after the prologue, B0 and X per iteration t = 0..ntiles, two in the epilogue.
+  if (qk) {
+    // Q of heads 32hb + 16b + l16 (B operand, k = 32 ks + 8 g ..); lazy reference and sum per head (log2 units)
+    uint4 qf[2][KS];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int h = hg64 * 64 + hb * 32 + b * 16 + l16;
+      const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)(h < H ? h : H - 1) * DQK + g * 8;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qf[b][ks] = *(const uint4*)(qrow + ks * 32);
+    }
+    float m_ref[2] = {-1e30f, -1e30f}, l_run[2] = {0.0f, 0.0f};
+    __builtin_amdgcn_s_waitcnt(0);  // Q has arrived: the tile loads below are this wave's only loads
+    __syncthreads();
+    if (ntiles > 0) issue(0);
+    if (ntiles > 1) issue(1);
+    for (int t = 0; t <= ntiles; ++t) {
+      DSV41_TST(8 * (t % 6) + 2, 0);
+      if (t + 1 < ntiles)
+        __builtin_amdgcn_s_waitcnt(kLd | (0x7 << 4) | (0xf << 8));  // vmcnt(kLd): tile t has landed
+      else
+        __builtin_amdgcn_s_waitcnt(0);
+      DSV41_TST(8 * (t % 6) + 3, 0);
+      lds_barrier();  // B0
+      DSV41_TS(8 * (t % 6) + 0);
+      if (t >= ntiles) {
+        lds_barrier();  // X
+        break;
+      }
+      const uint16_t* buf = ktile + (t % NBUF) * TILE_ELEMS;
+      const int jr = 16 * kb + l16;
+      // chunk (4 ks + g) ^ (jr & 7) = 4 ks + (g ^ (jr & 3)) + (jr & 4) for even ks, - (jr & 4) for odd ks: two
+      // base addresses and immediate offsets
+      const uint16_t* kre = buf + jr * DQK + ((g ^ (jr & 3)) + (jr & 4)) * 8;
+      const uint16_t* kro = kre - (jr & 4) * 16;
+      f32x4_t s[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint4 kf = *(const uint4*)((ks & 1 ? kro : kre) + ks * 32);
+        s[0] = mfma_bf16_16x16x32(kf, qf[0][ks], s[0]);
+        s[1] = mfma_bf16_16x16x32(kf, qf[1][ks], s[1]);
+      }
+      // s[b][i]: key 16kb + 4g + i of the tile, head 32hb + 16b + l16
+      const uint16_t* const* rp = rptr[t % NBUF];
+      bool ok[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ok[i] = rp[16 * kb + 4 * g + i] != nullptr;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {  // partial maxima of the 4 keys of this lane (no cross-lane step)
+        float tm = -1e30f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s[b][i] = ok[i] ? s[b][i] * sl2 : -1e30f;
+          tm = fmaxf(tm, s[b][i]);
+        }
+        smax[kb][g][32 * hb + 16 * b + l16] = tm;
+      }
+      if (t + 2 < ntiles) issue(t + 2);
+      lds_barrier();  // X
+      DSV41_TS(8 * (t % 6) + 1);
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int hl = 32 * hb + 16 * b + l16;
+        float tmax = smax[0][0][hl];
+#pragma unroll
+        for (int u = 1; u < 8; ++u) tmax = fmaxf(tmax, smax[u >> 2][u & 3][hl]);
+        const float m_new = tmax > m_ref[b] + kRescale ? tmax : m_ref[b];
+        const float alpha = __builtin_amdgcn_exp2f(m_ref[b] - m_new);  // v_exp_f32: arguments <= 0 here
+        l_run[b] *= alpha;
+        m_ref[b] = m_new;
+        if (kb == 0 && g == 0) salpha[t & 1][hl] = alpha;
+        float p[4], psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = __builtin_amdgcn_exp2f(s[b][i] - m_new);  // masked keys: 2^(-1e30 - m) = 0
+          psum += p[i];
+        }
+        pex[t & 1][2 * hb + b][kb][lane] = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
+        l_run[b] += psum;  // this lane's keys only; summed over the lane groups at the end
+      }
+    }
+    // per-head sums of both key halves (smax is free after the last X) and the normalisation factors
+    smax[kb][g][32 * hb + l16] = l_run[0];
+    smax[kb][g][32 * hb + 16 + l16] = l_run[1];
+    __syncthreads();  // E1
+    if (kb == 0 && g == 0) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int hl = 32 * hb + 16 * b + l16, h = hg64 * 64 + hl;
+        float l = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) l += smax[u >> 2][u & 3][hl];
+        hfac[hl] = 1.0f / (l + exp2f(a.sink[h < H ? h : H - 1] * kLog2e - m_ref[b]));
+      }
+    }
+    __syncthreads();  // E2
+  } else {
+    // O of heads 16b + 4g + i, columns cq*DV/4 + 16 ct + l16
+    f32x4_t o[4][CT];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int c = 0; c < CT; ++c) o[b][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    int ix_next = ntiles > 3 ? load_ix(3) : -1;  // resolver lanes: entries of tile t + 3, consumed in iteration t
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int t = 0; t <= ntiles; ++t) {
+      lds_barrier();  // B0
+      DSV41_TST(8 * (t % 6) + 4, 256);
+      if (t >= 1) {
+        const int tp = t - 1;
+        // rescale by the factors of tile t - 1, then o += P V over its 32 keys
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          float al[4];
+          bool any = false;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            al[i] = salpha[tp & 1][16 * b + 4 * g + i];
+            any = any || al[i] != 1.0f;
+          }
+          if (__ballot(any)) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) o[b][ct][i] *= al[i];
+          }
+        }
+        // 16x16x32 MFMA over the tile's 32 keys in the k order (4g + i, then 16 + 4g + i): the A operand of head
+        // block b is its two 16-key probability fragments side by side, the B operand two transposed V reads
+        const uint16_t* buf = ktile + (tp % NBUF) * TILE_ELEMS;
+        uint4 pa[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const uint2 p0 = pex[tp & 1][b][0][lane], p1 = pex[tp & 1][b][1][lane];
+          pa[b] = make_uint4(p0.x, p0.y, p1.x, p1.y);
+        }
+        const int vj = 4 * g + (l16 >> 2);  // key rows vj (first half) and vj + 16 (second half); (vj + 16) & 7 = vj & 7
+        const uint16_t* vrow = buf + vj * DQK + ((l16 & 1) << 2);
+        const int vsw = vj & 7;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          const int cch = ((cq * (DV / 4) + ct * 16) >> 3) + ((l16 & 3) >> 1);
+          const uint2 v0 = lds_read_tr16(vrow + ((cch ^ vsw) << 3));
+          const uint2 v1 = lds_read_tr16(vrow + 16 * DQK + ((cch ^ vsw) << 3));
+          const uint4 vb = make_uint4(v0.x, v0.y, v1.x, v1.y);
+#pragma unroll
+          for (int b = 0; b < 4; ++b) o[b][ct] = mfma_bf16_16x16x32(pa[b], vb, o[b][ct]);
+        }
+      }
+      DSV41_TST(8 * (t % 6) + 5, 256);
+      lds_barrier();  // X
+      DSV41_TST(8 * (t % 6) + 6, 256);
+      if (t >= ntiles) break;
+      if (t + 3 < ntiles) {  // wave 4: pointers of tile t + 3 (its slot last served tile t - 1's validity mask)
+        resolve(t + 3, ix_next);
+        ix_next = t + 4 < ntiles ? load_ix(t + 4) : -1;
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) stg[(16 * b + 4 * g + i) * DV + cq * (DV / 4) + ct * 16 + l16] = o[b][ct][i];
+    __syncthreads();  // E1
+    __syncthreads();  // E2
+  }
+  constexpr int CG = DV / 8;
+#pragma unroll 1
+  for (int e = tid; e < 64 * CG; e += 512) {
+    const int hl = e / CG, c = (e - hl * CG) * 8, h = hg64 * 64 + hl;
+    if (h >= H) continue;
+    const float f = hfac[hl];
+    const float4 x0 = *(const float4*)(stg + hl * DV + c), x1 = *(const float4*)(stg + hl * DV + c + 4);
+    *(uint4*)(a.out + (long)r * a.out_rstride + (long)h * DV + c) =
+        make_uint4(pack_bf16x2(x0.x * f, x0.y * f), pack_bf16x2(x0.z * f, x0.w * f), pack_bf16x2(x1.x * f, x1.y * f),
+                   pack_bf16x2(x1.z * f, x1.w * f));
+  }
+}
+
 // Merge bf16-normalised partials: out = sum_s w_s l_s o_s / (sum_s w_s l_s + exp(sink - M)), w_s = exp(m_s - M).
 // One workgroup per (row, 4 heads); thread -> (head, 8 consecutive columns); all split loads are independent.
 template <int DV>
@@ -1006,7 +1296,7 @@ int launch_attn(AttnArgs& a, hipStream_t st) {
   }
   dim3 grid(a.nsplit, (a.H + 63) / 64, a.R);
   if (a.nsplit == 1 && a.rd == 0) {  // (rows padded to a multiple of 8: contiguous row ranges per XCD)
-    attn_prefill_kernel<DQK, DV><<<dim3(1, grid.y, (a.R + kXcds - 1) / kXcds * kXcds), 512, 0, st>>>(a);
+    attn_prefill_ws_kernel<DQK, DV><<<dim3(1, grid.y, (a.R + kXcds - 1) / kXcds * kXcds), 512, 0, st>>>(a);
     DSV41_CHECK_LAUNCH();
     return 0;
   }

@@ -109,6 +109,11 @@ __device__ long long g_dsv41_ts[64];
   do {                                                                                                    \
     if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) g_dsv41_ts[i] = wall_clock64(); \
   } while (0)
+// As DSV41_TS, from thread `thr` of block (0,0,0).
+#define DSV41_TST(i, thr)                                                                                  \
+  do {                                                                                                     \
+    if (threadIdx.x == (thr) && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) g_dsv41_ts[i] = wall_clock64(); \
+  } while (0)
 // Per-workgroup start / end stamps (first 4096 workgroups of a launch, linear block id).
 __device__ long long g_dsv41_wg[4096][2];
 #define DSV41_WG_TS(k)                                                                                     \
@@ -132,6 +137,9 @@ __device__ long long g_dsv41_ck[1024][8];  // shader clock at the same points
   } while (0)
 #define DSV41_TS(i) \
   do {              \
+  } while (0)
+#define DSV41_TST(i, thr) \
+  do {                    \
   } while (0)
 #define DSV41_WG_TS(k) \
   do {                 \
