@@ -925,35 +925,36 @@ __global__ void __launch_bounds__(512) attn_prefill_kernel(const AttnArgs a) {
   }
 }
 
-// Many query rows, pipelined roles: the same work as attn_prefill_kernel (one workgroup per (query row, 64 heads),
-// whole key list) with 32-key tiles and the two halves of the tile work overlapped across waves:
+// Many query rows, pipelined roles: one workgroup per (query row, 64 heads), whole key list, 32-key tiles, and the
+// two halves of the tile work overlapped across waves:
 //   QK waves 0..3, w = (hb = w & 1: heads 32hb..32hb+31, kb = w >> 1: keys 16kb..16kb+15 of the tile): S for tile t
-//       (16x16x32 bf16 MFMA, Q of 32 heads in VGPRs, each K fragment used for two head blocks), the per-head tile
-//       maximum exchanged with the other key half, the probabilities (bf16, MFMA operand order) and the per-head
-//       rescale factor published through LDS.  These waves also gather the tiles (direct-to-LDS loads, two ahead).
-//   PV waves 4..7, cq = w - 4: O[64 heads x columns cq*DV/4 ..] += P V for tile t - 1 (16x16x16 bf16 MFMA, each
-//       transposed V fragment used for four head blocks).  Wave 4 also loads the index entries and resolves the
-//       row pointers three tiles ahead.
-// Four tile buffers: tile t (QK), t - 1 (PV), t + 1 and t + 2 (in flight).  Per tile two workgroup barriers:
-//   B0: tile t has landed, P / rescale of tile t - 1 and the pointers of tile t + 2 are visible;
-//   X:  both key halves' tile maxima of tile t are visible (and PV of tile t - 1 is done).
+//       (16x16x32 bf16 MFMA, Q of 32 heads in VGPRs, each K fragment used for two head blocks), per-lane partial
+//       maxima exchanged with the wave of the other key half through LDS (a flag word per wave, no workgroup
+//       barrier), then the probabilities (bf16, MFMA operand order) and the per-head rescale factor published through
+//       LDS.  Wave 0 also loads the index entries and resolves the row pointers three tiles ahead.
+//   PV waves 4..7, cq = w - 4: O[64 heads x columns cq*DV/4 ..] += P V for tile t - 1 (16x16x32 bf16 MFMA over the
+//       tile's 32 keys, each transposed V fragment used for four head blocks), interleaved with the direct-to-LDS
+//       gathers of tile t + 2 (counted vmcnt waits).
+// Four tile buffers: tile t (QK), t - 1 (PV), t + 1 and t + 2 (in flight).  One workgroup barrier per tile (B0):
+// tile t has landed; P / rescale of tile t - 1 and the row pointers of tile t + 2 are visible.
 template <int DQK, int DV>
 __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) {
   constexpr int KS = DQK / 32;  // 32-deep k steps of QK^T
   constexpr int CT = DV / 64;   // 16-column output tiles per PV wave (a quarter of DV)
   constexpr int U = DQK / 8;    // 16-byte chunks per row; chunk c of row j at j*U + (c ^ (j & 7))
-  static_assert(U % 8 == 0 && CT >= 1, "row widths");
+  static_assert(U % 8 == 0 && CT >= 1 && KS >= 2, "row widths");
   constexpr int TILE = 32, NBUF = 4;
   constexpr int TILE_ELEMS = TILE * DQK;
-  constexpr int kLd = TILE * U / 256;  // loads per QK-wave lane per tile
+  constexpr int kLd = TILE * U / 256;  // loads per PV-wave lane per tile
   static_assert(TILE * U % 256 == 0 && kLd < 16, "vmcnt immediate");
   static_assert(64 * DV * 4 <= NBUF * TILE_ELEMS * 2, "output staging fits the tile buffers");
   constexpr float kRescale = 8.0f;
   __shared__ __align__(16) uint16_t ktile[NBUF * TILE_ELEMS];
   __shared__ const uint16_t* rptr[NBUF][TILE];
   __shared__ uint2 pex[2][4][2][64];  // [tile parity][head block][key block][lane]
-  __shared__ float smax[2][4][64];    // [key half][lane group][head]; reused for the per-half sums at the end
-  __shared__ float salpha[2][64];     // [tile parity][head]: rescale factor (1 when the reference stays)
+  __shared__ float xmax[2][4][64];    // [key half][lane group][head]: partial maxima; at the end the partial sums
+  __shared__ int xflag[4];            // QK wave w: tiles whose partial maxima are in xmax
+  __shared__ __align__(16) float salpha[2][64];  // [tile parity][head]: rescale factor (1 when the reference stays)
   __shared__ float hfac[64];
 
   const int hg64 = blockIdx.y;
@@ -971,11 +972,11 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   const int* irow = a.t > 0 ? a.idx + (long)r * a.idx_rstride : nullptr;
   const int L = a.L;
   const int ntiles = (L + TILE - 1) / TILE;
-  const bool resolver = wave == 4 && lane < TILE;
-  auto load_ix = [&](int ti) {  // resolver lanes: index-list entry of key position ti*TILE + lane (or -1)
-    const int j = ti * TILE + lane;
+  // wave 0 loads index entries for two tiles at a time (tile 2u + (lane >> 5), key lane & 31) ...
+  auto load_ix2 = [&](int u) {
+    const int j = (2 * u + (lane >> 5)) * TILE + (lane & 31);
     const int jj = a.mode == 1 ? j - W : j;
-    return resolver && j < L && jj >= 0 && irow ? irow[jj] : -1;
+    return wave == 0 && j < L && jj >= 0 && irow ? irow[jj] : -1;
   };
   long slot, pos = 0, pmax = 0, plim = 0;
   if (a.mode == 1) {
@@ -988,9 +989,10 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   }
   const uint16_t* base1 = a.kv1 + slot * a.kv1_sstride;
   const uint16_t* base2 = a.kv2 ? a.kv2 + slot * a.kv2_sstride : nullptr;
-  auto resolve = [&](int ti, int ix) {  // resolver lanes: row pointer of key position ti*TILE + lane
-    if (resolver) {
-      const int j = ti * TILE + lane;
+  // ... and the lanes holding tile ti (half ti & 1 of the wave) resolve its row pointers
+  auto resolve = [&](int ti, int ix) {
+    if (wave == 0 && (lane >> 5) == (ti & 1)) {
+      const int j = ti * TILE + (lane & 31);
       const uint16_t* p = nullptr;
       if (j < L) {
         if (a.mode == 1 && j < W) {
@@ -1004,37 +1006,24 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
           p = ix < a.n1 ? base1 + (long)ix * DQK : base2 + (long)(ix - a.n1) * DQK;
         }
       }
-      rptr[ti % NBUF][lane] = p;
+      rptr[ti % NBUF][lane & 31] = p;
     }
-  };
-  auto issue = [&](int ti) {  // QK waves: direct-to-LDS 16-byte loads (inline assembly: no compiler waits)
-    uint16_t* buf = ktile + (ti % NBUF) * TILE_ELEMS;
-    const uint16_t* const* rp = rptr[ti % NBUF];
-    const uint16_t* src[kLd];  // all row pointers read before the first load (the loads clobber memory)
-#pragma unroll
-    for (int rd = 0; rd < kLd; ++rd) {
-      const int cc = rd * 256 + wave * 64 + lane;  // LDS chunk position
-      const int j = cc / U, cs = cc - j * U;
-      const int c = cs ^ (j & 7);
-      const uint16_t* p = rp[j];
-      src[rd] = p ? p + c * 8 : g_zero_row;
-    }
-#pragma unroll
-    for (int rd = 0; rd < kLd; ++rd) lds_dma16(src[rd], buf + (rd * 256 + wave * 64) * 8);
   };
 
   {
-    const int i0 = load_ix(0), i1 = load_ix(1), i2 = load_ix(2);
-    resolve(0, i0);
-    resolve(1, i1);
-    resolve(2, i2);
+    const int p0 = load_ix2(0), p1 = load_ix2(1);
+    resolve(0, p0);
+    resolve(1, p0);
+    resolve(2, p1);
   }
-  const float sl2 = a.scale * kLog2e;
+  if (tid < 4) xflag[tid] = 0;
   float* stg = (float*)ktile;  // output staging [64 heads][DV] once the tiles are done
+#define PF_TS(k, thr) \
+  if (t >= 30 && t < 34) DSV41_TST(16 * (t - 30) + (k), thr)
   // The two roles run separate loops (so Q and the O accumulators never share registers) with the same barrier
-  // sequence: one after the prologue, B0 and X per iteration t = 0..ntiles, two in the epilogue.
+  // sequence: one after the prologue, B0 per iteration t = 0..ntiles, two in the epilogue.
   if (qk) {
-    // Q of heads 32hb + 16b + l16 (B operand, k = 32 ks + 8 g ..); lazy reference and sum per head (log2 units)
+    // Q of heads 32hb + 16b + l16 (B operand, k = 32 ks + 8 g ..); lazy reference and per-lane sums (log2 units)
     uint4 qf[2][KS];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
@@ -1044,22 +1033,22 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
       for (int ks = 0; ks < KS; ++ks) qf[b][ks] = *(const uint4*)(qrow + ks * 32);
     }
     float m_ref[2] = {-1e30f, -1e30f}, l_run[2] = {0.0f, 0.0f};
-    __builtin_amdgcn_s_waitcnt(0);  // Q has arrived: the tile loads below are this wave's only loads
+    const float sl2 = a.scale * kLog2e;
+    // wave 0: index entries of tiles (t+3 rounded down to even, +1) in ix_cur, of the next pair in ix_nxt
+    int ix_cur = load_ix2(1), ix_nxt = load_ix2(2);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (ntiles > 0) issue(0);
-    if (ntiles > 1) issue(1);
     for (int t = 0; t <= ntiles; ++t) {
-      DSV41_TST(8 * (t % 6) + 2, 0);
-      if (t + 1 < ntiles)
-        __builtin_amdgcn_s_waitcnt(kLd | (0x7 << 4) | (0xf << 8));  // vmcnt(kLd): tile t has landed
-      else
-        __builtin_amdgcn_s_waitcnt(0);
-      DSV41_TST(8 * (t % 6) + 3, 0);
+      PF_TS(0, 0);
       lds_barrier();  // B0
-      DSV41_TS(8 * (t % 6) + 0);
-      if (t >= ntiles) {
-        lds_barrier();  // X
-        break;
+      PF_TS(1, 0);
+      if (t >= ntiles) break;
+      if (t + 3 < ntiles) {  // wave 0: pointers of tile t + 3 (its slot last served tile t - 1, now done)
+        resolve(t + 3, ix_cur);
+        if ((t + 3) & 1) {  // pair consumed: the next one moves up, the one after is loaded (two tiles ahead)
+          ix_cur = ix_nxt;
+          ix_nxt = load_ix2((t + 3) / 2 + 2);
+        }
       }
       const uint16_t* buf = ktile + (t % NBUF) * TILE_ELEMS;
       const int jr = 16 * kb + l16;
@@ -1067,37 +1056,51 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
       // base addresses and immediate offsets
       const uint16_t* kre = buf + jr * DQK + ((g ^ (jr & 3)) + (jr & 4)) * 8;
       const uint16_t* kro = kre - (jr & 4) * 16;
-      f32x4_t s[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+      f32x4_t s[2][2];  // [head block][k-step parity]: four independent accumulator chains
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const uint4 kf = *(const uint4*)((ks & 1 ? kro : kre) + ks * 32);
-        s[0] = mfma_bf16_16x16x32(kf, qf[0][ks], s[0]);
-        s[1] = mfma_bf16_16x16x32(kf, qf[1][ks], s[1]);
-      }
-      // s[b][i]: key 16kb + 4g + i of the tile, head 32hb + 16b + l16
+      for (int b = 0; b < 2; ++b) s[b][0] = s[b][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      uint4 kf[KS];  // the whole tile's K fragments (and the validity of its keys) are read first
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *(const uint4*)((ks & 1 ? kro : kre) + ks * 32);
       const uint16_t* const* rp = rptr[t % NBUF];
       bool ok[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) ok[i] = rp[16 * kb + 4 * g + i] != nullptr;
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {  // partial maxima of the 4 keys of this lane (no cross-lane step)
+      for (int ks = 0; ks < KS; ++ks) {
+        s[0][ks & 1] = mfma_bf16_16x16x32(kf[ks], qf[0][ks], s[0][ks & 1]);
+        s[1][ks & 1] = mfma_bf16_16x16x32(kf[ks], qf[1][ks], s[1][ks & 1]);
+      }
+      // sc[b][i]: key 16kb + 4g + i of the tile, head 32hb + 16b + l16 (scaled to log2 units, masked)
+      float sc[2][4];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {  // partial maxima of the 4 keys of this lane
         float tm = -1e30f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          s[b][i] = ok[i] ? s[b][i] * sl2 : -1e30f;
-          tm = fmaxf(tm, s[b][i]);
+          sc[b][i] = ok[i] ? (s[b][0][i] + s[b][1][i]) * sl2 : -1e30f;
+          tm = fmaxf(tm, sc[b][i]);
         }
-        smax[kb][g][32 * hb + 16 * b + l16] = tm;
+        xmax[kb][g][32 * hb + 16 * b + l16] = tm;
       }
-      if (t + 2 < ntiles) issue(t + 2);
-      lds_barrier();  // X
-      DSV41_TS(8 * (t % 6) + 1);
+      PF_TS(2, 0);
+      // pairwise exchange with wave w ^ 2 (same heads, other key half): LDS operations of a wave complete in order,
+      // so the flag is seen after the maxima; the partner read this wave's previous maxima before its B0
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): maxima written
+      if (lane == 0) __hip_atomic_store(&xflag[wave], t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      for (int spin = 0;  // bounded
+           __hip_atomic_load(&xflag[wave ^ 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < t + 1 && spin < (1 << 22);
+           ++spin)
+        __builtin_amdgcn_s_sleep(1);
+      __asm__ volatile("" ::: "memory");  // the partner's maxima are read after the flag
+      PF_TS(3, 0);
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         const int hl = 32 * hb + 16 * b + l16;
-        float tmax = smax[0][0][hl];
+        float tmax = xmax[0][0][hl];
 #pragma unroll
-        for (int u = 1; u < 8; ++u) tmax = fmaxf(tmax, smax[u >> 2][u & 3][hl]);
+        for (int u = 1; u < 8; ++u) tmax = fmaxf(tmax, xmax[u >> 2][u & 3][hl]);
         const float m_new = tmax > m_ref[b] + kRescale ? tmax : m_ref[b];
         const float alpha = __builtin_amdgcn_exp2f(m_ref[b] - m_new);  // v_exp_f32: arguments <= 0 here
         l_run[b] *= alpha;
@@ -1106,100 +1109,149 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
         float p[4], psum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          p[i] = __builtin_amdgcn_exp2f(s[b][i] - m_new);  // masked keys: 2^(-1e30 - m) = 0
+          p[i] = __builtin_amdgcn_exp2f(sc[b][i] - m_new);  // masked keys: 2^(-1e30 - m) = 0
           psum += p[i];
         }
         pex[t & 1][2 * hb + b][kb][lane] = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
         l_run[b] += psum;  // this lane's keys only; summed over the lane groups at the end
       }
     }
-    // per-head sums of both key halves (smax is free after the last X) and the normalisation factors
-    smax[kb][g][32 * hb + l16] = l_run[0];
-    smax[kb][g][32 * hb + 16 + l16] = l_run[1];
-    __syncthreads();  // E1
+    // per-head sums over both key halves and the 4 lane groups, normalisation factors
+    __syncthreads();  // E1: every wave is past its last read of xmax
+    xmax[kb][g][32 * hb + l16] = l_run[0];
+    xmax[kb][g][32 * hb + 16 + l16] = l_run[1];
+    lds_barrier();  // QK waves only see each other's sums after this (the PV waves pass it too)
     if (kb == 0 && g == 0) {
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         const int hl = 32 * hb + 16 * b + l16, h = hg64 * 64 + hl;
         float l = 0.0f;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) l += smax[u >> 2][u & 3][hl];
+        for (int u = 0; u < 8; ++u) l += xmax[u >> 2][u & 3][hl];
         hfac[hl] = 1.0f / (l + exp2f(a.sink[h < H ? h : H - 1] * kLog2e - m_ref[b]));
       }
     }
-    __syncthreads();  // E2
+    __syncthreads();  // E3
   } else {
+    // gathers: LDS chunk position cc = rd*256 + cq*64 + lane holds chunk (cc % U) ^ (row & 7) of row cc / U; the
+    // (row, byte offset) of each load is fixed per lane, packed as row << 16 | offset
+    uint32_t gsrc[kLd];
+#pragma unroll
+    for (int rd = 0; rd < kLd; ++rd) {
+      const int cc = rd * 256 + cq * 64 + lane;
+      const int j = cc / U, cs = cc - j * U;
+      gsrc[rd] = ((uint32_t)j << 16) | (uint32_t)((cs ^ (j & 7)) * 16);
+    }
+    const uint16_t* src[kLd];  // gather sources of a tile, read before the first load (the loads clobber memory)
+    auto sources = [&](int ti) {
+      const uint16_t* const* rp = rptr[ti % NBUF];
+#pragma unroll
+      for (int rd = 0; rd < kLd; ++rd) {
+        const uint16_t* p = rp[gsrc[rd] >> 16];
+        src[rd] = p ? (const uint16_t*)((const char*)p + (gsrc[rd] & 0xffff)) : g_zero_row;
+      }
+    };
+    auto dma = [&](int ti, int rd) {  // direct-to-LDS 16-byte load (inline assembly: no compiler waits around it)
+      lds_dma16(src[rd], ktile + (ti % NBUF) * TILE_ELEMS + (rd * 256 + cq * 64) * 8);
+    };
     // O of heads 16b + 4g + i, columns cq*DV/4 + 16 ct + l16
     f32x4_t o[4][CT];
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int c = 0; c < CT; ++c) o[b][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    int ix_next = ntiles > 3 ? load_ix(3) : -1;  // resolver lanes: entries of tile t + 3, consumed in iteration t
-    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if (ntiles > 0) {
+      sources(0);
+#pragma unroll
+      for (int rd = 0; rd < kLd; ++rd) dma(0, rd);
+    }
+    if (ntiles > 1) {
+      sources(1);
+#pragma unroll
+      for (int rd = 0; rd < kLd; ++rd) dma(1, rd);
+    }
+    const int vj = 4 * g + (l16 >> 2);  // key rows vj (first half) and vj + 16 (second half); (vj + 16) & 7 = vj & 7
+    const int vsw = vj & 7;
     for (int t = 0; t <= ntiles; ++t) {
+      PF_TS(8, 256);
+      if (t < ntiles) {
+        if (t + 1 < ntiles)
+          __builtin_amdgcn_s_waitcnt(kLd | (0x7 << 4) | (0xf << 8));  // vmcnt(kLd): tile t has landed
+        else
+          __builtin_amdgcn_s_waitcnt(0);
+      }
+      PF_TS(9, 256);
       lds_barrier();  // B0
-      DSV41_TST(8 * (t % 6) + 4, 256);
-      if (t >= 1) {
-        const int tp = t - 1;
-        // rescale by the factors of tile t - 1, then o += P V over its 32 keys
+      PF_TS(10, 256);
+      // PV of tile t - 1, interleaved with the gathers of tile t + 2 into buffer (t + 2) % NBUF (free since the PV of
+      // tile t - 2; its pointers were resolved in iteration t - 1)
+      const int tp = t - 1;
+      const bool mm = t >= 1, gather = t + 2 < ntiles;
+      if (gather) sources(t + 2);
+      const uint16_t* vrow = ktile + (tp % NBUF) * TILE_ELEMS + vj * DQK + ((l16 & 1) << 2);
+      auto vread = [&](int ct) {
+        const int cch = ((cq * (DV / 4) + ct * 16) >> 3) + ((l16 & 3) >> 1);
+        const uint2 v0 = lds_read_tr16(vrow + ((cch ^ vsw) << 3));
+        const uint2 v1 = lds_read_tr16(vrow + 16 * DQK + ((cch ^ vsw) << 3));
+        return make_uint4(v0.x, v0.y, v1.x, v1.y);
+      };
+      // every LDS read of the tile first (rescale factors of heads 16b + 4g .. + 3, P fragments, V fragments),
+      // before the gathers (which clobber memory): one LDS latency per tile
+      uint4 pa[4], vb[CT];
+      float4 al[4];
+      if (mm) {
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          float al[4];
-          bool any = false;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            al[i] = salpha[tp & 1][16 * b + 4 * g + i];
-            any = any || al[i] != 1.0f;
-          }
-          if (__ballot(any)) {
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) o[b][ct][i] *= al[i];
-          }
-        }
-        // 16x16x32 MFMA over the tile's 32 keys in the k order (4g + i, then 16 + 4g + i): the A operand of head
-        // block b is its two 16-key probability fragments side by side, the B operand two transposed V reads
-        const uint16_t* buf = ktile + (tp % NBUF) * TILE_ELEMS;
-        uint4 pa[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
+          al[b] = *(const float4*)&salpha[tp & 1][16 * b + 4 * g];
+          // 16x16x32 MFMA over the tile's 32 keys in the k order (4g + i, then 16 + 4g + i): the A operand of
+          // head block b is its two 16-key probability fragments side by side, the B operand two transposed V reads
           const uint2 p0 = pex[tp & 1][b][0][lane], p1 = pex[tp & 1][b][1][lane];
           pa[b] = make_uint4(p0.x, p0.y, p1.x, p1.y);
         }
-        const int vj = 4 * g + (l16 >> 2);  // key rows vj (first half) and vj + 16 (second half); (vj + 16) & 7 = vj & 7
-        const uint16_t* vrow = buf + vj * DQK + ((l16 & 1) << 2);
-        const int vsw = vj & 7;
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          const int cch = ((cq * (DV / 4) + ct * 16) >> 3) + ((l16 & 3) >> 1);
-          const uint2 v0 = lds_read_tr16(vrow + ((cch ^ vsw) << 3));
-          const uint2 v1 = lds_read_tr16(vrow + 16 * DQK + ((cch ^ vsw) << 3));
-          const uint4 vb = make_uint4(v0.x, v0.y, v1.x, v1.y);
+        for (int ct = 0; ct < CT; ++ct) vb[ct] = vread(ct);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+      if (mm) {  // rescale by the factors of tile t - 1 (rarely needed: skipped unless some factor differs from 1)
 #pragma unroll
-          for (int b = 0; b < 4; ++b) o[b][ct] = mfma_bf16_16x16x32(pa[b], vb, o[b][ct]);
+        for (int b = 0; b < 4; ++b) {
+          const bool any = al[b].x != 1.0f || al[b].y != 1.0f || al[b].z != 1.0f || al[b].w != 1.0f;
+          if (__ballot(any)) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+              o[b][ct][0] *= al[b].x;
+              o[b][ct][1] *= al[b].y;
+              o[b][ct][2] *= al[b].z;
+              o[b][ct][3] *= al[b].w;
+            }
+          }
         }
       }
-      DSV41_TST(8 * (t % 6) + 5, 256);
-      lds_barrier();  // X
-      DSV41_TST(8 * (t % 6) + 6, 256);
-      if (t >= ntiles) break;
-      if (t + 3 < ntiles) {  // wave 4: pointers of tile t + 3 (its slot last served tile t - 1's validity mask)
-        resolve(t + 3, ix_next);
-        ix_next = t + 4 < ntiles ? load_ix(t + 4) : -1;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        if (gather) {
+#pragma unroll
+          for (int rd = ct * kLd / CT; rd < (ct + 1) * kLd / CT; ++rd) dma(t + 2, rd);
+        }
+        if (mm) {
+#pragma unroll
+          for (int b = 0; b < 4; ++b) o[b][ct] = mfma_bf16_16x16x32(pa[b], vb[ct], o[b][ct]);
+        }
       }
+      PF_TS(11, 256);
     }
+    __syncthreads();  // E1: every PV wave is past its last V read, so the tile buffers can take the output
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
         for (int i = 0; i < 4; ++i) stg[(16 * b + 4 * g + i) * DV + cq * (DV / 4) + ct * 16 + l16] = o[b][ct][i];
-    __syncthreads();  // E1
-    __syncthreads();  // E2
+    lds_barrier();    // E2
+    __syncthreads();  // E3
   }
+#undef PF_TS
   constexpr int CG = DV / 8;
 #pragma unroll 1
   for (int e = tid; e < 64 * CG; e += 512) {
