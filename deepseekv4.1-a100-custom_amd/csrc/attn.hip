@@ -153,8 +153,7 @@ __global__ void __launch_bounds__(256) attn_split_kernel(const AttnArgs a) {
       p[e] = x;
       tmax = fmaxf(tmax, x);
     }
-    tmax = fmaxf(tmax, wave_shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, wave_shfl_xor(tmax, 32));
+    tmax = row_max4(tmax);
     const float m_new = fmaxf(m_run, tmax);
     const float alpha = exp2f((m_run - m_new) * kLog2e);
     float psum = 0.0f;
@@ -164,8 +163,7 @@ __global__ void __launch_bounds__(256) attn_split_kernel(const AttnArgs a) {
       p[e] = rptr[row] ? exp2f((p[e] - m_new) * kLog2e) : 0.0f;
       psum += p[e];
     }
-    psum += wave_shfl_xor(psum, 16);
-    psum += wave_shfl_xor(psum, 32);
+    psum = row_sum4(psum);
     l_run = alpha * l_run + psum;
     m_run = m_new;
 
@@ -520,8 +518,7 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
       x[i] = rp[rb + 4 * g + i] ? s[i] * sl2 : -1e30f;
       tmax = fmaxf(tmax, x[i]);
     }
-    tmax = fmaxf(tmax, wave_shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, wave_shfl_xor(tmax, 32));
+    tmax = row_max4(tmax);
     const bool bump = tmax > m_ref + kRescale;
     if (__ballot(bump)) {  // wave-uniform: some head of this wave needs a new reference
       const float m_new = bump ? tmax : m_ref;
@@ -543,8 +540,7 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
       p[i] = rp[rb + 4 * g + i] ? exp2f(x[i] - m_ref) : 0.0f;
       psum += p[i];
     }
-    psum += wave_shfl_xor(psum, 16);
-    psum += wave_shfl_xor(psum, 32);
+    psum = row_sum4(psum);
     l_run += psum;
     const uint2 pa = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
     // V operand: lane (column l16 of the 16-column tile, rows rb + 4g .. +3) via the transpose read: input lane
@@ -826,8 +822,7 @@ __global__ void __launch_bounds__(512) attn_prefill_kernel(const AttnArgs a) {
         s[b][i] = rp[32 * kh + 16 * b + 4 * g + i] ? s[b][i] * sl2 : -1e30f;
         tmax = fmaxf(tmax, s[b][i]);
       }
-    tmax = fmaxf(tmax, wave_shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, wave_shfl_xor(tmax, 32));
+    tmax = row_max4(tmax);
     if (g == 0) smax[hb][kh][l16] = tmax;
     lds_barrier();
     tmax = fmaxf(smax[hb][0][l16], smax[hb][1][l16]);  // both key halves: the tile maximum of the head
@@ -849,8 +844,7 @@ __global__ void __launch_bounds__(512) attn_prefill_kernel(const AttnArgs a) {
         }
         pex[hb][2 * kh + b][lane] = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
       }
-      psum += wave_shfl_xor(psum, 16);
-      psum += wave_shfl_xor(psum, 32);
+      psum = row_sum4(psum);
       l_run += psum;
     }
     lds_barrier();

@@ -83,6 +83,24 @@ DSV41_DEV uint32_t score_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// max(x, 0) for finite x in one v_med3_f32 (fmaxf adds a canonicalisation of its MFMA-produced operand).
+DSV41_DEV float relu(float x) { return __builtin_amdgcn_fmed3f(x, 0.0f, 3.402823466e38f); }
+
+// Sum / max over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48), result in every lane: two VALU row
+// swaps (v_permlane32_swap, v_permlane16_swap) instead of LDS-routed shuffles.
+DSV41_DEV float row_sum4(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+DSV41_DEV float row_max4(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 template <typename T>
 DSV41_DEV T wave_shfl_xor(T v, int m) {
   return __shfl_xor(v, m, 64);

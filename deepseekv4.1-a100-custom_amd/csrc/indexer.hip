@@ -138,6 +138,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
 constexpr int kPQ = 8;       // query rows per workgroup
 constexpr int kPChunk = 256;  // keys per LDS chunk (32 KB)
 
+template <int NHT>  // 16-head tiles: ceil(HI / 16)
 __global__ void __launch_bounds__(256) index_score_prefill_kernel(const ScoreArgs a, int key_split) {
   __shared__ __align__(16) uint8_t kbuf[2][kPChunk * 128];
   __shared__ float sbuf[2][kPChunk];
@@ -175,7 +176,7 @@ __global__ void __launch_bounds__(256) index_score_prefill_kernel(const ScoreArg
   // query fragments of this wave's 2 rows and their head weights
   i32x8_t qa[2][kHT];
   float wr[2][kHT][4];
-  const int nht = (a.HI + 15) / 16;
+  constexpr int nht = NHT;
 #pragma unroll
   for (int qq = 0; qq < 2; ++qq) {
     const int r = min(r0 + wave * 2 + qq, a.R - 1);
@@ -226,11 +227,10 @@ __global__ void __launch_bounds__(256) index_score_prefill_kernel(const ScoreArg
           if (ht < nht) {
             const f32x4_t acc = mfma_fp8_16x16x128(qa[qq][ht], bfrag, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sum += wr[qq][ht][i] * fmaxf(acc[i], 0.0f);
+            for (int i = 0; i < 4; ++i) sum += wr[qq][ht][i] * relu(acc[i]);
           }
         }
-        sum += wave_shfl_xor(sum, 16);
-        sum += wave_shfl_xor(sum, 32);
+        sum = row_sum4(sum);
         if (g == 0 && rows[qq] < a.R && t < clr[qq] && t < kb1)
           a.out[(long)rows[qq] * a.out_rstride + t] = sum * ksc;
       }
@@ -505,7 +505,12 @@ int launch_score(ScoreArgs& a, hipStream_t st) {
     const int qblocks = (a.R + kPQ - 1) / kPQ;
     int split = (512 + qblocks - 1) / qblocks;
     split = split < 1 ? 1 : (split > 16 ? 16 : split);
-    index_score_prefill_kernel<<<dim3(split, qblocks), 256, 0, st>>>(a, split);
+    switch ((a.HI + 15) / 16) {
+      case 1: index_score_prefill_kernel<1><<<dim3(split, qblocks), 256, 0, st>>>(a, split); break;
+      case 2: index_score_prefill_kernel<2><<<dim3(split, qblocks), 256, 0, st>>>(a, split); break;
+      case 3: index_score_prefill_kernel<3><<<dim3(split, qblocks), 256, 0, st>>>(a, split); break;
+      default: index_score_prefill_kernel<4><<<dim3(split, qblocks), 256, 0, st>>>(a, split); break;
+    }
     DSV41_CHECK_LAUNCH();
     return 0;
   }

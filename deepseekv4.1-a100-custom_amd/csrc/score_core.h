@@ -61,9 +61,8 @@ DSV41_DEV float score_tile(const i32x8_t (&qa8)[kHT], const uint4 (&qa16)[kHT][4
 #pragma unroll
   for (int ht = 0; ht < kHT; ++ht)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sum += wr[ht][i] * fmaxf(acc[ht][i], 0.0f);
-  sum += wave_shfl_xor(sum, 16);
-  sum += wave_shfl_xor(sum, 32);
+    for (int i = 0; i < 4; ++i) sum += wr[ht][i] * relu(acc[ht][i]);
+  sum = row_sum4(sum);
   return sum;
 }
 

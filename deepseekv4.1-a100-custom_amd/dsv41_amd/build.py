@@ -18,7 +18,7 @@ OBJ = PKG.parent / "_build"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
-         "-packed-fp32-ops", f"-I{INCLUDE}", f"-I{CSRC}"]
+         "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form=1", f"-I{INCLUDE}", f"-I{CSRC}"]
 
 
 def _compile(src: Path, extra=(), tag: str = "") -> Path:
