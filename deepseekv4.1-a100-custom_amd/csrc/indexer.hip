@@ -208,31 +208,48 @@ __global__ void __launch_bounds__(256) index_score_prefill_kernel(const ScoreArg
     const uint8_t* kb = kbuf[ci & 1];
     const float* sb = sbuf[ci & 1];
     const long wave_lim = clr[1] > clr[0] ? clr[1] : clr[0];
-#pragma unroll 2
-    for (int kt = 0; kt < kPChunk / 16; ++kt) {
+    // two 16-key tiles per step: all 2 x 2 x NHT MFMAs first, then the epilogues (the first tile's VALU work covers
+    // the second tile's MFMA latency)
+#pragma unroll 1
+    for (int kt = 0; kt < kPChunk / 16; kt += 2) {
       const int t0 = c0 + kt * 16;
       if (t0 >= kb1 || t0 >= wave_lim) break;  // wave-uniform
-      const int kl = kt * 16 + l16;
-      const uint4 k0 = *(const uint4*)(kb + kl * 128 + (((2 * g) ^ (kl & 7)) << 4));
-      const uint4 k1 = *(const uint4*)(kb + kl * 128 + (((2 * g + 1) ^ (kl & 7)) << 4));
-      const i32x8_t bfrag = i32x8_t{(int)k0.x, (int)k0.y, (int)k0.z, (int)k0.w, (int)k1.x, (int)k1.y, (int)k1.z,
-                                    (int)k1.w};
-      const float ksc = sb[kt * 16 + l16];
-      const int t = t0 + l16;
+      f32x4_t acc[2][2][kHT];  // [tile][row][head tile]
+      float ksc[2];
 #pragma unroll
-      for (int qq = 0; qq < 2; ++qq) {
-        float sum = 0.0f;
+      for (int u = 0; u < 2; ++u) {
+        const int kl = (kt + u) * 16 + l16;
+        const uint4 k0 = *(const uint4*)(kb + kl * 128 + (((2 * g) ^ (kl & 7)) << 4));
+        const uint4 k1 = *(const uint4*)(kb + kl * 128 + (((2 * g + 1) ^ (kl & 7)) << 4));
+        const i32x8_t bfrag = i32x8_t{(int)k0.x, (int)k0.y, (int)k0.z, (int)k0.w, (int)k1.x, (int)k1.y, (int)k1.z,
+                                      (int)k1.w};
+        ksc[u] = sb[kl];
 #pragma unroll
-        for (int ht = 0; ht < kHT; ++ht) {
-          if (ht < nht) {
-            const f32x4_t acc = mfma_fp8_16x16x128(qa[qq][ht], bfrag, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
+        for (int qq = 0; qq < 2; ++qq)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sum += wr[qq][ht][i] * relu(acc[i]);
-          }
+          for (int ht = 0; ht < nht; ++ht)
+            acc[u][qq][ht] = mfma_fp8_16x16x128(qa[qq][ht], bfrag, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
+      }
+      // every MFMA of the step is issued before the epilogues start (the empty statements pin the results here)
+      if constexpr (NHT == 4)
+        __asm__ volatile("" : "+v"(acc[0][0][0]), "+v"(acc[0][0][1]), "+v"(acc[0][0][2]), "+v"(acc[0][0][3]),
+                         "+v"(acc[0][1][0]), "+v"(acc[0][1][1]), "+v"(acc[0][1][2]), "+v"(acc[0][1][3]),
+                         "+v"(acc[1][0][0]), "+v"(acc[1][0][1]), "+v"(acc[1][0][2]), "+v"(acc[1][0][3]),
+                         "+v"(acc[1][1][0]), "+v"(acc[1][1][1]), "+v"(acc[1][1][2]), "+v"(acc[1][1][3]));
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = t0 + u * 16 + l16;
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+          float sum = 0.0f;
+#pragma unroll
+          for (int ht = 0; ht < nht; ++ht)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum += wr[qq][ht][i] * relu(acc[u][qq][ht][i]);
+          sum = row_sum4(sum);
+          if (g == 0 && rows[qq] < a.R && t < clr[qq] && t < kb1)
+            a.out[(long)rows[qq] * a.out_rstride + t] = sum * ksc[u];
         }
-        sum = row_sum4(sum);
-        if (g == 0 && rows[qq] < a.R && t < clr[qq] && t < kb1)
-          a.out[(long)rows[qq] * a.out_rstride + t] = sum * ksc;
       }
     }
   }
