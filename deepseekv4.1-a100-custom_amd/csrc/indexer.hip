@@ -600,7 +600,7 @@ int dsv41_topk_indices(const float* score, long ld, int R, int n, int k, const l
   a.out = out;
   a.out_rstride = out_rstride;
   a.offset = offset;
-  if (R >= 512 && n <= 17408) topk_kernel<256, 17408><<<R, 256, 0, (hipStream_t)stream>>>(a);  // many short rows
+  if (R >= 512 && n <= 17408) topk_kernel<512, 17408><<<R, 512, 0, (hipStream_t)stream>>>(a);  // many short rows
   else topk_kernel<1024, 32768><<<R, 1024, 0, (hipStream_t)stream>>>(a);
   DSV41_CHECK_LAUNCH();
   return 0;
