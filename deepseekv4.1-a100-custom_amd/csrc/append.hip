@@ -191,11 +191,30 @@ struct KvWriteArgs {
   int D, rd;
   float eps;
   int commit_from;
+  // prefill window (one sequence, positions pos0 + r): the ring's history rows of positions pos0 - hist .. pos0 - 1
+  // are copied to hist_tmp[0 .. hist) before the chunk overwrites their slots; blocks n_chunk .. n_chunk + hist - 1
+  // copy the history rows whose slot no committed chunk row overwrites
+  uint16_t* hist_tmp;
+  int hist, n_chunk;
 };
+
+// Copy ring row `slot` of sequence s to dst (the whole block, 16-byte units; the row width is a multiple of 8).
+DSV41_DEV void copy_ring_row(const KvWriteArgs& a, long s, long slot, uint16_t* dst) {
+  const uint4* src = (const uint4*)(a.cache + s * a.cache_sstride + slot * (long)a.D);
+  for (int u = threadIdx.x; u < a.D / 8; u += blockDim.x) ((uint4*)dst)[u] = src[u];
+}
 
 __global__ void __launch_bounds__(kRowThreads) kv_write_kernel(const KvWriteArgs a) {
   __shared__ float red[4];
   const int r = blockIdx.x;
+  if (a.hist_tmp && r >= a.n_chunk) {  // history row whose slot is not overwritten by the chunk
+    const int h = r - a.n_chunk;
+    const long q = a.pos0 - a.hist + h;
+    const long r0 = ((q - a.pos0) % a.W + a.W) % a.W;  // chunk row offset that maps to the same slot
+    const bool overwritten = r0 < a.n_chunk;  // some committed row r0 + k*W lies in [commit_from, n_chunk)
+    if (!overwritten) copy_ring_row(a, 0, q % a.W, a.hist_tmp + (long)h * a.D);
+    return;
+  }
   long p = a.pos ? a.pos[r] : a.pos0 + (long)(r % a.rows_per_seq) * a.pos_stride;
   p = p < 0 ? 0 : p;
   const long s = a.seq ? a.seq[r] : (long)(r / a.rows_per_seq);
@@ -212,6 +231,12 @@ __global__ void __launch_bounds__(kRowThreads) kv_write_kernel(const KvWriteArgs
   o.group = 32;
   o.out = r >= a.commit_from ? a.cache + s * a.cache_sstride + (p % a.W) * (long)a.D : nullptr;
   o.out2 = a.tmp ? a.tmp + (long)r * a.D : nullptr;
+  if (a.hist_tmp && o.out) {  // the slot's previous row (position p - W .. p - 1 congruent to p) leaves first
+    const long q_old = a.pos0 - a.W + (p - a.pos0) % a.W;
+    const long h = q_old - (a.pos0 - a.hist);
+    if (h >= 0 && h < a.hist) copy_ring_row(a, s, p % a.W, a.hist_tmp + h * a.D);
+    __syncthreads();  // every thread's reads of the old row are complete before row_op writes the slot
+  }
   row_op(o, red);
 }
 
@@ -414,8 +439,24 @@ int dsv41_kv_write(const void* x, long x_rstride, const void* w, const float* co
   if (!row_ok(D, 32) || rd % 2 != 0 || rd > D || W <= 0) return (int)hipErrorInvalidValue;
   KvWriteArgs a{(const uint16_t*)x, x_rstride, (const uint16_t*)w, cos_t, sin_t, pos, seq, pos0, pos_stride,
                 rows_per_seq > 0 ? rows_per_seq : 1, (uint16_t*)cache, cache_sstride, W, (uint16_t*)tmp, D, rd, eps,
-                commit_from};
+                commit_from, nullptr, 0, n_rows};
   kv_write_kernel<<<n_rows, kRowThreads, 0, (hipStream_t)stream>>>(a);
+  DSV41_CHECK_LAUNCH();
+  return 0;
+}
+
+int dsv41_window_kv(const void* x, long x_rstride, const void* w, const float* cos_t, const float* sin_t,
+                    long start_pos, int n_rows, void* ring, int W, void* out, int hist, int D, int rd, float eps,
+                    void* stream) {
+  if (n_rows <= 0) return 0;
+  if (!row_ok(D, 32) || D % 8 != 0 || rd % 2 != 0 || rd > D || W <= 0 || start_pos < 0 || hist < 0 ||
+      hist > W - 1 || hist > start_pos)
+    return (int)hipErrorInvalidValue;
+  uint16_t* o = (uint16_t*)out;
+  KvWriteArgs a{(const uint16_t*)x, x_rstride, (const uint16_t*)w, cos_t, sin_t, nullptr, nullptr, start_pos, 1,
+                n_rows, (uint16_t*)ring, 0, W, o + (long)hist * D, D, rd, eps, n_rows > W ? n_rows - W : 0,
+                hist > 0 ? o : nullptr, hist, n_rows};
+  kv_write_kernel<<<n_rows + hist, kRowThreads, 0, (hipStream_t)stream>>>(a);
   DSV41_CHECK_LAUNCH();
   return 0;
 }

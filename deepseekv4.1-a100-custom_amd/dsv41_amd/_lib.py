@@ -29,6 +29,7 @@ SIGNATURES = {
     "dsv41_select_topk": [_P, _L, _I, _I, _I, _P, _I, _P, _L, _P, _L, _P],
     "dsv41_topk_indices": [_P, _L, _I, _I, _I, _P, _L, _I, _I, _I, _P, _L, _P],
     "dsv41_kv_write": [_P, _L, _P, _P, _P, _P, _P, _L, _L, _I, _P, _L, _I, _P, _I, _I, _I, _F, _I, _P],
+    "dsv41_window_kv": [_P, _L, _P, _P, _P, _L, _I, _P, _I, _P, _I, _I, _I, _F, _P],
     "dsv41_append_rows": [_P, _L, _P, _F, _P, _P, _I, _P, _L, _L, _L, _P, _I, _P, _L, _P, _L, _I, _I, _P, _L, _P, _L,
                           _I, _I, _P],
     "dsv41_decode_appends": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _I, _P, _P,

@@ -12,9 +12,27 @@ import torch
 from ._lib import as_i64, call, ptr, require_gpu, stream
 
 
+_WIDX = {}  # window index tensors by shape: functions of (window, bsz, seqlen, start_pos or history length) only
+
+
+def _cached_idx(key, make):
+    t = _WIDX.get(key)
+    if t is None:
+        if len(_WIDX) > 256:
+            _WIDX.clear()
+        t = _WIDX[key] = make()
+    return t
+
+
 def window_topk_idxs(window: int, bsz: int, seqlen: int, start_pos: int, device) -> torch.Tensor:
     """get_window_topk_idxs (dsv41/model.py:132-254): physical ring slots (start_pos > 0) or temporary-row
-    positions (start_pos == 0) of every query's causal window, -1 invalid; int32 [bsz, seqlen, width]."""
+    positions (start_pos == 0) of every query's causal window, -1 invalid; int32 [bsz, seqlen, width].  The result
+    is cached per shape and must not be written to."""
+    return _cached_idx(("slots", window, bsz, seqlen, start_pos, str(device)),
+                       lambda: _window_topk_idxs(window, bsz, seqlen, start_pos, device))
+
+
+def _window_topk_idxs(window: int, bsz: int, seqlen: int, start_pos: int, device) -> torch.Tensor:
     if seqlen <= 0:
         return torch.empty((bsz, 0, 0), dtype=torch.int32, device=device)
     if start_pos == 0:
@@ -49,21 +67,19 @@ def window_kv(kv_raw: torch.Tensor, norm_w: torch.Tensor, eps: float, cos: torch
         return ring[:b], window_topk_idxs(W, b, 1, start_pos, dev)
     hist = min(int(start_pos), W - 1)
     tmp = torch.empty(b, hist + s, d, device=dev, dtype=kv_raw.dtype)
-    if hist:
-        slots = torch.remainder(torch.arange(start_pos - hist, start_pos, device=dev), W)
-        tmp[:, :hist] = ring[:b, slots]
-    chunk = tmp[:, hist:]
-    # one launch per batch row keeps the temporary row stride (hist + s) explicit
+    # one launch per batch row: history copy-out (before the commit), chunk rows, ring commit
     for bi in range(b):
-        call("dsv41_kv_write", ptr(x[bi * s:(bi + 1) * s]), d, ptr(w), ptr(cos), ptr(sin), None, None, start_pos, 1, s,
-             ptr(ring[bi:bi + 1]), ring.stride(0), W, ptr(chunk[bi]), s, d, rd, float(eps), max(0, s - W), st)
+        call("dsv41_window_kv", ptr(x[bi * s:(bi + 1) * s]), d, ptr(w), ptr(cos), ptr(sin), int(start_pos), s,
+             ptr(ring[bi:bi + 1]), W, ptr(tmp[bi]), hist, d, rd, float(eps), st)
     if start_pos == 0:
         return tmp, window_topk_idxs(W, b, s, 0, dev)
-    width = min(W, hist + s)
-    qq = (hist + torch.arange(s, device=dev)).unsqueeze(1)
-    idx = (qq - W + 1).clamp_min(0) + torch.arange(width, device=dev).unsqueeze(0)
-    idx = torch.where(idx <= qq, idx, -1).to(torch.int32).unsqueeze(0).expand(b, -1, -1).contiguous()
-    return tmp, idx
+
+    def make():
+        width = min(W, hist + s)
+        qq = (hist + torch.arange(s, device=dev)).unsqueeze(1)
+        idx = (qq - W + 1).clamp_min(0) + torch.arange(width, device=dev).unsqueeze(0)
+        return torch.where(idx <= qq, idx, -1).to(torch.int32).unsqueeze(0).expand(b, -1, -1).contiguous()
+    return tmp, _cached_idx(("hist", W, b, s, hist, str(dev)), make)
 
 
 def write_compress_kv(cache: torch.Tensor, latent: torch.Tensor, start_pos: int, ratio: int, cos: torch.Tensor,

@@ -115,6 +115,15 @@ int dsv41_kv_write(const void* x, long x_rstride, const void* w, const float* co
                    long cache_sstride, int W, void* tmp, int n_rows, int D, int rd, float eps, int commit_from,
                    void* stream);
 
+/* Attention._window_kv for a prefill chunk of one sequence (dsv41/model.py:1057-1298, the continuation copy
+ * :1170-1298): out = [history | chunk] with history = ring rows of positions start_pos - hist .. start_pos - 1
+ * (copied out before the commit), chunk row r = fq8(rope(rmsnorm(x[r]))) at position start_pos + r; the last
+ * min(n_rows, W) chunk rows are committed to ring[(start_pos + r) % W].  ring is the sequence's [W, D] block, out
+ * [hist + n_rows, D]; 0 <= hist <= min(start_pos, W - 1). */
+int dsv41_window_kv(const void* x, long x_rstride, const void* w, const float* cos_t, const float* sin_t,
+                    long start_pos, int n_rows, void* ring, int W, void* out, int hist, int D, int rd, float eps,
+                    void* stream);
+
 /* Compressed-KV append (dsv41/decode.py:157-164, dsv41/model.py:1320-1348, SharedAttn.write_compress_kv :508-541)
  * and index-key append (dsv41/decode.py:270-282, dsv41/model.py:696-732, SharedAttn.write_index_k :543-574):
  * row r of x -> [rmsnorm(norm_w)] -> [rope(last rd) at (pos[r] or pos0 + (r % rows_per_seq)*pos_stride) + pos_add] -> fake quant

@@ -377,6 +377,24 @@ def kv_write(x, w, cos, sin, pos, seq, cache, rd, eps) -> np.ndarray:
     return cache
 
 
+def window_kv(x, w, cos, sin, start_pos: int, ring, rd, eps):
+    """Attention._window_kv (dsv41/model.py:1057-1298) for one sequence and a chunk of s >= 1 rows at positions
+    start_pos..: rows = fq8(rope(rmsnorm(x))); history = the ring rows of positions start_pos - hist .. start_pos - 1
+    (hist = min(start_pos, W - 1), captured BEFORE the commit, :1174-1200); the last min(s, W) chunk rows are then
+    committed at pos % W (:1260-1296).  Returns ([history | rows] [hist + s, D], the updated ring copy [W, D])."""
+    ring = np.array(ring, np.float32, copy=True)
+    W = ring.shape[0]
+    x = np.asarray(x, np.float32)
+    s = x.shape[0]
+    y = bf16(rmsnorm(x, w, eps))
+    rows = np.stack([bf16(fake_quant_fp8(rope(y[r], cos, sin, np.int64(start_pos + r), rd), 32)) for r in range(s)])
+    hist = min(int(start_pos), W - 1)
+    history = np.stack([ring[(start_pos - hist + h) % W] for h in range(hist)]) if hist else rows[:0]
+    for r in range(max(0, s - W), s):
+        ring[(start_pos + r) % W] = rows[r]
+    return np.concatenate([history, rows]), ring
+
+
 def compress_row(latent, cos, sin, pos, rd) -> np.ndarray:
     """Compressed-KV row (dsv41/decode.py:157-162, dsv41/model.py:1320-1346): rope(last rd) at the group's start
     position -> bf16 -> fq4(16, e4m3 scale) -> bf16."""

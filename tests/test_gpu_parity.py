@@ -109,6 +109,36 @@ def test_kv_write(D):
     _fp8_close(host(ct), want, f"kv_write D={D}")
 
 
+def test_window_kv_chunks():
+    """Attention._window_kv (dsv41/model.py:1057-1298) over a sequence fed in chunks (fresh chunk longer than W,
+    continuations shorter and longer than W, single rows): [history | chunk] rows, window indices and the ring after
+    the commit, for two batch rows, against the oracle."""
+    import dsv41_amd  # noqa: F401
+    from dsv41_amd import cache as C
+    r = rng(14)
+    W, D, rd, b = 128, 576, 64, 2
+    cos, sin = O.rope_tables(rd, 8192, 0, 10000.0, 1.0, 32, 1)
+    w = O.bf16(r.random(D).astype(np.float32) + 0.5)
+    ring_t = bf(np.zeros((b, W, D), np.float32))
+    ring = [np.zeros((W, D), np.float32) for _ in range(b)]
+    start = 0
+    for s in [200, 60, 1, 300, 5, 128, 1]:
+        x = O.bf16(r.standard_normal((b, s, D)).astype(np.float32) * 2)
+        print(f"[window_kv] start {start} chunk {s}", flush=True)
+        out, idx = C.window_kv(bf(x), bf(w), 1e-6, f32(cos), f32(sin), rd, ring_t, start)
+        for bi in range(b):
+            want, ring[bi] = O.window_kv(x[bi], w, cos, sin, start, ring[bi], rd, 1e-6)
+            if s == 1 and start > 0:  # decode shape: the ring itself and its slot indices
+                np.testing.assert_array_equal(host(idx[bi]), O.window_idx(W, 1, start))
+            else:
+                hist, want_idx = (0, O.window_idx(W, s, 0)) if start == 0 else O.prefill_window_idx(W, s, start)
+                assert out.shape[1] == hist + s
+                _fp8_close(host(out[bi]), want, f"window_kv rows b{bi} start {start}")
+                np.testing.assert_array_equal(host(idx[bi]), want_idx)
+            _fp8_close(host(ring_t[bi]), ring[bi], f"window_kv ring b{bi} start {start}")
+        start += s
+
+
 def test_compressed_and_index_key_appends():
     import dsv41_amd
     from dsv41_amd import cache as C

@@ -263,3 +263,31 @@ def test_kv_write_composition():
     row = O.rope(O.bf16(O.rmsnorm(x[0:1], w, 1e-6)), cos, sin, np.int64(300), rd)
     np.testing.assert_array_equal(out[2, 300 % W], O.bf16(O.fake_quant_fp8(row, 32))[0])
     assert np.count_nonzero(out) == np.count_nonzero(out[2, 300 % W]) + np.count_nonzero(out[0, 5])
+
+
+def test_window_kv_history_brute_force():
+    """Attention._window_kv (dsv41/model.py:1057-1298): feeding a sequence chunk by chunk, every returned history
+    equals the last min(start, W-1) rows produced before the chunk (a plain list of all rows, no ring arithmetic),
+    and the ring holds exactly the last W rows at their slots."""
+    r = np.random.default_rng(5)
+    W, D, rd = 16, 64, 16
+    cos, sin = O.rope_tables(rd, 512, 0, 10000.0, 1.0, 32, 1)
+    w = O.bf16(r.random(D).astype(np.float32) + 0.5)
+    ring = np.zeros((W, D), np.float32)
+    produced = []
+    start = 0
+    for s in [5, 1, 9, 16, 3, 40, 1, 17, 2]:
+        x = O.bf16(r.standard_normal((s, D)).astype(np.float32))
+        out, ring = O.window_kv(x, w, cos, sin, start, ring, rd, 1e-6)
+        hist = min(start, W - 1)
+        want_hist = np.stack(produced[start - hist:start]) if hist else np.zeros((0, D), np.float32)
+        np.testing.assert_array_equal(out[:hist], want_hist)
+        produced.extend(out[hist:])
+        start += s
+        for p in range(max(0, start - W), start):
+            np.testing.assert_array_equal(ring[p % W], produced[p])
+    # the chunk rows themselves are the kv_write composition (rmsnorm -> rope -> fq8) at their positions
+    x = O.bf16(r.standard_normal((3, D)).astype(np.float32))
+    out, _ = O.window_kv(x, w, cos, sin, 100, np.zeros((W, D), np.float32), rd, 1e-6)
+    cache = O.kv_write(x, w, cos, sin, [100, 101, 102], [0, 0, 0], np.zeros((1, W, D), np.float32), rd, 1e-6)
+    np.testing.assert_array_equal(out[W - 1:], cache[0, [100 % W, 101 % W, 102 % W]])
