@@ -309,6 +309,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--calib-copy", action="store_true", help="one 64 MiB device copy (rocprof counter calibration)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the C3 prefill leg, its phase times printed as JSON (for profiling; not the bench line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the path shards by slot with no exchange; see the design "
@@ -324,6 +326,9 @@ def main():
         b = torch.neg(a)
         torch.cuda.synchronize(dev)
         del a, b
+    if args.prefill_only:
+        print(json.dumps({"prefill": run_prefill(args, dev)}), flush=True)
+        return
     r = run_decode(args, dev)
     cfg = r["cfg"]
     kb, ku = r["kern_bytes"], r["kern_us"]
