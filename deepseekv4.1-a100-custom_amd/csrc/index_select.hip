@@ -31,7 +31,7 @@ constexpr int kIsKeysPerWave = kIsChunk / 8;   // 4 column tiles of 16 keys
 constexpr int kIsPer = kIsChunk / kIsThreads;  // positions per thread in the selection
 constexpr int kIsSpec = 16;                    // candidates per chunk read together with the counts
 constexpr int kIsCand = 2048;                  // candidates staged in LDS (more: read from the workspace)
-constexpr int kIsMaxChunks = 128;              // chunks per row (rows up to 65536 positions)
+constexpr int kIsMaxChunks = 512;              // chunks per row (rows up to 262144 positions)
 constexpr int kIsMaxWG = 512;                  // resident workgroups: 2 per CU
 constexpr int kIsSpinLimit = 1 << 20;
 
@@ -65,7 +65,11 @@ DSV41_DEV void row_wait(const unsigned long long* flags, int ns, unsigned long l
   (void)done;
 }
 
+// MAXC: the largest chunk count per row the instance handles (128: the candidate-prefix gather and the chunk
+// prefix scans fit 4 loads per thread and two waves; kIsMaxChunks: 16 loads per thread and a workgroup scan).
+template <int MAXC>
 __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArgs g) {
+  static_assert(MAXC <= kIsThreads && MAXC % 64 == 0, "one thread per chunk");
   const ScoreArgs& a = g.s;
   const int R = a.R, ns = g.nslots;
   const int r = blockIdx.x % R, ch = blockIdx.x / R;
@@ -76,7 +80,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   __shared__ int tmp[8];
   __shared__ int wcnt[8][2];
   __shared__ int s_bin, s_need, s_cnt, s_selb, s_over;
-  __shared__ int pc[kIsMaxChunks + 1], na_q[kIsMaxChunks], nc_q[kIsMaxChunks];
+  __shared__ int pc[MAXC + 1], na_q[MAXC], nc_q[MAXC];
   __shared__ __align__(16) unsigned long long lc[kIsCand + 2];
   __shared__ RankScratch rs;
 
@@ -89,6 +93,8 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   const unsigned long long e0 =
       __hip_atomic_load(g.flags + (long)r * ns + ch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) / 2;
   const int c = (int)(clr < 0 ? 0 : (clr > a.n_pos ? a.n_pos : clr)), k = g.k;
+  if (clr > a.n_pos && ch == 0 && t == 0)  // positions beyond n_pos were promised never to be valid
+    __hip_atomic_store(g.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int nht = (a.HI + 15) / 16;
   i32x8_t qa8[kHT];
   uint4 qa16[kHT][4];  // (bf16 queries: unused here)
@@ -265,7 +271,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     na_q[t] = (int)(cv & 0xffffffffu);
     nc_q[t] = (int)(cv >> 32);
   }
-  constexpr int kSpecPer = kIsMaxChunks * kIsSpec / kIsThreads;
+  constexpr int kSpecPer = MAXC * kIsSpec / kIsThreads;
   unsigned long long sv[kSpecPer];
 #pragma unroll
   for (int u = 0; u < kSpecPer; ++u) {
@@ -273,25 +279,41 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     sv[u] = q < ns ? __hip_atomic_load(crow + q * kIsChunk + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
   }
   __syncthreads();
-  if (wave < 2) {  // prefix of the candidate counts (2 x 64 chunks); entries above B in earlier chunks
-    const int q = wave * 64 + lane;
-    const int x = q < ns ? nc_q[q] : 0;
-    const int ix = wave_incl_scan(x);
-    pc[q + 1] = ix;  // (wave 1 adds wave 0's total below)
-    const int y = q < ch ? na_q[q] : 0;
-    const int iy = wave_incl_scan(y);
-    if (lane == 63) wcnt[wave][0] = iy, wcnt[wave][1] = ix;
-    const bool over = __ballot(x > kIsSpec) != 0;
-    if (lane == 0) tmp[wave] = over;
+  if constexpr (MAXC <= 128) {
+    if (wave < 2) {  // prefix of the candidate counts (2 x 64 chunks); entries above B in earlier chunks
+      const int q = wave * 64 + lane;
+      const int x = q < ns ? nc_q[q] : 0;
+      const int ix = wave_incl_scan(x);
+      pc[q + 1] = ix;  // (wave 1 adds wave 0's total below)
+      const int y = q < ch ? na_q[q] : 0;
+      const int iy = wave_incl_scan(y);
+      if (lane == 63) wcnt[wave][0] = iy, wcnt[wave][1] = ix;
+      const bool over = __ballot(x > kIsSpec) != 0;
+      if (lane == 0) tmp[wave] = over;
+    }
+    __syncthreads();
+    if (t >= 64 && t < 128) pc[t + 1] += wcnt[0][1];
+    if (t == 0) {
+      pc[0] = 0;
+      s_selb = wcnt[0][0] + wcnt[1][0];
+      s_over = tmp[0] | tmp[1];
+    }
+    __syncthreads();
+  } else {  // one chunk per thread: workgroup scans
+    const int x = t < ns ? nc_q[t] : 0;
+    const int y = t < ch ? na_q[t] : 0;
+    const int over = __syncthreads_or(x > kIsSpec);
+    int tx, ty;
+    const int ex = block_scan_dpp<kIsThreads>(x, tmp, &tx);
+    block_scan_dpp<kIsThreads>(y, tmp, &ty);
+    if (t < ns) pc[t + 1] = ex + x;
+    if (t == 0) {
+      pc[0] = 0;
+      s_selb = ty;
+      s_over = over;
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if (t >= 64 && t < 128) pc[t + 1] += wcnt[0][1];
-  if (t == 0) {
-    pc[0] = 0;
-    s_selb = wcnt[0][0] + wcnt[1][0];
-    s_over = tmp[0] | tmp[1];
-  }
-  __syncthreads();
   const int m = pc[ns];
   const bool staged = m <= kIsCand;
   if (t == 0 && staged) lc[m] = 0ull;  // pad for pairwise reads
@@ -394,7 +416,10 @@ int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_r
   g.cand = g.cnt + (long)R * ns;
   g.flags = g.cand + (long)R * ns * kIsChunk;
   g.err = (int*)(g.flags + (long)R * ns);
-  index_select_kernel<<<R * ns, kIsThreads, 0, (hipStream_t)stream>>>(g);
+  if (ns <= 128)
+    index_select_kernel<128><<<R * ns, kIsThreads, 0, (hipStream_t)stream>>>(g);
+  else
+    index_select_kernel<kIsMaxChunks><<<R * ns, kIsThreads, 0, (hipStream_t)stream>>>(g);
   DSV41_CHECK_LAUNCH();
   return 0;
 }

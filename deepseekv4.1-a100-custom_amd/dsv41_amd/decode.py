@@ -57,7 +57,9 @@ class DecodeLayer:
     def selector(self, rows: int, device) -> DecodeSelector:
         sel = self._selectors.get(rows)
         if sel is None:
-            sel = self._selectors[rows] = DecodeSelector(rows, self.k8.shape[1], self.topk, device)
+            # cl never covers the tables' spare last row
+            sel = self._selectors[rows] = DecodeSelector(rows, self.k8.shape[1], self.topk, device,
+                                                         max_cl=self.k8.shape[1] - 1)
         return sel
 
     def attn_workspace(self, B: int, h: int, L: int, device) -> torch.Tensor:

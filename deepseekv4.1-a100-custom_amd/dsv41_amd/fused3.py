@@ -68,25 +68,29 @@ def topk_indices(score: torch.Tensor, k: int, cl: torch.Tensor) -> torch.Tensor:
 
 class DecodeSelector:
     """index_score + topk_indices of the graph decode (dsv41/decode.py:289-294) for a fixed (rows, n_pos, k).  With
-    e4m3 keys and a grid that fits (rows * ceil(n_pos / 512) <= 512 workgroups, n_pos <= 65536) both run in one
+    e4m3 keys and a grid that fits (rows * ceil(n_sel / 512) <= 512 workgroups, n_sel <= 262144) both run in one
     launch (dsv41_index_select); otherwise the score kernel builds a 4096-bin histogram of the score keys and the
     top-k follows from it (one workgroup per row up to 36864 positions, else a compaction pass plus a finalize).
     Holds the score buffer and the zero-initialised workspaces, which every call leaves ready for the next
-    (reusable, graph-capturable).  keep_scores: also write the scores (self.score) on the one-launch path."""
+    (reusable, graph-capturable).  keep_scores: also write the scores (self.score) on the one-launch path.
+    max_cl: the largest valid count cl the caller will pass (the decode tables end with a spare row that cl never
+    covers, dsv41/decode.py:176-181, 287); the one-launch path scores and selects positions < n_sel = min(n_pos,
+    max_cl) only."""
 
-    def __init__(self, rows: int, n_pos: int, k: int, device, keep_scores: bool = False):
+    def __init__(self, rows: int, n_pos: int, k: int, device, keep_scores: bool = False, max_cl: int | None = None):
         self.rows, self.n_pos, self.k = rows, n_pos, k
+        self.n_sel = n_pos if max_cl is None else max(1, min(n_pos, int(max_cl)))
         nbytes = lib().dsv41_select_workspace_bytes(rows, n_pos)
         self.ws = torch.zeros(nbytes // 4, dtype=torch.int32, device=device)
         self.nbytes = nbytes
         ld = (n_pos + 3) // 4 * 4  # 16-byte aligned rows: the selection reads float4
         self.score = torch.empty(rows, ld, dtype=torch.float32, device=device)[:, :n_pos]
         self.out = torch.empty(rows, 1, k, dtype=torch.int32, device=device)
-        ns = (n_pos + 511) // 512
-        self.one_launch = ns <= 128 and rows * ns <= 512
+        ns = (self.n_sel + 511) // 512
+        self.one_launch = ns <= 512 and rows * ns <= 512
         self.keep_scores = keep_scores
         if self.one_launch:
-            self.fnbytes = lib().dsv41_index_select_workspace_bytes(rows, n_pos)
+            self.fnbytes = lib().dsv41_index_select_workspace_bytes(rows, self.n_sel)
             self.fws = torch.zeros(self.fnbytes // 4, dtype=torch.int32, device=device)
 
     def score_into(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None) -> None:
@@ -107,7 +111,7 @@ class DecodeSelector:
         """Scores + top-k in one launch from the prepared e4m3 queries (q8, wf)."""
         ks = k_scale if k_scale.dtype == torch.float32 else k_scale.float()
         call("dsv41_index_select", ptr(q8), 64 * 128, ptr(wf), 64, self.rows, H, ptr(index_k), index_k.stride(0),
-             ptr(ks), ks.stride(0), ptr(seq), ptr(cl), self.n_pos, self.k, 0, ptr(self.fws), self.fnbytes,
+             ptr(ks), ks.stride(0), ptr(seq), ptr(cl), self.n_sel, self.k, 0, ptr(self.fws), self.fnbytes,
              ptr(self.score) if self.keep_scores else None, self.score.stride(0), ptr(self.out), self.k,
              stream(self.score.device))
         return self.out

@@ -90,9 +90,10 @@ long dsv41_index_select_workspace_bytes(int R, int n_pos);
  * positions 0..cl[r).  out [R, k]: the k largest scores' positions, ascending, + offset, -1 padding when cl[r] < k;
  * ties lowest index first (the set of dsv41_topk_indices on the same scores).  score_out (may be null): the scores,
  * -inf for cl[r] <= t < n_pos.  Needs R * ceil(n_pos / 512) <= 512 workgroups (resident together: the rows'
- * workgroups meet at two barriers) and n_pos <= 65536; otherwise hipErrorInvalidValue (use dsv41_index_score +
- * dsv41_select_topk).  A barrier wait that gives up (a workgroup never arrived) sets the workspace's last-but-three
- * int32 to 1. */
+ * workgroups meet at two barriers) and n_pos <= 262144; otherwise hipErrorInvalidValue (use dsv41_index_score +
+ * dsv41_select_topk).  n_pos may be less than the key table's rows (the decode tables' spare last row is never
+ * valid); a cl[r] > n_pos is clamped to n_pos and sets the workspace's last-but-three int32 to 2.  A barrier wait
+ * that gives up (a workgroup never arrived) sets it to 1. */
 int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_rstride, int R, int HI,
                        const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
                        const long* cl, int n_pos, int k, int offset, void* ws, long ws_bytes, float* score_out,
