@@ -372,6 +372,7 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   constexpr int TILE_ELEMS = TILE * DQK;
   constexpr int kLoadsPerTile = TILE * U / 512;  // 16-byte direct-to-LDS loads per wave per tile
   static_assert(kLoadsPerTile < 16, "vmcnt immediate");
+  static_assert(16 * DQK / 8 % 64 == 0 && 16 * DQK <= TILE_ELEMS, "Q staging");
   constexpr float kRescale = 8.0f;
   constexpr int KT_ELEMS = 2 * TILE_ELEMS > 4 * 16 * (DV + 4) * 2 ? 2 * TILE_ELEMS : 4 * 16 * (DV + 4) * 2;
   __shared__ __align__(16) uint16_t ktile[KT_ELEMS];  // two tile buffers; the merge buffer aliases them
@@ -416,12 +417,22 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
     return j < j1 && jj >= 0 && irow ? irow[jj] : -1;
   };
   ixs[tid] = load_ix(tid);  // the first kIxPre entries of the split, kept in LDS
-  uint4 qf[KS];
+  // Q of the 16 heads (16 x DQK bf16, rows of missing heads repeat the last head and are never written) is staged
+  // once through the second tile buffer with direct-to-LDS loads; every wave then reads its fragments from LDS (the
+  // 8 waves each loading all of Q would pull 8x the bytes through the CU while every CU starts at once)
+  uint16_t* const qlds = ktile + TILE_ELEMS;
   {
-    const int h = h0 + l16 < H ? h0 + l16 : H - 1;  // rows of missing heads are never written
-    const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)h * DQK;
+    constexpr int QCH = 16 * DQK / 8;  // 16-byte chunks
+    constexpr int PR = DQK / 8;        // chunks per head row
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qrow + ks * 32 + g * 8);
+    for (int u = 0; u < (QCH + 511) / 512; ++u) {
+      const int cid = u * 512 + wave * 64 + lane;
+      if (u * 512 + wave * 64 < QCH) {  // wave-uniform: a whole wave's chunks lie inside Q (QCH % 64 == 0)
+        const int hh = cid / PR, part = cid - hh * PR;
+        const int h = h0 + hh < H ? h0 + hh : H - 1;
+        lds_dma16(a.q + (long)r * a.q_rstride + (long)h * DQK + part * 8, qlds + (u * 512 + wave * 64) * 8);
+      }
+    }
   }
   long slot, pos = 0, pmax = 0, plim = 0;
   if (a.mode == 1) {
@@ -477,9 +488,12 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   __builtin_amdgcn_s_waitcnt(0);  // Q has arrived too: no wait for it is left inside the tile loop
   DSV41_PH(1);
   __syncthreads();
+  uint4 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qlds + l16 * DQK + ks * 32 + g * 8);
   if (ntiles > 0) resolve(0);
   if (ntiles > 1) resolve(1);
-  __syncthreads();
+  __syncthreads();  // (Q has been read: its buffer takes tile 1)
   DSV41_TS(11);
   DSV41_PH(2);
   if (ntiles > 0) issue(0);
