@@ -83,6 +83,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   __shared__ int pc[MAXC + 1], na_q[MAXC], nc_q[MAXC];
   __shared__ __align__(16) unsigned long long lc[kIsCand + 2];
   __shared__ RankScratch rs;
+  __shared__ __align__(16) uint8_t qs[64 * 128];  // the row's prepared e4m3 queries, staged once
 
   // ---- A. row data (independent loads), scores, histogram
   DSV41_PH(0);
@@ -96,6 +97,10 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   if (clr > a.n_pos && ch == 0 && t == 0)  // positions beyond n_pos were promised never to be valid
     __hip_atomic_store(g.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int nht = (a.HI + 15) / 16;
+  // the row's queries (64 heads x 128 e4m3 = 512 chunks of 16 bytes) go to LDS once, one direct load per thread
+  // (every wave needs all of them); heads >= HI are never read back
+  if (t < a.HI * 8) lds_dma16((const uint16_t*)((const uint8_t*)a.q + (long)r * a.q_rstride) + t * 8,
+                              (uint16_t*)qs + wave * 64 * 8);
   i32x8_t qa8[kHT];
   uint4 qa16[kHT][4];  // (bf16 queries: unused here)
   float wl[kHT];
@@ -103,11 +108,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   for (int ht = 0; ht < kHT; ++ht) {
     const int h = ht * 16 + l16;
     const bool hv = ht < nht && h < a.HI;
-    const int hc = hv ? h : 0;
-    const uint4* qrow = (const uint4*)((const uint8_t*)a.q + (long)r * a.q_rstride + (long)hc * 128 + g4 * 32);
-    const uint4 u0 = qrow[0], u1 = qrow[1];
-    qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
-    wl[ht] = hv ? a.w[(long)r * a.w_rstride + hc] : 0.0f;
+    wl[ht] = hv ? a.w[(long)r * a.w_rstride + h] : 0.0f;
   }
 #ifdef DSV41_TIMING
   __builtin_amdgcn_s_waitcnt(0);
@@ -138,7 +139,14 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   for (int ht = 0; ht < kHT; ++ht)
 #pragma unroll
     for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[ht], 4 * g4 + i, 64);
-  __syncthreads();  // histogram cleared
+  __syncthreads();  // histogram cleared, queries staged
+#pragma unroll
+  for (int ht = 0; ht < kHT; ++ht) {
+    const int h = ht * 16 + l16;
+    const int hc = ht < nht && h < a.HI ? h : 0;
+    const uint4 u0 = *(const uint4*)(qs + hc * 128 + g4 * 32), u1 = *(const uint4*)(qs + hc * 128 + g4 * 32 + 16);
+    qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+  }
   DSV41_TS(52);
   const bool sel = c > k;  // (otherwise every valid position is taken)
   float* orow = a.out ? a.out + (long)r * a.out_rstride : nullptr;
