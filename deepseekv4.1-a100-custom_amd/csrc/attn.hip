@@ -1379,7 +1379,7 @@ int dispatch(AttnArgs& a, int dqk, int dv, hipStream_t st) {
   return (int)hipErrorInvalidValue;
 }
 
-// Split plan.  Decode kernel: ~256 workgroups over (rows x 16-head groups x splits), >= 2 tiles of 64 keys per
+// Split plan.  Decode kernel: <= 192 workgroups over (rows x 16-head groups x splits), >= 2 tiles of 64 keys per
 // split.  64-head kernel: >= 512 workgroups when rows are few, >= 2 tiles of 32 keys per split.
 void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
   const bool dec = use_decode_kernel(R, H);
@@ -1389,10 +1389,12 @@ void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
   if (want > 0) {
     per = (tiles + want - 1) / want;
   } else if (dec) {
-    // ~256 workgroups, >= 2 tiles per split; the decode kernel balances the tiles over the splits
+    // <= 192 workgroups (three quarters of the CUs; each holds one), >= 2 tiles per split; the decode kernel balances
+    // the tiles over the splits.  Measured at C2 (16 units): 12 splits 21.7 us, 16 splits 25.5 us; at C5 (192
+    // units): 1 split 39.7 us, 2 splits 49.1 us (a second round of workgroups).
     const long wgs = (long)R * ((H + 15) / 16);
     const int cap = tiles / 2 < 1 ? 1 : tiles / 2;
-    int ns = (int)(wgs >= 256 ? 1 : (256 + wgs - 1) / wgs);
+    int ns = (int)(wgs >= 192 ? 1 : 192 / wgs);
     if (ns > cap) ns = cap;
     *nsplit = ns;
     *chunk = (tiles + ns - 1) / ns * tile;
