@@ -17,12 +17,17 @@
 namespace {
 
 template <int KFMT, bool HIST>
-__global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
+__global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a, int nx) {
+  // 1-D grid: block b runs on XCD b % 8 (round-robin dispatch); key chunk x belongs to XCD x % 8 and its R rows
+  // follow one another there, so rows of one sequence (MTP drafts) read the chunk's keys from that XCD's L2
+  const int bxcd = blockIdx.x % kXcds, bj = blockIdx.x / kXcds;
+  const int by = bj % a.R, bx = (bj / a.R) * kXcds + bxcd;
+  if (bx >= nx) return;
   DSV41_TS(30);
   DSV41_WG_TS(0);
-  if (blockIdx.y == 0) DSV41_PH(0);
+  if (by == 0) DSV41_PH(0);
   __shared__ int lhist[HIST ? kHistBins : 1];
-  const int r = blockIdx.y;
+  const int r = by;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (HIST) {
 #pragma unroll 1
@@ -30,7 +35,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
     __syncthreads();
   }
   const int l16 = lane & 15, g = lane >> 4;
-  const int kt0 = blockIdx.x * kKeysPerWG + wave * kKeysPerWave;
+  const int kt0 = bx * kKeysPerWG + wave * kKeysPerWave;
   long cl = row_cl(a, r);
   if (cl > a.n_pos) cl = a.n_pos;
   float* orow = a.out + (long)r * a.out_rstride;
@@ -39,7 +44,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
       for (int t = kt0 + lane; t < kt0 + kKeysPerWave && t < a.n_pos; t += 64) orow[t] = -__builtin_inff();
     if (!HIST) return;
   } else {
-  if (blockIdx.y == 0) DSV41_PH(1);
+  if (by == 0) DSV41_PH(1);
   const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
   const int nht = (a.HI + 15) / 16;
   const int lim = (int)cl;
@@ -92,7 +97,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
     if (!hv) wl[ht] = 0.0f;
   }
   DSV41_TS(31);
-  if (blockIdx.y == 0) DSV41_PH(2);
+  if (by == 0) DSV41_PH(2);
   float wr[kHT][4];  // weights of the heads this lane's accumulators hold: ht*16 + 4g + i
 #pragma unroll
   for (int ht = 0; ht < kHT; ++ht)
@@ -117,7 +122,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
   }
   }  // kt0 < cl
   DSV41_TS(32);
-  if (blockIdx.y == 0) DSV41_PH(3);
+  if (by == 0) DSV41_PH(3);
   if (HIST) {
     __syncthreads();
     int* gh = a.hist + (long)r * kHistBins;
@@ -127,7 +132,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a) {
       if (v) atomicAdd(&gh[i], v);
     }
   }
-  if (blockIdx.y == 0) DSV41_PH(4);
+  if (by == 0) DSV41_PH(4);
   DSV41_WG_TS(1);
 }
 
@@ -531,13 +536,14 @@ int launch_score(ScoreArgs& a, hipStream_t st) {
     DSV41_CHECK_LAUNCH();
     return 0;
   }
-  dim3 grid((a.n_pos + kKeysPerWG - 1) / kKeysPerWG, a.R);
+  const int nx = (a.n_pos + kKeysPerWG - 1) / kKeysPerWG;
+  const dim3 grid((nx + kXcds - 1) / kXcds * kXcds * a.R);
   if (a.hist) {
-    if (a.kfmt == 1) index_score_kernel<1, true><<<grid, 256, 0, st>>>(a);
-    else index_score_kernel<0, true><<<grid, 256, 0, st>>>(a);
+    if (a.kfmt == 1) index_score_kernel<1, true><<<grid, 256, 0, st>>>(a, nx);
+    else index_score_kernel<0, true><<<grid, 256, 0, st>>>(a, nx);
   } else {
-    if (a.kfmt == 1) index_score_kernel<1, false><<<grid, 256, 0, st>>>(a);
-    else index_score_kernel<0, false><<<grid, 256, 0, st>>>(a);
+    if (a.kfmt == 1) index_score_kernel<1, false><<<grid, 256, 0, st>>>(a, nx);
+    else index_score_kernel<0, false><<<grid, 256, 0, st>>>(a, nx);
   }
   DSV41_CHECK_LAUNCH();
   return 0;
