@@ -155,7 +155,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     const int p = pw + nt * 16 + l16;
     const float sum = score_tile<1>(qa8, qa16, wr, nht, k0[nt], k1[nt], nullptr);
     if (g4 == 0) {
-      const float v = p < c ? sum * ksc[nt] : 0.0f;
+      const float v = p < c ? (is_cand(a, r, p) ? sum * ksc[nt] : -__builtin_inff()) : 0.0f;
       sc[p - ch * kIsChunk] = v;
       if (p < c && sel) atomicAdd(&lhist[score_key(v) >> 20], 1);
       if (orow && p < a.n_pos) orow[p] = p < c ? v : -__builtin_inff();
@@ -387,7 +387,8 @@ long dsv41_index_select_workspace_bytes(int R, int n_pos) {
 int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_rstride, int R, int HI,
                        const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
                        const long* cl, int n_pos, int k, int offset, void* ws, long ws_bytes, float* score_out,
-                       long score_rstride, int* out, long out_rstride, void* stream) {
+                       long score_rstride, int* out, long out_rstride, const void* cand, long cand_rstride,
+                       void* stream) {
   if (R <= 0 || k <= 0) return 0;
   const int ns = is_slots(n_pos);
   if (n_pos <= 0 || HI <= 0 || HI > 64 || !cl || !kscale || ns > kIsMaxChunks || (long)R * ns > kIsMaxWG)
@@ -413,6 +414,8 @@ int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_r
   a.write_masked = 1;
   a.out = score_out;
   a.out_rstride = score_rstride;
+  a.cand = (const uint8_t*)cand;
+  a.cand_rstride = cand_rstride;
   g.k = k;
   g.offset = offset;
   g.idx = out;

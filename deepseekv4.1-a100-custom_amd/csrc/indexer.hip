@@ -112,8 +112,9 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a, int
       const float sum = score_tile<KFMT>(qa8, qa16, wr, nht, k0[nt], k1[nt], kb16[nt]);
       if (g == 0 && t < a.n_pos) {
         if (t < lim) {
-          orow[t] = sum * ksc[nt];
-          if (HIST) atomicAdd(&lhist[score_key(sum * ksc[nt]) >> 20], 1);
+          const float v = is_cand(a, r, t) ? sum * ksc[nt] : -__builtin_inff();
+          orow[t] = v;
+          if (HIST) atomicAdd(&lhist[score_key(v) >> 20], 1);
         } else if (a.write_masked) {
           orow[t] = -__builtin_inff();
         }
@@ -253,7 +254,7 @@ __global__ void __launch_bounds__(256) index_score_prefill_kernel(const ScoreArg
             for (int i = 0; i < 4; ++i) sum += wr[qq][ht][i] * relu(acc[u][qq][ht][i]);
           sum = row_sum4(sum);
           if (g == 0 && rows[qq] < a.R && t < clr[qq] && t < kb1)
-            a.out[(long)rows[qq] * a.out_rstride + t] = sum * ksc[u];
+            a.out[(long)rows[qq] * a.out_rstride + t] = is_cand(a, rows[qq], t) ? sum * ksc[u] : -__builtin_inff();
         }
       }
     }
@@ -549,6 +550,63 @@ int launch_score(ScoreArgs& a, hipStream_t st) {
   return 0;
 }
 
+
+// ------------------------------------------------------------------------------------------------ candidate blocks
+// select_candidate_blocks (dsv41/model.py:256-265): per row the maxima of the masked scores over blocks of bs
+// positions (positions >= cl(r) count as -inf), the block of position cl(r) - 1 forced to +inf, the topk_blocks
+// largest blocks (ties lowest block first) kept when their value is finite, expanded to a per-position mask.
+struct CandArgs {
+  const float* score;
+  long ld;
+  int R, n, width, bs, nb, kb;
+  const long* cl;
+  long cl_start;
+  int cl_ratio, rows_per_seq;
+  float* bmax;  // [R, nbp]
+  long nbp;
+  int* sel;  // [R, kb] selected blocks, ascending
+  uint8_t* mask;
+  long mask_rstride;
+};
+
+DSV41_DEV long cand_row_cl(const CandArgs& a, int r) {
+  if (a.cl) return a.cl[r];
+  return (a.cl_start + (long)(r % a.rows_per_seq) + 1) / a.cl_ratio;
+}
+
+__global__ void __launch_bounds__(256) cand_blockmax_kernel(const CandArgs a) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)a.R * a.nb) return;
+  const int r = (int)(i / a.nb), b = (int)(i - (long)r * a.nb);
+  long c = cand_row_cl(a, r);
+  c = c < 0 ? 0 : (c > a.n ? a.n : c);
+  float m = -__builtin_inff();
+  const float* row = a.score + (long)r * a.ld;
+  const long t1 = min((long)(b + 1) * a.bs, c);
+  for (long t = (long)b * a.bs; t < t1; ++t) m = fmaxf(m, row[t]);
+  if (c > 0 && b == (int)((c - 1) / a.bs)) m = __builtin_inff();
+  a.bmax[(long)r * a.nbp + b] = m;
+}
+
+__global__ void __launch_bounds__(256) cand_expand_kernel(const CandArgs a) {
+  const int r = blockIdx.y;
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= a.width) return;
+  const int b = (int)(t / a.bs);
+  const int* srow = a.sel + (long)r * a.kb;
+  int lo = 0, hi = a.kb;  // srow is ascending (with -1 padding only when a row has fewer blocks than kb)
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    const int v = srow[mid];
+    if (v >= 0 && v < b) lo = mid + 1; else hi = mid;
+  }
+  bool keep = false;
+  if (lo < a.kb && srow[lo] == b && b < a.nb) keep = a.bmax[(long)r * a.nbp + b] > -__builtin_inff();
+  a.mask[(long)r * a.mask_rstride + t] = keep ? 1 : 0;
+}
+
+long cand_nbp(int n, int bs) { return ((n + bs - 1) / bs + 3) / 4 * 4; }
+
 }  // namespace
 
 extern "C" {
@@ -563,7 +621,7 @@ int dsv41_read_wg_idx(long long* host) { return (int)hipMemcpyFromSymbol(host, H
 int dsv41_index_score(const void* q, long q_rstride, const float* w, long w_rstride, int R, int HI, int D, int kfmt,
                       const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
                       int rows_per_slot, const long* cl, long cl_start, int cl_ratio, int n_pos, int write_masked,
-                      float* out, long out_rstride, int* hist, void* stream) {
+                      float* out, long out_rstride, int* hist, const void* cand, long cand_rstride, void* stream) {
   if (D != 128 || (kfmt == 1 && !kscale) || (!cl && cl_ratio <= 0)) return (int)hipErrorInvalidValue;
   ScoreArgs a{};
   a.q = (const uint16_t*)q;
@@ -587,6 +645,8 @@ int dsv41_index_score(const void* q, long q_rstride, const float* w, long w_rstr
   a.out = out;
   a.out_rstride = out_rstride;
   a.hist = hist;
+  a.cand = (const uint8_t*)cand;
+  a.cand_rstride = cand_rstride;
   return launch_score(a, (hipStream_t)stream);
 }
 
@@ -608,6 +668,49 @@ int dsv41_topk_indices(const float* score, long ld, int R, int n, int k, const l
   a.offset = offset;
   if (R >= 512 && n <= 17408) topk_kernel<512, 17408><<<R, 512, 0, (hipStream_t)stream>>>(a);  // many short rows
   else topk_kernel<1024, 32768><<<R, 1024, 0, (hipStream_t)stream>>>(a);
+  DSV41_CHECK_LAUNCH();
+  return 0;
+}
+
+long dsv41_candidate_blocks_workspace_bytes(int R, int n, int topk_blocks, int block_size) {
+  if (R <= 0 || n <= 0 || block_size <= 0 || topk_blocks <= 0) return 0;
+  const int nb = (n + block_size - 1) / block_size, kb = topk_blocks < nb ? topk_blocks : nb;
+  return (long)R * cand_nbp(n, block_size) * 4 + (long)R * kb * 4;
+}
+
+int dsv41_candidate_blocks(const float* score, long ld, int R, int n, int width, const long* cl, long cl_start,
+                           int cl_ratio, int rows_per_seq, int topk_blocks, int block_size, void* mask,
+                           long mask_rstride, void* ws, long ws_bytes, void* stream) {
+  if (R <= 0 || width <= 0) return 0;
+  if (n <= 0 || n > width || block_size <= 0 || topk_blocks <= 0 || (!cl && cl_ratio <= 0) || !mask)
+    return (int)hipErrorInvalidValue;
+  if (!ws || ws_bytes < dsv41_candidate_blocks_workspace_bytes(R, n, topk_blocks, block_size))
+    return (int)hipErrorInvalidValue;
+  CandArgs a{};
+  a.score = score;
+  a.ld = ld;
+  a.R = R;
+  a.n = n;
+  a.width = width;
+  a.bs = block_size;
+  a.nb = (n + block_size - 1) / block_size;
+  a.kb = topk_blocks < a.nb ? topk_blocks : a.nb;
+  a.cl = cl;
+  a.cl_start = cl_start;
+  a.cl_ratio = cl_ratio;
+  a.rows_per_seq = rows_per_seq > 0 ? rows_per_seq : 1;
+  a.nbp = cand_nbp(n, block_size);
+  a.bmax = (float*)ws;
+  a.sel = (int*)((char*)ws + (long)R * a.nbp * 4);
+  a.mask = (uint8_t*)mask;
+  a.mask_rstride = mask_rstride;
+  hipStream_t st = (hipStream_t)stream;
+  cand_blockmax_kernel<<<(int)(((long)R * a.nb + 255) / 256), 256, 0, st>>>(a);
+  DSV41_CHECK_LAUNCH();
+  // the kb largest block maxima of every row (all nb blocks valid: cl = (nb - 1 + 0 + 1) / 1)
+  const int rc = dsv41_topk_indices(a.bmax, a.nbp, R, a.nb, a.kb, nullptr, a.nb - 1, 1, 1, 0, a.sel, a.kb, stream);
+  if (rc) return rc;
+  cand_expand_kernel<<<dim3((width + 255) / 256, R), 256, 0, st>>>(a);
   DSV41_CHECK_LAUNCH();
   return 0;
 }

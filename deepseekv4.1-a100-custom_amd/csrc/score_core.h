@@ -26,7 +26,12 @@ struct ScoreArgs {
   float* out;
   long out_rstride;
   int* hist;  // optional [R, kHistBins]: counts of score_key(score) >> 20 over t < cl (decode selection)
+  const uint8_t* cand;  // optional candidate mask [R, >= n_pos] (nonzero = candidate): other t < cl score -inf
+  long cand_rstride;
 };
+
+// Candidate mask of position t of row r (true when no mask is given).
+DSV41_DEV bool is_cand(const ScoreArgs& a, int r, long t) { return !a.cand || a.cand[(long)r * a.cand_rstride + t]; }
 
 DSV41_DEV long row_cl(const ScoreArgs& a, int r) {
   if (a.cl) return a.cl[r];

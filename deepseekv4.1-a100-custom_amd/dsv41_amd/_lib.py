@@ -22,10 +22,13 @@ SIGNATURES = {
     "dsv41_sattn2": [_P, _P, _L, _I, _P, _L, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _F, _P, _I, _I, _I, _I, _I,
                      _P, _L, _P],
     "dsv41_index_score": [_P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _L, _P, _I, _P, _L, _I, _I, _I, _P, _L, _P,
-                          _P],
+                          _P, _L, _P],
     "dsv41_select_workspace_bytes": [_I, _I],
     "dsv41_index_select_workspace_bytes": [_I, _I],
-    "dsv41_index_select": [_P, _L, _P, _L, _I, _I, _P, _L, _P, _L, _P, _P, _I, _I, _I, _P, _L, _P, _L, _P, _L, _P],
+    "dsv41_index_select": [_P, _L, _P, _L, _I, _I, _P, _L, _P, _L, _P, _P, _I, _I, _I, _P, _L, _P, _L, _P, _L, _P,
+                           _L, _P],
+    "dsv41_candidate_blocks_workspace_bytes": [_I, _I, _I, _I],
+    "dsv41_candidate_blocks": [_P, _L, _I, _I, _I, _P, _L, _I, _I, _I, _I, _P, _L, _P, _L, _P],
     "dsv41_select_topk": [_P, _L, _I, _I, _I, _P, _I, _P, _L, _P, _L, _P],
     "dsv41_topk_indices": [_P, _L, _I, _I, _I, _P, _L, _I, _I, _I, _P, _L, _P],
     "dsv41_kv_write": [_P, _L, _P, _P, _P, _P, _P, _L, _L, _I, _P, _L, _I, _P, _I, _I, _I, _F, _I, _P],
@@ -40,7 +43,7 @@ SIGNATURES = {
     "dsv41_rmsnorm": [_P, _P, _P, _L, _I, _F, _P],
 }
 _RESTYPE = {"dsv41_attn_workspace_bytes": _L, "dsv41_select_workspace_bytes": _L,
-            "dsv41_index_select_workspace_bytes": _L}
+            "dsv41_index_select_workspace_bytes": _L, "dsv41_candidate_blocks_workspace_bytes": _L}
 
 _lib = None
 

@@ -18,11 +18,22 @@ def qprep(q: torch.Tensor, weights: torch.Tensor):
     return q8, wf
 
 
-def _score(q, index_k, weights, seq, cl, k_scale, out, write_masked: bool, hist, prepared=None):
+def _cand_args(cand, B: int, n_pos: int):
+    """(pointer, row stride) of a candidate mask bool/uint8 [B, 1, >= n_pos] or [B, >= n_pos] (None: no mask)."""
+    if cand is None:
+        return None, 0
+    c = cand.reshape(B, -1)
+    if c.dtype not in (torch.bool, torch.uint8) or c.shape[1] < n_pos or c.stride(1) != 1:
+        raise RuntimeError(f"index_score: candidate mask {tuple(cand.shape)} {cand.dtype} does not cover {n_pos}")
+    return ptr(c), c.stride(0)
+
+
+def _score(q, index_k, weights, seq, cl, k_scale, out, write_masked: bool, hist, prepared=None, cand=None):
     """prepared = (q8, wf) from qprep / decode_appends for e4m3 keys (computed here when None)."""
     B, _, H, D = q.shape
     dev = q.device
     n_pos = index_k.shape[1]
+    cp, cs = _cand_args(cand, B, n_pos)
     assert index_k.stride(2) == 1 and index_k.stride(1) == D and D == 128 and H <= 64
     if index_k.dtype == torch.float8_e4m3fn:
         if k_scale is None:
@@ -32,25 +43,26 @@ def _score(q, index_k, weights, seq, cl, k_scale, out, write_masked: bool, hist,
         q8, wf = prepared if prepared is not None else qprep(q, weights)
         call("dsv41_index_score", ptr(q8), 64 * 128, ptr(wf), 64, B, H, D, 1, ptr(index_k), index_k.stride(0), ptr(ks),
              ks.stride(0), ptr(seq), 1, ptr(cl), 0, 1, n_pos, int(write_masked), ptr(out), out.stride(0), ptr(hist),
-             stream(dev))
+             cp, cs, stream(dev))
     else:
         qc = q.contiguous()
         w = weights.reshape(B, H).float().contiguous()
         call("dsv41_index_score", ptr(qc), H * D, ptr(w), H, B, H, D, 0, ptr(index_k), index_k.stride(0), None, 0,
-             ptr(seq), 1, ptr(cl), 0, 1, n_pos, int(write_masked), ptr(out), out.stride(0), ptr(hist), stream(dev))
+             ptr(seq), 1, ptr(cl), 0, 1, n_pos, int(write_masked), ptr(out), out.stride(0), ptr(hist), cp, cs,
+             stream(dev))
 
 
 def index_score(q: torch.Tensor, index_k: torch.Tensor, weights: torch.Tensor, seq: torch.Tensor, cl: torch.Tensor,
                 cand: torch.Tensor | None = None, k_scale: torch.Tensor | None = None) -> torch.Tensor:
     """dsv41/fused3.py:46-62.  q: bf16 [B, 1, H, D]; index_k: [S, n_pos, D] bf16 (reference storage) or
     float8_e4m3fn with k_scale fp32 [S, n_pos] (per-row scale); weights [B, 1, H] or [B, H] (already scaled);
-    seq, cl: int64 [B] -> fp32 [B, n_pos], -inf for t >= cl.  Positions >= cl are not read."""
-    if cand is not None:
-        raise NotImplementedError("index_score: candidate-block masks are not supported by this path")
+    seq, cl: int64 [B] -> fp32 [B, n_pos], -inf for t >= cl.  Positions >= cl are not read.  cand: bool [B, 1,
+    >= n_pos] (the candidate mask of dsv41/decode.py:311-315): positions that are not candidates score -inf."""
     B, _, H, D = q.shape
     dev = require_gpu(q, index_k, weights)
     out = torch.empty(B, index_k.shape[1], device=dev, dtype=torch.float32)
-    _score(q, index_k, weights, as_i64(seq.reshape(-1), dev), as_i64(cl.reshape(-1), dev), k_scale, out, True, None)
+    _score(q, index_k, weights, as_i64(seq.reshape(-1), dev), as_i64(cl.reshape(-1), dev), k_scale, out, True, None,
+           cand=cand)
     return out
 
 
@@ -93,13 +105,13 @@ class DecodeSelector:
             self.fnbytes = lib().dsv41_index_select_workspace_bytes(rows, self.n_sel)
             self.fws = torch.zeros(self.fnbytes // 4, dtype=torch.int32, device=device)
 
-    def score_into(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None) -> None:
+    def score_into(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None, cand=None) -> None:
         """The score kernel alone (scores + histogram into this object's buffers)."""
         require_gpu(q, index_k, weights)
         B = q.shape[0]
         if B != self.rows or index_k.shape[1] != self.n_pos:
             raise RuntimeError(f"DecodeSelector built for {self.rows} x {self.n_pos}, got {B} x {index_k.shape[1]}")
-        _score(q, index_k, weights, seq, cl, k_scale, self.score, False, self.ws, prepared)
+        _score(q, index_k, weights, seq, cl, k_scale, self.score, False, self.ws, prepared, cand=cand)
 
     def select(self, cl) -> torch.Tensor:
         """Top-k from the buffered scores + histogram; leaves the histogram zeroed."""
@@ -107,16 +119,17 @@ class DecodeSelector:
              ptr(self.ws), self.nbytes, ptr(self.out), self.k, stream(self.score.device))
         return self.out
 
-    def select_one_launch(self, q8, wf, H: int, index_k, k_scale, seq, cl) -> torch.Tensor:
+    def select_one_launch(self, q8, wf, H: int, index_k, k_scale, seq, cl, cand=None) -> torch.Tensor:
         """Scores + top-k in one launch from the prepared e4m3 queries (q8, wf)."""
         ks = k_scale if k_scale.dtype == torch.float32 else k_scale.float()
+        cp, cs = _cand_args(cand, self.rows, self.n_sel)
         call("dsv41_index_select", ptr(q8), 64 * 128, ptr(wf), 64, self.rows, H, ptr(index_k), index_k.stride(0),
              ptr(ks), ks.stride(0), ptr(seq), ptr(cl), self.n_sel, self.k, 0, ptr(self.fws), self.fnbytes,
-             ptr(self.score) if self.keep_scores else None, self.score.stride(0), ptr(self.out), self.k,
+             ptr(self.score) if self.keep_scores else None, self.score.stride(0), ptr(self.out), self.k, cp, cs,
              stream(self.score.device))
         return self.out
 
-    def __call__(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None) -> torch.Tensor:
+    def __call__(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None, cand=None) -> torch.Tensor:
         dev = require_gpu(q, index_k, weights)
         seq = as_i64(seq.reshape(-1), dev)
         cl = as_i64(cl.reshape(-1), dev)
@@ -125,6 +138,6 @@ class DecodeSelector:
                 raise RuntimeError(f"DecodeSelector built for {self.rows} x {self.n_pos}, got {q.shape[0]} x "
                                    f"{index_k.shape[1]}")
             q8, wf = prepared if prepared is not None else qprep(q, weights)
-            return self.select_one_launch(q8, wf, q.shape[2], index_k, k_scale, seq, cl)
-        self.score_into(q, index_k, weights, seq, cl, k_scale, prepared)
+            return self.select_one_launch(q8, wf, q.shape[2], index_k, k_scale, seq, cl, cand)
+        self.score_into(q, index_k, weights, seq, cl, k_scale, prepared, cand)
         return self.select(cl)

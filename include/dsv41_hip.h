@@ -58,11 +58,14 @@ int dsv41_sattn2(const void* q, const void* kv_win, long win_sstride, int win, c
  * slot(r) = seq[r] (or r / rows_per_slot when seq is null); cl(r) = cl[r] (or (cl_start + r % rows_per_slot + 1) /
  * cl_ratio, the causal compressed length of a prefill chunk, dsv41/model.py:819-830, when cl is null).
  * hist (may be null): [R, 4096] int32 histogram of the top 12 bits of the order-preserving key of every score
- * written (t < cl), accumulated atomically -- the input of dsv41_select_topk; it must be zero on entry. */
+ * written (t < cl), accumulated atomically -- the input of dsv41_select_topk; it must be zero on entry.
+ * cand (may be null): candidate mask [R, >= n_pos] bytes (row stride cand_rstride; nonzero = candidate), the CAND
+ * argument of dsv41/fused3.py:20-41 and the consumer mask of dsv41/model.py:854-866: t < cl(r) that is not a
+ * candidate scores -inf (and is still a valid position for the top-k). */
 int dsv41_index_score(const void* q, long q_rstride, const float* w, long w_rstride, int R, int HI, int D, int kfmt,
                       const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
                       int rows_per_slot, const long* cl, long cl_start, int cl_ratio, int n_pos, int write_masked,
-                      float* out, long out_rstride, int* hist, void* stream);
+                      float* out, long out_rstride, int* hist, const void* cand, long cand_rstride, void* stream);
 
 /* Index-query preparation for the e4m3 score path (the query side of dsv41/decode.py:284-288 after the reference's
  * FP4 rounding): per (row, head) a power-of-two scale 2^e = 2^ceil(log2(amax/448)), q8 = e4m3(q / 2^e) and
@@ -93,11 +96,26 @@ long dsv41_index_select_workspace_bytes(int R, int n_pos);
  * workgroups meet at two barriers) and n_pos <= 262144; otherwise hipErrorInvalidValue (use dsv41_index_score +
  * dsv41_select_topk).  n_pos may be less than the key table's rows (the decode tables' spare last row is never
  * valid); a cl[r] > n_pos is clamped to n_pos and sets the workspace's last-but-three int32 to 2.  A barrier wait
- * that gives up (a workgroup never arrived) sets it to 1. */
+ * that gives up (a workgroup never arrived) sets it to 1.  cand (may be null): candidate mask as in
+ * dsv41_index_score (dsv41/decode.py:311-315). */
 int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_rstride, int R, int HI,
                        const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
                        const long* cl, int n_pos, int k, int offset, void* ws, long ws_bytes, float* score_out,
-                       long score_rstride, int* out, long out_rstride, void* stream);
+                       long score_rstride, int* out, long out_rstride, const void* cand, long cand_rstride,
+                       void* stream);
+
+/* Workspace of dsv41_candidate_blocks (block maxima and the selected blocks of every row). */
+long dsv41_candidate_blocks_workspace_bytes(int R, int n, int topk_blocks, int block_size);
+
+/* select_candidate_blocks (dsv41/model.py:256-265) on the masked scores of the candidate source layer
+ * (dsv41/model.py:838-852, dsv41/decode.py:309-313): per row r the maxima of score[r, b*bs .. (b+1)*bs) over
+ * positions < cl(r) (others count as -inf), the block of position cl(r) - 1 forced to +inf, the topk_blocks largest
+ * blocks kept when their value is finite (ties: lowest block first; the reference leaves them unspecified), expanded
+ * to mask[r, 0 .. width) bytes (1 = candidate) -- the block covering t, also past n.  cl(r) = cl[r], or
+ * (cl_start + r % rows_per_seq + 1) / cl_ratio when cl is null.  score: fp32 [R, >= n] (row stride ld), n <= width. */
+int dsv41_candidate_blocks(const float* score, long ld, int R, int n, int width, const long* cl, long cl_start,
+                           int cl_ratio, int rows_per_seq, int topk_blocks, int block_size, void* mask,
+                           long mask_rstride, void* ws, long ws_bytes, void* stream);
 
 /* fused3.topk_indices + cuda/topk_select.cu (dsv41/fused3.py:65-75, dsv41/cuda/topk_select.cu:94-168), also the
  * selection of Indexer.__call__ (dsv41/model.py:868-893): per row the k largest of score[r, 0..c) with c =

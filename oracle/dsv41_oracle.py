@@ -32,6 +32,10 @@ PINNING = {
     "topk": "brute force: sorted(range(n), key=(-score, index))[:k] on small n; ascending + -1 mask",
     "kv_write": "composition rmsnorm -> bf16 -> rope -> bf16 -> fq8 (dsv41/test_fused2_units.py:39-49)",
     "fp8_key_encode": "exact round trip of FP4-grid rows through e4m3 + per-row pow2 scale (closed-form argument)",
+    "window_kv": "brute force: histories == the last rows produced before each chunk; ring == the last W rows",
+    "select_candidate_blocks": "properties of the top blocks (forced last block, count, every kept block max >= every "
+                               "dropped finite one, whole blocks); indexer with candidates chunked == full exactly "
+                               "(dsv41/test_long_prefill.py:66-96)",
 }
 
 
@@ -339,15 +343,45 @@ def topk_indices(score, k: int, cl) -> np.ndarray:
     return out
 
 
+def select_candidate_blocks(score, cl, topk_blocks: int, block_size: int) -> np.ndarray:
+    """select_candidate_blocks (dsv41/model.py:256-265) on score rows [R, T] whose positions >= cl[r] are masked:
+    block maxima over block_size positions (positions >= cl count as -inf), the block of position cl - 1 forced to
+    +inf, the min(topk_blocks, n_blocks) largest kept when finite (ties -> lower block, this build's rule), expanded
+    to a bool mask [R, T]."""
+    score = np.asarray(score, np.float32)
+    R, T = score.shape
+    nb = -(-T // block_size)
+    out = np.zeros((R, T), bool)
+    for r in range(R):
+        c = int(min(max(int(cl[r]), 0), T))
+        m = np.full(nb, -np.inf, np.float32)
+        for blk in range(nb):
+            seg = score[r, blk * block_size:min((blk + 1) * block_size, c)]
+            if seg.size:
+                m[blk] = seg.max()
+        if c > 0:
+            m[(c - 1) // block_size] = np.inf
+        order = sorted(range(nb), key=lambda blk: (-m[blk], blk))
+        for blk in order[:min(topk_blocks, nb)]:
+            if m[blk] > -np.inf:
+                out[r, blk * block_size:(blk + 1) * block_size] = True
+    return out
+
+
 def indexer_prefill(q, weights, index_k, start_pos: int, ratio: int, topk: int, offset: int, k_scale=None,
-                    query_chunk: int = 64) -> np.ndarray:
+                    query_chunk: int = 64, candidates=None, candidate_source=None):
     """Indexer.__call__ for seqlen > 1 (dsv41/model.py:766-893): score = sum_h w relu(q_h . K^T) per query chunk,
-    causal mask t >= (start+i+1)//ratio, top-min(topk, end//ratio), ascending, +offset, -1 where masked.
-    q [b,s,H,D], weights [b,s,H], index_k [b,T,D] -> int32 [b,s,min(topk,end//ratio)]."""
+    causal mask t >= (start+i+1)//ratio, [candidate mask], top-min(topk, end//ratio), ascending, +offset, -1 where
+    masked.  q [b,s,H,D], weights [b,s,H], index_k [b,T,D] -> int32 [b,s,min(topk,end//ratio)].
+    candidates (bool [b, s, >= T], a consumer layer, :854-866): scores of non-candidates are -inf (they stay valid
+    positions: the selection takes them last, lowest index first).  candidate_source = (topk_blocks, block_size) (the
+    source layer, :838-852): also returns the mask of select_candidate_blocks over the masked scores, [b, s, T]."""
     q = np.asarray(q, np.float32)
     b, s, H, D = q.shape
     kk = min(topk, (start_pos + s) // ratio)
     out = np.full((b, s, kk), -1, np.int32)
+    T = np.asarray(index_k).shape[1]
+    cmask = np.zeros((b, s, T), bool) if candidate_source is not None else None
     for bi in range(b):
         k = np.asarray(index_k[bi], np.float32)
         if k_scale is not None:
@@ -358,9 +392,13 @@ def indexer_prefill(q, weights, index_k, start_pos: int, ratio: int, topk: int, 
             for h in range(H):
                 sc += np.asarray(weights[bi, q0:q1, h], np.float32)[:, None] * np.maximum(q[bi, q0:q1, h] @ k.T, 0)
             cls = (start_pos + np.arange(q0, q1) + 1) // ratio
+            if candidate_source is not None:
+                cmask[bi, q0:q1] = select_candidate_blocks(sc, cls, candidate_source[0], candidate_source[1])
+            elif candidates is not None:
+                sc = np.where(np.asarray(candidates[bi, q0:q1, :k.shape[0]], bool), sc, -np.inf).astype(np.float32)
             sel = topk_indices(sc, kk, cls)
             out[bi, q0:q1] = np.where(sel >= 0, sel + offset, -1)
-    return out
+    return (out, cmask) if candidate_source is not None else out
 
 
 # ----------------------------------------------------------------------------------------------- appends

@@ -493,6 +493,97 @@ def test_decode_selector_long_row(n, cl):
     assert err <= 1e-2, err
 
 
+def test_candidate_blocks_select():
+    """select_candidate_blocks (dsv41/model.py:256-265) on masked scores: identical masks to the oracle (ties between
+    block maxima included), per-row valid counts covering whole, partial, single and empty rows."""
+    import dsv41_amd.indexer as I
+    r = rng(18)
+    R, T = 7, 1000
+    sc = r.standard_normal((R, T)).astype(np.float32)
+    sc[3] = np.round(sc[3])  # ties between blocks
+    cls = [1000, 999, 513, 400, 64, 1, 0]
+    for bs, kb in [(8, 16), (64, 4), (16, 1000)]:
+        print(f"[candidate blocks] bs {bs} kb {kb}", flush=True)
+        want = O.select_candidate_blocks(sc, cls, kb, bs)
+        masked = np.where(np.arange(T)[None, :] < np.asarray(cls)[:, None], sc, -np.inf).astype(np.float32)
+        got = I.select_candidate_blocks(f32(masked), i64(cls).view(R, 1), kb, bs).cpu().numpy()
+        np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "e4m3"])
+def test_index_topk_candidates(fmt):
+    """Indexer.__call__ with candidate blocks (dsv41/model.py:838-866): the source layer's mask equals the oracle's on
+    the kernel's own scores; a consumer layer's selection equals the oracle's top-k on its own masked scores (sparse
+    masks: the non-candidates fill the selection, lowest index first)."""
+    import dsv41_amd
+    r = rng(19)
+    b, s, H, D, start, ratio, topk = 1, 80, 64, 128, 900, 4, 64
+    T = (start + s) // ratio
+    q = _fp4_rows(r, (b, s, H, D), 1.0)
+    w = O.bf16(r.standard_normal((b, s, H)).astype(np.float32) * 0.1)
+    keys = _fp4_rows(r, (b, T + 10, D))
+    if fmt == "bf16":
+        kt, ks = bf(keys), None
+    else:
+        q8, s8 = O.key_encode_fp8(keys)
+        kt, ks = torch.from_numpy(q8).to(torch.float8_e4m3fn).to(DEV), f32(s8[..., 0])
+    cls = (start + np.arange(s) + 1) // ratio
+    idx, score, mask = dsv41_amd.index_topk(bf(q), bf(w), kt, start, ratio, topk, 0, k_scale=ks, return_score=True,
+                                            candidate_source=(6, 8))
+    sc = score.cpu().numpy()[0]
+    sc = np.where(np.arange(T)[None, :] < cls[:, None], sc, -np.inf).astype(np.float32)
+    want_mask = O.select_candidate_blocks(sc, cls, 6, 8)
+    got_mask = mask.cpu().numpy()[0]
+    np.testing.assert_array_equal(got_mask[:, :T], want_mask)
+    # a block straddling T extends past it (the reference's repeat_interleave over the key table width); beyond: none
+    straddle = (T + 7) // 8 * 8 - T
+    np.testing.assert_array_equal(got_mask[:, T:T + straddle], np.repeat(got_mask[:, T - 1:T], straddle, axis=1))
+    assert not got_mask[:, T + straddle:].any()
+    np.testing.assert_array_equal(idx.cpu().numpy()[0], O.topk_indices(sc, min(topk, T), cls))
+    for cand in [mask, torch.from_numpy(r.random((b, s, T + 10)) > 0.95).to(DEV)]:
+        idx2, score2 = dsv41_amd.index_topk(bf(q), bf(w), kt, start, ratio, topk, 0, k_scale=ks, return_score=True,
+                                            candidates=cand)
+        sc2 = score2.cpu().numpy()[0]
+        sc2 = np.where(np.arange(T)[None, :] < cls[:, None], sc2, -np.inf).astype(np.float32)
+        cm = cand.cpu().numpy()[0, :, :T]
+        assert np.all(np.isneginf(sc2[(~cm) & (np.arange(T)[None, :] < cls[:, None])]))
+        np.testing.assert_array_equal(sc2[cm & np.isfinite(sc2)], sc[cm & np.isfinite(sc2)])
+        np.testing.assert_array_equal(idx2.cpu().numpy()[0], O.topk_indices(sc2, min(topk, T), cls))
+
+
+def test_decode_candidates():
+    """Decode indexer with a candidate mask (dsv41/decode.py:309-315): fused3.index_score(cand=...) scores -inf
+    exactly at the non-candidates; the one-launch selector and the two-kernel path select the oracle's top-k of those
+    scores (non-candidates as last-resort fillers, lowest index first)."""
+    from dsv41_amd.fused3 import DecodeSelector, index_score
+    from dsv41_amd.workloads import encode_e4m3_rows, fp4_round
+    g = torch.Generator(device=DEV).manual_seed(20)
+    R, H, n = 4, 64, 6001
+    cls = [6000, 4097, 3000, 100]
+    keys = fp4_round(torch.randn(3, n, 128, generator=g, device=DEV) * 0.1)
+    k8, ks = encode_e4m3_rows(keys)
+    q = fp4_round(torch.randn(R, 1, H, 128, generator=g, device=DEV))
+    w = (torch.randn(R, H, generator=g, device=DEV) * 0.01).to(torch.bfloat16)
+    seq = i64([0, 2, 1, 2])
+    cand = torch.rand(R, 1, n, generator=g, device=DEV) > 0.6
+    cand[1, 0, :] = torch.arange(n, device=DEV) % 97 == 0  # row 1: fewer candidates than k
+    base = index_score(q, k8, w, seq, i64(cls), k_scale=ks).cpu().numpy()
+    sc = index_score(q, k8, w, seq, i64(cls), cand=cand, k_scale=ks).cpu().numpy()
+    cm = cand.cpu().numpy()[:, 0]
+    for i, c in enumerate(cls):
+        np.testing.assert_array_equal(sc[i, :c][cm[i, :c]], base[i, :c][cm[i, :c]])
+        assert np.all(np.isneginf(sc[i, :c][~cm[i, :c]]))
+    want = O.topk_indices(sc, 2048, cls)
+    for one in (True, False):
+        sel = DecodeSelector(R, n, 2048, DEV, keep_scores=True, max_cl=n - 1 if one else None)
+        if not one:
+            sel.one_launch = False
+        print(f"[decode candidates] one_launch {sel.one_launch}", flush=True)
+        idx = sel(q, k8, w, seq, i64(cls), k_scale=ks, cand=cand)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(idx.cpu().numpy()[:, 0], want)
+
+
 def test_topk_many_rows_bit_exact():
     """Prefill-shaped selection (many rows of <= 17408 positions: the 256-thread top-k), causal limits per row."""
     import dsv41_amd

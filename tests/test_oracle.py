@@ -291,3 +291,65 @@ def test_window_kv_history_brute_force():
     out, _ = O.window_kv(x, w, cos, sin, 100, np.zeros((W, D), np.float32), rd, 1e-6)
     cache = O.kv_write(x, w, cos, sin, [100, 101, 102], [0, 0, 0], np.zeros((1, W, D), np.float32), rd, 1e-6)
     np.testing.assert_array_equal(out[W - 1:], cache[0, [100 % W, 101 % W, 102 % W]])
+
+
+def test_select_candidate_blocks_properties():
+    """select_candidate_blocks (dsv41/model.py:256-265): the block of the last valid position is always kept; exactly
+    min(topk_blocks, blocks with a finite maximum) blocks are kept; every kept block's maximum is >= every dropped
+    finite block's maximum (strictly > with ties broken to the lower block); the mask is a union of whole blocks."""
+    r = np.random.default_rng(21)
+    T, bs, kb = 203, 8, 5
+    sc = r.standard_normal((6, T)).astype(np.float32)
+    sc[2] = np.round(sc[2])  # ties between block maxima
+    cls = [203, 150, 77, 8, 1, 0]
+    m = O.select_candidate_blocks(sc, cls, kb, bs)
+    nb = -(-T // bs)
+    for i, c in enumerate(cls):
+        blocks = [m[i, b * bs:(b + 1) * bs] for b in range(nb)]
+        assert all(x.all() or not x.any() for x in blocks)
+        kept = [b for b in range(nb) if blocks[b].any()]
+        bmax = [sc[i, b * bs:min((b + 1) * bs, c)].max() if b * bs < c else -np.inf for b in range(nb)]
+        finite = [b for b in range(nb) if bmax[b] > -np.inf]
+        assert len(kept) == min(kb, len(finite))
+        if c > 0:
+            assert (c - 1) // bs in kept
+        others = [b for b in kept if b != (c - 1) // bs]
+        dropped = [b for b in finite if b not in kept]
+        for a in others:
+            for d in dropped:
+                assert bmax[a] > bmax[d] or (bmax[a] == bmax[d] and a < d)
+    assert not m[5].any()  # no valid position: nothing kept (the forced block does not exist)
+
+
+@pytest.mark.parametrize("start", [0, 3, 1025])
+def test_indexer_candidates_chunk_invariant(start):
+    """dsv41/test_long_prefill.py:66-96 with candidates: for the plain, source and consumer modes, query chunks of 32
+    give exactly the selections (and source masks) of a single chunk."""
+    r = np.random.default_rng(22)
+    n, H, D, ratio, topk = 137, 2, 8, 2, 16
+    T = (start + n) // ratio
+    q = r.standard_normal((1, n, H, D)).astype(np.float32)
+    w = r.standard_normal((1, n, H)).astype(np.float32)
+    keys = r.standard_normal((1, T, D)).astype(np.float32)
+    cand = r.random((1, n, T)) > 0.3
+    for mode in ("plain", "source", "consumer"):
+        kw = {"candidate_source": (4, 8)} if mode == "source" else ({"candidates": cand} if mode == "consumer" else {})
+        full = O.indexer_prefill(q, w, keys, start, ratio, topk, 128, query_chunk=10000, **kw)
+        part = O.indexer_prefill(q, w, keys, start, ratio, topk, 128, query_chunk=32, **kw)
+        if mode == "source":
+            np.testing.assert_array_equal(full[0], part[0])
+            np.testing.assert_array_equal(full[1], part[1])
+        else:
+            np.testing.assert_array_equal(full, part)
+    # consumer: fewer finite candidates than topk -> the non-candidates (score -inf) fill in, lowest index first
+    sparse = np.zeros((1, n, T), bool)
+    sparse[:, :, ::9] = True
+    sel = O.indexer_prefill(q, w, keys, start, ratio, topk, 0, candidates=sparse)
+    i = n - 1
+    c = (start + i + 1) // ratio
+    finite = [t for t in range(0, c, 9)]
+    row = sel[0, i][sel[0, i] >= 0]
+    assert set(finite[:topk]) <= set(row.tolist()) or len(finite) > topk
+    if len(finite) < topk:
+        fill = [t for t in range(c) if t % 9 != 0][:topk - len(finite)]
+        assert sorted(row.tolist()) == sorted(finite + fill)
