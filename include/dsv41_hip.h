@@ -47,6 +47,29 @@ int dsv41_sattn2(const void* q, const void* kv_win, long win_sstride, int win, c
                  const long* plim, const float* sink, const float* cos_t, const float* sin_t, int rd, float scale,
                  void* out, int B, int h, int dqk, int dv, int want_nsplit, void* ws, long ws_bytes, void* stream);
 
+/* ------------------------------------------------------------------------------------------------ compressor */
+
+/* Compressor pooling of the decode step, DecodeRuntime.compressor2 (dsv41/decode.py:243-265) after the wkv / wgate
+ * projections: row r (position pos[r] of sequence seq[r]) writes kv[r], score[r] (fp32 [B, D], row stride x_rstride)
+ * to ring slot pos % ring of ring_kv / ring_sc ([S, ring, D] fp32, sequence stride ring_sstride; initialise kv 0 and
+ * score -inf), then pools the group of the `ratio` positions ending at pos[r] from the ring: per channel
+ * sum_q kv[q] softmax_q(score[q]), cast to bf16, rmsnorm(norm_w bf16 [D], eps) -> latent[r] bf16; should[r] (bytes)
+ * = (pos + 1) % ratio == 0.  Two launches (all ring writes before any pooling: drafts of one sequence see each other).
+ * D <= 1024, 1 <= ratio <= min(16, ring). */
+int dsv41_compress_pool_decode(const float* kv, const float* score, long x_rstride, float* ring_kv, float* ring_sc,
+                               long ring_sstride, int ring, const long* pos, const long* seq, int B, int D, int ratio,
+                               const void* norm_w, float eps, void* latent, long lat_rstride, void* should,
+                               void* stream);
+
+/* Compressor pooling of a prefill chunk, Compressor.__call__ (dsv41/model.py:593-660) after the projections, for one
+ * sequence: positions start_pos .. start_pos + n_rows - 1 with kv / score fp32 [n_rows, D]; every group of `ratio`
+ * positions that closes inside the chunk (n_groups of them, checked) is pooled as above into latent[g] (members before
+ * start_pos from the ring: the continuation's partial group, :600-606); then the chunk's last min(n_rows, ring)
+ * positions go to the ring ([ring, D] fp32 each). */
+int dsv41_compress_pool_prefill(const float* kv, const float* score, long x_rstride, float* ring_kv, float* ring_sc,
+                                int ring, long start_pos, int n_rows, int D, int ratio, const void* norm_w, float eps,
+                                void* latent, long lat_rstride, int n_groups, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ indexer */
 
 /* fused3.index_score (dsv41/fused3.py:20-62) and the score half of Indexer.__call__ (dsv41/model.py:766-893):

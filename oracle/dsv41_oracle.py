@@ -33,6 +33,9 @@ PINNING = {
     "kv_write": "composition rmsnorm -> bf16 -> rope -> bf16 -> fq8 (dsv41/test_fused2_units.py:39-49)",
     "fp8_key_encode": "exact round trip of FP4-grid rows through e4m3 + per-row pow2 scale (closed-form argument)",
     "window_kv": "brute force: histories == the last rows produced before each chunk; ring == the last W rows",
+    "compress_pool": "fed as any mix of prefill chunks and single decode rows, every closed group's latent equals the "
+                     "one-call start_pos 0 result; equal gate scores give the group mean, one dominant score gives that "
+                     "member; vs torch.softmax composition (library routine)",
     "select_candidate_blocks": "properties of the top blocks (forced last block, count, every kept block max >= every "
                                "dropped finite one, whole blocks); indexer with candidates chunked == full exactly "
                                "(dsv41/test_long_prefill.py:66-96)",
@@ -431,6 +434,64 @@ def window_kv(x, w, cos, sin, start_pos: int, ring, rd, eps):
     for r in range(max(0, s - W), s):
         ring[(start_pos + r) % W] = rows[r]
     return np.concatenate([history, rows]), ring
+
+
+def _pool(kv: np.ndarray, score: np.ndarray) -> np.ndarray:
+    """sum over axis -2 of kv * softmax(score, axis -2) in fp32 (dsv41/model.py:624, 645, dsv41/decode.py:263)."""
+    m = score.max(axis=-2, keepdims=True)
+    e = np.exp((score - m).astype(np.float32))
+    return (kv * (e / e.sum(axis=-2, keepdims=True))).sum(axis=-2).astype(np.float32)
+
+
+def compress_pool(kv, score, start_pos: int, ratio: int, ring_kv, ring_sc, norm_w, eps):
+    """Compressor.__call__ after the wkv / wgate projections (dsv41/model.py:593-660) for one sequence: kv, score fp32
+    [s, D] at positions start_pos..; a continuation's partial group takes its earlier members from the ring
+    (:600-606); every group that closes in the chunk is pooled, cast to bf16 and rmsnormed (:656-660); the chunk's last
+    min(s, RING) positions then go to the ring (:607-610, written here after the partial read, as there).  Returns
+    (latents bf16-valued [n_groups, D] (None when a continuation closes no group), ring_kv, ring_sc) (copies)."""
+    kv = np.asarray(kv, np.float32)
+    score = np.asarray(score, np.float32)
+    ring_kv = np.array(ring_kv, np.float32, copy=True)
+    ring_sc = np.array(ring_sc, np.float32, copy=True)
+    R = ring_kv.shape[0]
+    s = kv.shape[0]
+    partial = start_pos % ratio
+    pk = np.stack([ring_kv[(start_pos - partial + j) % R] for j in range(partial)]) if partial else kv[:0]
+    ps = np.stack([ring_sc[(start_pos - partial + j) % R] for j in range(partial)]) if partial else score[:0]
+    for j in range(max(0, s - R), s):
+        ring_kv[(start_pos + j) % R] = kv[j]
+        ring_sc[(start_pos + j) % R] = score[j]
+    allk = np.concatenate([pk, kv])  # positions start_pos - partial ..
+    alls = np.concatenate([ps, score])
+    n_groups = allk.shape[0] // ratio
+    if n_groups == 0:
+        return (np.zeros((0, kv.shape[1]), np.float32) if start_pos == 0 else None), ring_kv, ring_sc
+    g = _pool(allk[:n_groups * ratio].reshape(n_groups, ratio, -1), alls[:n_groups * ratio].reshape(n_groups, ratio, -1))
+    return bf16(rmsnorm(bf16(g), norm_w, eps)), ring_kv, ring_sc
+
+
+def compress_pool_decode(kv, score, pos, seq, ratio: int, ring_kv, ring_sc, norm_w, eps):
+    """DecodeRuntime.compressor2 after the projections (dsv41/decode.py:243-265): every row's kv / score go to
+    ring[seq, pos % RING] (all rows first, :258-259); each row then pools the `ratio` positions ending at pos from the
+    ring (ratio 2: pos - 1 and pos, :260-263) -> bf16 -> rmsnorm; should = (pos + 1) % ratio == 0.  ring_* [S, RING, D].
+    Returns (latent [B, D], should [B] bool, ring_kv, ring_sc)."""
+    kv = np.asarray(kv, np.float32)
+    score = np.asarray(score, np.float32)
+    ring_kv = np.array(ring_kv, np.float32, copy=True)
+    ring_sc = np.array(ring_sc, np.float32, copy=True)
+    R = ring_kv.shape[1]
+    pos = [int(p) for p in pos]
+    seq = [int(x) for x in seq]
+    for r in range(kv.shape[0]):
+        ring_kv[seq[r], pos[r] % R] = kv[r]
+        ring_sc[seq[r], pos[r] % R] = score[r]
+    lat = []
+    for r in range(kv.shape[0]):
+        sl = [(pos[r] - ratio + 1 + j) % R for j in range(ratio)]
+        lat.append(_pool(ring_kv[seq[r], sl], ring_sc[seq[r], sl]))
+    lat = bf16(rmsnorm(bf16(np.stack(lat)), norm_w, eps))
+    should = np.array([(p + 1) % ratio == 0 for p in pos])
+    return lat, should, ring_kv, ring_sc
 
 
 def compress_row(latent, cos, sin, pos, rd) -> np.ndarray:

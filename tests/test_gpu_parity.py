@@ -619,3 +619,43 @@ def test_sparse_attn_prefill_shape(dqk, dv, h):
     scale = dqk ** -0.5
     o = host(dsv41_amd.sparse_attn(bf(q), bf(kv), f32(sink), torch.from_numpy(idx).to(DEV), scale, d_v=dv))
     attn_close(o, O.sparse_attn(q, kv, sink, idx, scale, dv=dv), f"prefill {dqk}/{dv} h={h}")
+
+
+@pytest.mark.parametrize("ratio", [2, 4])
+def test_compress_pool_chunks(ratio):
+    """Compressor.__call__ / DecodeRuntime.compressor2 (dsv41/model.py:593-660, dsv41/decode.py:243-265) after the
+    projections: a sequence fed as prefill chunks (fresh, continuations with and without a partial group, longer than
+    the ring) and decode steps of two sequences at once; latents (bf16, rmsnormed) within one bf16 step of the oracle,
+    should flags and the fp32 rings exact."""
+    import dsv41_amd  # noqa: F401
+    from dsv41_amd import compressor as CP
+    r = rng(33)
+    D, R, S = 512, 8, 2
+    w = O.bf16(r.random(D).astype(np.float32) + 0.5)
+    rk_t, rs_t = CP.new_rings(S, D, DEV)
+    rk = np.zeros((S, R, D), np.float32)
+    rs = np.full((S, R, D), -np.inf, np.float32)
+    start = 0
+    for s in [5, 1, 1, 7, 1, 30, 2, 1, 1, 3]:
+        kv = r.standard_normal((S, s, D)).astype(np.float32)
+        sc = (2 * r.standard_normal((S, s, D))).astype(np.float32)
+        print(f"[compress_pool] ratio {ratio} start {start} chunk {s}", flush=True)
+        if s == 1 and start > 0:
+            lat, should = CP.compress_pool_decode(f32(kv), f32(sc), i64([start, start + 3]), i64([0, 1]), ratio,
+                                                  rk_t, rs_t, bf(w), 1e-6)
+            # sequence 1 runs 3 positions ahead (its own ring), as a second slot of the decode batch
+            want, wshould, rk, rs = O.compress_pool_decode(kv[:, 0], sc[:, 0], [start, start + 3], [0, 1], ratio, rk,
+                                                           rs, w, 1e-6)
+            np.testing.assert_array_equal(host(should), wshould)
+            np.testing.assert_allclose(host(lat[:, 0]), want, rtol=2 ** -7, atol=1e-5)
+        else:
+            got = CP.compress_pool(f32(kv[:1]), f32(sc[:1]), start, ratio, rk_t[:1], rs_t[:1], bf(w), 1e-6)
+            want, rk[0], rs[0] = O.compress_pool(kv[0], sc[0], start, ratio, rk[0], rs[0], w, 1e-6)
+            if want is None:
+                assert got is None
+            else:
+                assert got.shape == (1,) + want.shape
+                np.testing.assert_allclose(host(got[0]), want, rtol=2 ** -7, atol=1e-5)
+        np.testing.assert_array_equal(host(rk_t), rk)
+        np.testing.assert_array_equal(host(rs_t), rs)
+        start += s

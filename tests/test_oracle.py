@@ -353,3 +353,61 @@ def test_indexer_candidates_chunk_invariant(start):
     if len(finite) < topk:
         fill = [t for t in range(c) if t % 9 != 0][:topk - len(finite)]
         assert sorted(row.tolist()) == sorted(finite + fill)
+
+
+@pytest.mark.parametrize("ratio", [2, 4])
+def test_compress_pool_chunk_invariant(ratio):
+    """Compressor.__call__ / DecodeRuntime.compressor2 (dsv41/model.py:593-660, dsv41/decode.py:243-265): a sequence
+    fed as a mix of prefill chunks and single decode rows yields, for every group that closes, the latent of the
+    one-call start_pos 0 pooling of the whole sequence; decode rows that do not close a group say should=False."""
+    r = np.random.default_rng(31)
+    D, R, n = 64, 8, 57
+    kv = r.standard_normal((n, D)).astype(np.float32)
+    sc = (2 * r.standard_normal((n, D))).astype(np.float32)
+    w = O.bf16(r.random(D).astype(np.float32) + 0.5)
+    ring0 = (np.zeros((R, D), np.float32), np.full((R, D), -np.inf, np.float32))
+    full, _, _ = O.compress_pool(kv, sc, 0, ratio, *ring0, w, 1e-6)
+    assert full.shape == (n // ratio, D)
+    got = {}
+    rk, rs = ring0
+    start = 0
+    for s in [3, 1, 1, 6, 1, 13, 1, 2, 20, 1, 1, 1, 1, 5]:
+        s = min(s, n - start)
+        if s == 1 and start > 0:
+            lat, should, rk3, rs3 = O.compress_pool_decode(kv[start:start + 1], sc[start:start + 1], [start], [0], ratio,
+                                                           rk[None], rs[None], w, 1e-6)
+            rk, rs = rk3[0], rs3[0]
+            assert should[0] == ((start + 1) % ratio == 0)
+            if should[0]:
+                got[start // ratio] = lat[0]
+        else:
+            lat, rk, rs = O.compress_pool(kv[start:start + s], sc[start:start + s], start, ratio, rk, rs, w, 1e-6)
+            first = start // ratio
+            for g in range(0 if lat is None else lat.shape[0]):
+                got[first + g] = lat[g]
+        start += s
+    assert start == n and sorted(got) == list(range(n // ratio))
+    for g in range(n // ratio):
+        np.testing.assert_array_equal(got[g], full[g])
+
+
+def test_compress_pool_closed_forms():
+    """Equal gate scores pool to the group mean; a dominant gate score (+80 over the rest) selects its member; the
+    pooling equals the torch.softmax composition of dsv41/model.py:624."""
+    import torch
+    r = np.random.default_rng(32)
+    D, ratio = 32, 4
+    kv = r.standard_normal((12, D)).astype(np.float32)
+    w = np.ones(D, np.float32)
+    ring = (np.zeros((8, D), np.float32), np.full((8, D), -np.inf, np.float32))
+    eq, _, _ = O.compress_pool(kv, np.full((12, D), 0.3, np.float32), 0, ratio, *ring, w, 1e-6)
+    mean = kv.reshape(3, ratio, D).mean(axis=1)
+    np.testing.assert_array_equal(eq, O.bf16(O.rmsnorm(O.bf16(mean), w, 1e-6)))
+    sc = np.zeros((12, D), np.float32)
+    sc[2::ratio] = 80.0
+    dom, _, _ = O.compress_pool(kv, sc, 0, ratio, *ring, w, 1e-6)
+    np.testing.assert_array_equal(dom, O.bf16(O.rmsnorm(O.bf16(kv[2::ratio]), w, 1e-6)))
+    sc = r.standard_normal((12, D)).astype(np.float32)
+    t = (torch.from_numpy(kv).view(3, ratio, D) * torch.from_numpy(sc).view(3, ratio, D).softmax(dim=1)).sum(dim=1)
+    np.testing.assert_allclose(O._pool(kv.reshape(3, ratio, D), sc.reshape(3, ratio, D)), t.numpy(), rtol=1e-6,
+                               atol=1e-6)
