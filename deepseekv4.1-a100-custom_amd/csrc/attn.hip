@@ -49,6 +49,8 @@ struct AttnArgs {
   float* pl;
   float* pacc;  // [R, H, nsplit, DV]
   int* arrive;  // decode kernel: [R * head groups] split arrival counters (zero between launches), or null
+  unsigned long long* coop;  // with arrive, when every workgroup is resident at once: [R * head groups] counters
+                             // (launch epoch * 256 + arrivals), every split merges a slice; else null
   int units;    // with arrive: (row, 16-head group) units, placed upx per XCD (1-D grid of kXcds * upx * nsplit)
   int upx;
   const float* cos_t;
@@ -356,6 +358,86 @@ DSV41_DEV void merge_splits(const AttnArgs& a, int r, int h0, long pr, float (*w
   }
 }
 
+// Cooperative merge, run by every split workgroup sp of a unit once all nsplit have published: it merges
+// (head, 8-column group) elements [sp*E/ns, (sp+1)*E/ns) of the unit's E = 16 * DV / 8, one per thread.  The partials
+// were written with device-scope stores and are read with device-scope loads (coherent across the XCDs, wherever the
+// unit's workgroups ran).  Weights as merge_splits.
+// Device-scope (sc1) 16-byte accesses to the split partials of the cooperative merge: one request per 16 bytes, with
+// the cache policy of device-scope atomics (coherent across the XCDs).
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kCpolDevice = 16;  // sc1
+DSV41_DEV __amdgpu_buffer_rsrc_t pacc_rsrc(const float* pacc) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)pacc, 0, 0x7fffffff, 0x00020000);
+}
+
+template <int DV>
+DSV41_DEV void merge_slice(const AttnArgs& a, int r, int h0, long pr, int sp) {
+  constexpr int CG = DV / 8, E = 16 * CG;
+  static_assert(E / 2 <= 512, "a slice fits the workgroup (nsplit >= 2)");
+  constexpr int MS = 16;  // splits per batch of loads
+  const int ns = a.nsplit, H = a.H;
+  const int e = (int)((long)sp * E / ns) + (int)threadIdx.x;
+  if (e >= (int)((long)(sp + 1) * E / ns)) return;
+  const int hh = e / CG, c = (e - hh * CG) * 8, h = h0 + hh;
+  if (h >= H) return;
+  const long base = ((long)r * H + h) * ns;
+  const __amdgpu_buffer_rsrc_t rs = pacc_rsrc(a.pacc);
+  const float sink = a.sink[h];
+  float M = -1e30f, den = 0.0f, num[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll 1
+  for (int s0 = 0; s0 < ns; s0 += MS) {  // (online over batches: the weights are rescaled to the running maximum)
+    u32x4_t v[MS];
+    float m[MS], l[MS];
+#pragma unroll
+    for (int u = 0; u < MS; ++u) {
+      const bool ok = s0 + u < ns;
+      const long pi = base + (ok ? s0 + u : 0);
+      v[u] = ok ? __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((pi * DV + c) * 2), 0, kCpolDevice)
+                : u32x4_t{0, 0, 0, 0};
+      m[u] = ok ? __hip_atomic_load(a.pm + pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -1e30f;
+      l[u] = ok ? __hip_atomic_load(a.pl + pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+    }
+    float Mb = M;
+#pragma unroll
+    for (int u = 0; u < MS; ++u) Mb = fmaxf(Mb, m[u]);
+    const float f = exp2f((M - Mb) * kLog2e);
+    den *= f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) num[q] *= f;
+    M = Mb;
+#pragma unroll
+    for (int u = 0; u < MS; ++u) {
+      const float w = s0 + u < ns ? l[u] * exp2f((m[u] - M) * kLog2e) : 0.0f;
+      den += w;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t x = v[u][q];
+        num[2 * q] += w * __uint_as_float(x << 16);
+        num[2 * q + 1] += w * __uint_as_float(x & 0xffff0000u);
+      }
+    }
+  }
+  const float inv = 1.0f / (den + exp2f((sink - M) * kLog2e));
+  uint32_t pk[4];
+#pragma unroll
+  for (int q = 0; q < 8; q += 2) {
+    float re = round_bf16(num[q] * inv), im = round_bf16(num[q + 1] * inv);
+    const int cc = c + q;
+    if (a.rd > 0 && cc >= DV - a.rd) {
+      const int jj = (cc - (DV - a.rd)) >> 1;
+      const float cs = a.cos_t[pr * (a.rd / 2) + jj];
+      const float sn = -a.sin_t[pr * (a.rd / 2) + jj];
+      const float yr = re * cs - im * sn, yi = re * sn + im * cs;
+      re = yr;
+      im = yi;
+    }
+    pk[q / 2] = pack_bf16x2(re, im);
+  }
+  *(uint4*)(a.out + (long)r * a.out_rstride + (long)h * DV + c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+}
+
+constexpr int kCoopSpinLimit = 1 << 20;
+
 // Decode attention, 8 waves per workgroup (2 per SIMD): wave w handles key rows 16*(w&3)..+15 of every 64-key tile
 // and output columns [(w>>2)*DV/2, +DV/2) (QK^T and the softmax are computed by both column halves, identically).
 // The softmax keeps a reference maximum per head and rescales the accumulators only when the tile maximum exceeds
@@ -655,16 +737,51 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
 #pragma unroll
       for (int q = 0; q < 8; q += 2) pk[q / 2] = pack_bf16x2(v[q] * inv, v[q + 1] * inv);
       const long pi = ((long)r * H + hout) * a.nsplit + sp;
-      *(uint4*)((uint16_t*)a.pacc + pi * DV + c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-      if (c == 0) {
-        a.pm[pi] = M * ln2;  // natural-log units, as the merge expects
-        a.pl[pi] = L;
+      if (a.coop) {  // device-scope stores: read by the unit's other workgroups, possibly on other XCDs
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{pk[0], pk[1], pk[2], pk[3]}, pacc_rsrc(a.pacc),
+                                               (int)((pi * DV + c) * 2), 0, kCpolDevice);
+        if (c == 0) {
+          __hip_atomic_store(a.pm + pi, M * ln2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(a.pl + pi, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else {
+        *(uint4*)((uint16_t*)a.pacc + pi * DV + c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        if (c == 0) {
+          a.pm[pi] = M * ln2;  // natural-log units, as the merge expects
+          a.pl[pi] = L;
+        }
       }
     }
   }
   DSV41_TS(22);
   DSV41_PH(5);
   if (final_out || !a.arrive) {
+    DSV41_WG_TS(1);
+    return;
+  }
+  if (a.coop) {
+    // ---- every split workgroup of the unit merges a slice once all have published.  Counter = epoch * 256 +
+    // arrivals: the last arrival of a launch moves it to the next epoch (any nsplit <= 255, any history)
+    unsigned long long* cnt = a.coop + (long)r * ((H + 15) / 16) + hg;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned long long old = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned long long base = old & ~255ull;
+      if ((int)(old & 255) + 1 == a.nsplit) {
+        __hip_atomic_fetch_add(cnt, 256ull - a.nsplit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        int spins = 0;
+#pragma unroll 1
+        while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < base + a.nsplit &&
+               ++spins < kCoopSpinLimit)
+          __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    __syncthreads();
+    DSV41_PH(6);
+    merge_slice<DV>(a, r, h0, pr, sp);
+    DSV41_PH(7);
     DSV41_WG_TS(1);
     return;
   }
@@ -1379,6 +1496,21 @@ int dispatch(AttnArgs& a, int dqk, int dv, hipStream_t st) {
   return (int)hipErrorInvalidValue;
 }
 
+// Compute units per XCD of the current device (queried once per device).
+int cus_per_xcd() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n / kXcds;
+  }
+  return cached[dev];
+}
+
+constexpr int kFuseMaxSplits = 32;  // splits a decode launch merges itself
+
 // Split plan.  Decode kernel: <= 192 workgroups over (rows x 16-head groups x splits), >= 2 tiles of 64 keys per
 // split.  64-head kernel: >= 512 workgroups when rows are few, >= 2 tiles of 32 keys per split.
 void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
@@ -1390,8 +1522,8 @@ void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
     per = (tiles + want - 1) / want;
   } else if (dec) {
     // <= 192 workgroups (three quarters of the CUs; each holds one), >= 2 tiles per split; the decode kernel balances
-    // the tiles over the splits.  Measured at C2 (16 units): 12 splits 21.7 us, 16 splits 25.5 us; at C5 (192
-    // units): 1 split 39.7 us, 2 splits 49.1 us (a second round of workgroups).
+    // the tiles over the splits.  Measured at C2 (16 units, cooperative merge): 12 splits 19.5 us, 16 splits 20.2 us;
+    // at C5 (192 units): 1 split 39.7 us, 2 splits 49.1 us (a second round of workgroups).
     const long wgs = (long)R * ((H + 15) / 16);
     const int cap = tiles / 2 < 1 ? 1 : tiles / 2;
     int ns = (int)(wgs >= 192 ? 1 : 192 / wgs);
@@ -1412,15 +1544,18 @@ void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
 }
 
 // The decode kernel merges its own splits (XCD-local units) when there are enough units to occupy every XCD.
-constexpr int kFuseMaxSplits = 32;
 bool fuse_merge(int R, int H, int ns) { return ns > 1 && ns <= kFuseMaxSplits && (long)R * ((H + 15) / 16) >= kXcds; }
+
+// Decode-kernel workspace: the split arrival counters first (their size depends on R and H only, so calls with any
+// split count find them where the previous call left them at rest), then m, l (fp32) and the bf16 partials.
+long counter_bytes(int R, int H) {
+  const long units = (long)R * ((H + 15) / 16);
+  return (units * 4 + 8 + units * 8 + 255) / 256 * 256;  // int counters, pad, u64 counters
+}
 
 long workspace_bytes(int R, int H, int ns, int dv) {
   if (ns <= 1) return 0;
-  if (use_decode_kernel(R, H)) {  // m, l (fp32), bf16 partials, then the arrival counters
-    const long part = (long)R * H * ns * (8 + 2L * dv);
-    return fuse_merge(R, H, ns) ? part + (long)R * ((H + 15) / 16) * 4 : part;
-  }
+  if (use_decode_kernel(R, H)) return counter_bytes(R, H) + (long)R * H * ns * (8 + 2L * dv);
   return (long)R * H * ns * (2 + dv) * 4;
 }
 
@@ -1432,14 +1567,19 @@ int finish_plan(AttnArgs& a, int want_nsplit, void* ws, long ws_bytes, int dv) {
   if (ns > 1) {
     const long need = workspace_bytes(a.R, a.H, ns, dv);
     if (!ws || ws_bytes < need) return (int)hipErrorInvalidValue;
-    float* f = (float*)ws;
+    const bool dec = use_decode_kernel(a.R, a.H);
+    float* f = (float*)((char*)ws + (dec ? counter_bytes(a.R, a.H) : 0));
     a.pm = f;
     a.pl = f + (long)a.R * a.H * ns;
     a.pacc = f + 2L * a.R * a.H * ns;
-    if (use_decode_kernel(a.R, a.H) && fuse_merge(a.R, a.H, ns)) {
-      a.arrive = (int*)((char*)ws + (long)a.R * a.H * ns * (8 + 2L * dv));
+    if (dec && fuse_merge(a.R, a.H, ns)) {
       a.units = a.R * ((a.H + 15) / 16);
       a.upx = (a.units + kXcds - 1) / kXcds;
+      a.arrive = (int*)ws;
+      // cooperative merge when every workgroup of the launch can be resident at once (one per CU, the XCDs dealt
+      // round-robin): early arrivals wait for the rest of their unit
+      if ((long)a.upx * ns <= cus_per_xcd())
+        a.coop = (unsigned long long*)((char*)ws + ((long)a.units * 4 + 7) / 8 * 8);
     }
   }
   return 0;

@@ -8,18 +8,19 @@
 //   A. scores its 512 positions (8 waves x 64 keys, every key load issued up front, e4m3 keys against the prepared e4m3 queries, fp8 MFMA), keeps
 //      them in LDS, builds their 4096-bin histogram (top 12 bits of the order-preserving key) in LDS and adds it to
 //      the row's histogram with device-scope atomics
-//   B. row barrier 1; reads the row histogram: threshold bin B (where the running count from the top reaches k) and
-//      need = k - (entries above B)
+//   B. reads the row histogram until its total reaches the row's valid count (every chunk's additions have landed:
+//      this read is the row barrier and its data at once); threshold bin B (where the running count from the top
+//      reaches k) and need = k - (entries above B)
 //   C. classifies its positions (one per thread): entries above B are counted, bin-B candidates
-//      (key << 32 | ~position) stored in the chunk's slots, with the counts
-//   D. row barrier 2; clears its slice of the row histogram
-//   E. gathers every chunk's counts and candidates (the first kIsSpec of each chunk with the counts, in one round
-//      trip), threshold candidate T (exact ranks / radix passes over the candidates)
+//      (key << 32 | epoch tag << 18 | ~position) stored in the chunk's slots, then the counts with the launch epoch
+//   D. reads every chunk's count word and the first kIsSpec candidates of each chunk until all carry this launch's
+//      epoch (the second row barrier and the gather in one round trip); clears its slice of the row histogram
+//   E. threshold candidate T (exact ranks / radix passes over the candidates)
 //   F. writes its taken positions (above B, or candidates >= T) at their global offset.
 // Data exchanged between workgroups (histogram, counts, candidates) is written and read with device-scope atomic
 // operations, which the hardware keeps coherent across the XCDs' L2 caches, so no cache maintenance is needed.  The
-// row barriers use one flag word per chunk (see row_wait); a wait gives up after kIsSpinLimit polls and sets the
-// error word, so every wave exits.
+// epoch of a launch is one more than the one the chunk's count word holds from the previous launch.  A wait gives up
+// after kIsSpinLimit polls and sets the error word, so every wave exits.
 #include "score_core.h"
 #include "select_core.h"
 
@@ -35,6 +36,14 @@ constexpr int kIsMaxChunks = 512;              // chunks per row (rows up to 262
 constexpr int kIsMaxWG = 512;                  // resident workgroups: 2 per CU
 constexpr int kIsSpinLimit = 1 << 20;
 
+constexpr int kIsTagShift = 18;  // candidate low word: epoch tag (14 bits) << 18 | (~position & 0x3ffff)
+static_assert(kIsMaxChunks * kIsChunk <= (1 << kIsTagShift), "positions fit below the epoch tag");
+
+// Candidate value: order by key, then by lower position; every candidate of one launch carries the same tag.
+DSV41_DEV unsigned long long is_cand_value(uint32_t key, int p, uint32_t tag) {
+  return (unsigned long long)key << 32 | tag << kIsTagShift | (~(uint32_t)p & ((1u << kIsTagShift) - 1));
+}
+
 struct IsArgs {
   ScoreArgs s;                // prepared e4m3 queries, folded weights, e4m3 keys + scales, seq, cl, n_pos; out or null
   int k, offset;
@@ -42,28 +51,14 @@ struct IsArgs {
   long idx_rstride;
   int nslots;                 // chunks per row
   int* hist;                  // [R, kHistBins], zero between launches
-  unsigned long long* cnt;    // [R, nslots]: above | candidates << 32
+  unsigned long long* cnt;    // [R, nslots]: epoch << 32 | candidates << 16 | above
   unsigned long long* cand;   // [R, nslots * kIsChunk]
-  unsigned long long* flags;  // [R, nslots] barrier flags
   int* err;
 };
 
-// Row barrier on flag words: chunk ch of row r owns flag[r][ch], which only grows (2e after launch e - 1).  At
-// phase ph (1, 2) of launch e a workgroup stores 2e + ph into its flag and waits until every flag of the row is
-// >= 2e + ph: threads 0..nslots-1 read the row's flags each poll (one round trip, no same-address contention).
-DSV41_DEV void row_wait(const unsigned long long* flags, int ns, unsigned long long target, int* done, int* err) {
-  const int t = threadIdx.x;
-  int spins = 0;
-#pragma unroll 1
-  while (true) {
-    const bool ok = t >= ns || __hip_atomic_load(flags + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target;
-    const int all = __syncthreads_and(ok);
-    if (all || ++spins >= kIsSpinLimit) break;
-    __builtin_amdgcn_s_sleep(4);
-  }
-  if (t == 0 && spins >= kIsSpinLimit) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  (void)done;
-}
+#ifdef DSV41_TIMING
+__device__ int g_is_spins[1024][2];  // polls of the two waits per workgroup
+#endif
 
 // MAXC: the largest chunk count per row the instance handles (128: the candidate-prefix gather and the chunk
 // prefix scans fit 4 loads per thread and two waves; kIsMaxChunks: 16 loads per thread and a workgroup scan).
@@ -90,9 +85,10 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   DSV41_TS(48);
   const long clr = row_cl(a, r);
   const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
-  // this chunk's flag is 2e after launch e - 1 (earlier launches have completed): e is this launch's epoch
-  const unsigned long long e0 =
-      __hip_atomic_load(g.flags + (long)r * ns + ch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) / 2;
+  // this launch's epoch: one more than the one this chunk's count word holds (earlier launches have completed)
+  const uint32_t epoch =
+      (uint32_t)(__hip_atomic_load(g.cnt + (long)r * ns + ch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32) + 1;
+  const uint32_t tag = epoch & ((1u << (32 - kIsTagShift)) - 1);
   const int c = (int)(clr < 0 ? 0 : (clr > a.n_pos ? a.n_pos : clr)), k = g.k;
   if (clr > a.n_pos && ch == 0 && t == 0)  // positions beyond n_pos were promised never to be valid
     __hip_atomic_store(g.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -166,14 +162,15 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   DSV41_PH(1);
   DSV41_TS(54);
   int* gh = g.hist + (long)r * kHistBins;
-  unsigned long long* rflags = g.flags + (long)r * ns;
+  unsigned long long* rcnt = g.cnt + (long)r * ns;
   int* oidx = g.idx + (long)r * g.idx_rstride;
-  if (!sel) {  // everything is selected: arrive twice without waiting (keeps the row's arrival count)
+  if (!sel) {  // everything is selected: no exchange (every chunk of the row takes this branch); epoch advances
     if (ch == 0) {
 #pragma unroll 1
       for (int i = t; i < k; i += kIsThreads) oidx[i] = i < c ? i + g.offset : -1;
     }
-    if (t == 0) __hip_atomic_store(rflags + ch, 2 * e0 + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == 0)
+      __hip_atomic_store(rcnt + ch, (unsigned long long)epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
 #pragma unroll 1
@@ -181,33 +178,41 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     const int v = lhist[i];
     if (v) atomicAdd(&gh[i], v);
   }
-  // ---- B. row barrier 1, threshold bin
-  __builtin_amdgcn_s_waitcnt(0);
+  // ---- B. the row histogram once it holds all c valid positions (row barrier and data in one read), threshold bin
   DSV41_PH(2);
-  __syncthreads();
   if (t == 0) {
-    __hip_atomic_store(rflags + ch, 2 * e0 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_bin = 0;  // (a histogram holding fewer than k entries is a caller error)
     s_need = k;
     s_cnt = 0;
   }
-  row_wait(rflags, ns, 2 * e0 + 1, nullptr, g.err);
-  DSV41_PH(3);
   {
     constexpr int BP = kHistBins / kIsThreads;  // bins per thread: 4095 - BP*t (h[0]) down to 4096 - BP*(t+1)
     int h[BP];
+    int local, total, above, spins = 0;
+#pragma unroll 1
+    while (true) {
 #pragma unroll
-    for (int u = 0; u < BP / 2; ++u) {
-      const unsigned long long v = __hip_atomic_load(
-          (unsigned long long*)(gh + kHistBins - BP * (t + 1) + 2 * u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      h[BP - 1 - 2 * u] = (int)(v & 0xffffffffu);
-      h[BP - 2 - 2 * u] = (int)(v >> 32);
+      for (int u = 0; u < BP / 2; ++u) {
+        const unsigned long long v = __hip_atomic_load(
+            (unsigned long long*)(gh + kHistBins - BP * (t + 1) + 2 * u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        h[BP - 1 - 2 * u] = (int)(v & 0xffffffffu);
+        h[BP - 2 - 2 * u] = (int)(v >> 32);
+      }
+      local = 0;
+#pragma unroll
+      for (int i = 0; i < BP; ++i) local += h[i];
+      above = block_scan_dpp<kIsThreads>(local, tmp, &total);  // (total is uniform over the workgroup)
+      if (total == c) break;
+      if (++spins >= kIsSpinLimit) {
+        if (t == 0) __hip_atomic_store(g.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
     }
-    int local = 0;
-#pragma unroll
-    for (int i = 0; i < BP; ++i) local += h[i];
-    int total;
-    int above = block_scan_dpp<kIsThreads>(local, tmp, &total);
+    DSV41_PH(3);
+#ifdef DSV41_TIMING
+    if (t == 0 && blockIdx.x < 1024) g_is_spins[blockIdx.x][0] = spins;
+#endif
     if (above < k && k <= above + local) {
 #pragma unroll 1
       for (int i = 0; i < BP; ++i) {
@@ -250,43 +255,65 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
 #pragma unroll
     for (int e = 0; e < kIsPer; ++e)
       if (p0 + e < c && key[e] >= lo && key[e] < hi)
-        __hip_atomic_store(crow + o++, (unsigned long long)key[e] << 32 | (uint32_t)~(uint32_t)(p0 + e),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(crow + o++, is_cand_value(key[e], p0 + e, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  // the counts go out after this workgroup's candidates have landed: a reader that sees this epoch in the count word
+  // finds the candidates in place
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
   if (t == 0) {
     unsigned ta = 0, tc = 0;
 #pragma unroll
     for (int w = 0; w < 8; ++w) ta += wcnt[w][0], tc += wcnt[w][1];
-    __hip_atomic_store(g.cnt + (long)r * ns + ch, (unsigned long long)ta | (unsigned long long)tc << 32,
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(rcnt + ch, (unsigned long long)epoch << 32 | tc << 16 | ta, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   }
-  // ---- D. row barrier 2; the histogram has been read by every chunk
-  __builtin_amdgcn_s_waitcnt(0);
+  // ---- D. counts of all chunks + speculative candidate prefixes, read until every count word carries this epoch
+  // and every speculative candidate below its chunk's count carries this epoch's tag (row barrier and gather in one)
   DSV41_PH(4);
-  __syncthreads();
-  if (t == 0) __hip_atomic_store(rflags + ch, 2 * e0 + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  row_wait(rflags, ns, 2 * e0 + 2, nullptr, g.err);
-  DSV41_PH(5);
+  constexpr int kSpecPer = MAXC * kIsSpec / kIsThreads;
+  unsigned long long sv[kSpecPer];
   {
+    int spins = 0;
+#pragma unroll 1
+    while (true) {
+      unsigned long long cv = 0ull;
+      if (t < ns) cv = __hip_atomic_load(rcnt + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int u = 0; u < kSpecPer; ++u) {
+        const int id = u * kIsThreads + t, q = id / kIsSpec, e = id % kIsSpec;
+        sv[u] = q < ns ? __hip_atomic_load(crow + q * kIsChunk + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+      }
+      if (t < ns) {
+        na_q[t] = (int)(cv & 0xffffu);
+        nc_q[t] = (int)((cv >> 16) & 0xffffu);
+      }
+      bool ok = t >= ns || (uint32_t)(cv >> 32) == epoch;
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < kSpecPer; ++u) {
+        const int id = u * kIsThreads + t, q = id / kIsSpec, e = id % kIsSpec;
+        if (q < ns && e < nc_q[q]) ok = ok && (uint32_t)(sv[u] >> kIsTagShift & ((1u << (32 - kIsTagShift)) - 1)) == tag;
+      }
+      if (__syncthreads_and(ok)) {
+#ifdef DSV41_TIMING
+        if (t == 0 && blockIdx.x < 1024) g_is_spins[blockIdx.x][1] = spins;
+#endif
+        break;
+      }
+      if (++spins >= kIsSpinLimit) {
+        if (t == 0) __hip_atomic_store(g.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  DSV41_PH(5);
+  {  // every chunk has read the histogram (its count word is out): clear this chunk's slice for the next launch
     const int zb = (kHistBins + ns - 1) / ns, z0 = ch * zb, z1 = min(kHistBins, z0 + zb);
 #pragma unroll 1
     for (int i = z0 + t; i < z1; i += kIsThreads) gh[i] = 0;
   }
-  // ---- E. counts of all chunks + speculative candidate prefixes
-  if (t < ns) {
-    const unsigned long long cv = __hip_atomic_load(g.cnt + (long)r * ns + t, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-    na_q[t] = (int)(cv & 0xffffffffu);
-    nc_q[t] = (int)(cv >> 32);
-  }
-  constexpr int kSpecPer = MAXC * kIsSpec / kIsThreads;
-  unsigned long long sv[kSpecPer];
-#pragma unroll
-  for (int u = 0; u < kSpecPer; ++u) {
-    const int id = u * kIsThreads + t, q = id / kIsSpec, e = id % kIsSpec;
-    sv[u] = q < ns ? __hip_atomic_load(crow + q * kIsChunk + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
-  }
-  __syncthreads();
   if constexpr (MAXC <= 128) {
     if (wave < 2) {  // prefix of the candidate counts (2 x 64 chunks); entries above B in earlier chunks
       const int q = wave * 64 + lane;
@@ -358,7 +385,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   for (int e = 0; e < kIsPer; ++e) {
     const bool ok = p0 + e < c;
     take[e] = ok && (key[e] >= hi ||
-                     (key[e] >= lo && ((unsigned long long)key[e] << 32 | (uint32_t)~(uint32_t)(p0 + e)) >= T));
+                     (key[e] >= lo && is_cand_value(key[e], p0 + e, tag) >= T));
     nt += take[e];
   }
   int o = base + block_scan_dpp<kIsThreads>(nt, tmp, &tot);
@@ -375,6 +402,7 @@ int is_slots(int n_pos) { return (n_pos + kIsChunk - 1) / kIsChunk; }
 extern "C" {
 
 #ifdef DSV41_TIMING
+int dsv41_read_spins_is(int* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_is_spins), sizeof(g_is_spins)); }
 int dsv41_read_ph_is(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ph), sizeof(g_dsv41_ph)); }
 int dsv41_read_ts_is(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
 #endif
@@ -425,8 +453,7 @@ int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_r
   g.hist = (int*)w;
   g.cnt = (unsigned long long*)(w + (long)R * kHistBins * 4);
   g.cand = g.cnt + (long)R * ns;
-  g.flags = g.cand + (long)R * ns * kIsChunk;
-  g.err = (int*)(g.flags + (long)R * ns);
+  g.err = (int*)(g.cand + (long)R * ns * kIsChunk + (long)R * ns);  // (after a spare [R, nslots] u64 region)
   if (ns <= 128)
     index_select_kernel<128><<<R * ns, kIsThreads, 0, (hipStream_t)stream>>>(g);
   else

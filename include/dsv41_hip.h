@@ -21,7 +21,10 @@ extern "C" {
 /* ------------------------------------------------------------------------------------------------ attention */
 
 /* Workspace bytes for R query rows x H heads over L key positions with output width dv (0 when one split covers
- * a row).  want_nsplit <= 0 lets the library choose the split count; pass the same value to the launch. */
+ * a row).  want_nsplit <= 0 lets the library choose the split count; pass the same value to the launch.  The
+ * workspace opens with split arrival counters (placed by R and H only): allocate it zeroed once per (R, H); every
+ * launch leaves the counters ready for the next, whatever its split count (launches sharing it must be
+ * stream-ordered). */
 long dsv41_attn_workspace_bytes(int R, int H, int L, int dv, int want_nsplit);
 
 /* kernels.sparse_attn (dsv41/kernels.py:172-256) and fused.sparse_attn_decode (dsv41/fused.py:269-280).
@@ -106,8 +109,9 @@ long dsv41_select_workspace_bytes(int R, int n);
 int dsv41_select_topk(const float* score, long ld, int R, int n, int k, const long* cl, int offset, void* ws,
                       long ws_bytes, int* out, long out_rstride, void* stream);
 
-/* Workspace of dsv41_index_select for R rows of n_pos positions.  Allocate it zeroed once: every call leaves its
- * histogram zeroed and its arrival counters consistent for the next call (calls sharing it must be stream-ordered). */
+/* Workspace of dsv41_index_select for R rows of n_pos positions.  Allocate it zeroed once per (R, n_pos): every
+ * call leaves its histogram zeroed and its per-chunk count words (which carry the launch epoch) consistent for the
+ * next call (calls sharing it must be stream-ordered). */
 long dsv41_index_select_workspace_bytes(int R, int n_pos);
 
 /* The decode indexer in one launch: fused3.index_score followed by fused3.topk_indices (dsv41/decode.py:284-294;

@@ -260,8 +260,8 @@ def test_sattn2_reference_geometry(p):
 @pytest.mark.parametrize("H", [64, 40])
 def test_sattn2_absorbed_mla_ragged_with_drafts(H):
     """576/512 absorbed MLA, k = 2048, 4 slots at ragged positions, plus 6 draft rows of one sequence with plim
-    causal masking (the MTP verify shape, dsv41/fused2.py:351-360), at 64 and 40 heads.  Two calls share one
-    workspace (its split counters must be left ready)."""
+    causal masking (the MTP verify shape, dsv41/fused2.py:351-360), at 64 and 40 heads.  Calls with different split
+    counts share one workspace (its split counters must be left ready whatever the previous call's split count)."""
     import dsv41_amd
     from dsv41_amd._lib import lib
     r = rng(9)
@@ -281,12 +281,13 @@ def test_sattn2_absorbed_mla_ragged_with_drafts(H):
         idx[b, 0, :nv] = np.sort(r.choice(cl, nv, replace=False))
     cos = np.zeros((1, 1), np.float32)
     want = O.sattn2(q, ring, ckv, idx, pos, seq, pmax, pos, sink, cos, cos, 0, dqk ** -0.5, dv=dv)
-    nbytes = lib().dsv41_attn_workspace_bytes(10, H, win + k, dv, 0)
+    splits = [0, 0, 3, 5, 2, 0]
+    nbytes = max(lib().dsv41_attn_workspace_bytes(10, H, win + k, dv, n) for n in splits)
     ws = torch.zeros(max(nbytes, 4) // 4, dtype=torch.float32, device=DEV)
-    for call_no in range(2):
+    for call_no, ns in enumerate(splits):
         o = dsv41_amd.sattn2(bf(q), bf(ring), bf(ckv), torch.from_numpy(idx).to(DEV), i64(pos), f32(sink), f32(cos),
-                             f32(cos), 0, dqk ** -0.5, i64(seq), i64(pmax), plim=i64(pos), d_v=dv, ws=ws)
-        attn_close(host(o), want, f"sattn2 mla ragged+drafts H={H} call {call_no}")
+                             f32(cos), 0, dqk ** -0.5, i64(seq), i64(pmax), plim=i64(pos), d_v=dv, nsplit=ns, ws=ws)
+        attn_close(host(o), want, f"sattn2 mla ragged+drafts H={H} call {call_no} nsplit {ns}")
 
 
 # ------------------------------------------------------------------------------------------------ indexer
