@@ -31,10 +31,13 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def decode_bytes(cfg, idx_sets=None):
+def decode_bytes(cfg, idx_sets=None, fused=True):
     """Algorithmic HBM bytes per launch of the decode kernels.  indexer: per slot the valid index keys (128 B + 4 B
-    scale each), per query row the prepared e4m3 query and weights and the k indices written.  sattn: per slot the
-    union of the selected compressed rows and the ring rows (576 x bf16 each), per query row q, output and indices."""
+    scale each), per query row the index query and weights and the k indices written; fused (the step's cache
+    appends in the same launch): the bf16 index query and weights, and per row the appends' inputs and outputs
+    (pre-norm KV row and ring row, latent and compressed row (576 x bf16 each), raw index key (bf16), e4m3 key and
+    scale).  sattn: per slot the union of the selected compressed rows and the ring rows (576 x bf16 each), per query
+    row q, output and indices."""
     from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN
     per_kernel = {"indexer": 0, "sattn": 0}
     R = cfg.slots * cfg.rows_per_slot
@@ -43,7 +46,10 @@ def decode_bytes(cfg, idx_sets=None):
         per_kernel["indexer"] += n * (DI + 4)
         sel = min(cfg.topk, n) if idx_sets is None else idx_sets[s]
         per_kernel["sattn"] += (sel + WIN) * DQK * 2
-    per_kernel["indexer"] += R * (64 * DI + 64 * 4 + cfg.topk * 4)
+    if fused:
+        per_kernel["indexer"] += R * (HI * DI * 2 + HI * 2 + cfg.topk * 4 + 4 * DQK * 2 + DI * 2 + DI + 4)
+    else:
+        per_kernel["indexer"] += R * (64 * DI + 64 * 4 + cfg.topk * 4)
     per_kernel["sattn"] += R * (H * DQK * 2 + H * DV * 2 + cfg.topk * 4)
     return per_kernel
 
@@ -82,10 +88,18 @@ def run_decode(args, dev):
     pos, seq, pmax = st["pos"], st["seq"], st["pmax"]
     cl = torch.div(pos + 1, cfg.ratio, rounding_mode="floor")  # once per token, shared by every layer
 
-    def layer_step(lay):
+    fused = not args.separate_appends and cfg.rows_per_slot == 1  # (the one-launch appends need one row per slot)
+
+    def appends_select(lay):
+        if fused:
+            return lay.appends_select(st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos, seq,
+                                      st["q_idx"], st["w_idx"], cl)
         lay.appends(st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos, seq, st["q_idx"],
                     st["w_idx"])
-        idx = lay.select(st["q_idx"], st["w_idx"], pos, seq, cl)
+        return lay.select(st["q_idx"], st["w_idx"], pos, seq, cl)
+
+    def layer_step(lay):
+        idx = appends_select(lay)
         return lay.attend(st["q"], idx, pos, seq, pmax, plim=pos)
 
     stream = torch.cuda.current_stream(dev)
@@ -94,23 +108,27 @@ def run_decode(args, dev):
             layer_step(lay)
     torch.cuda.synchronize(dev)
 
-    # ---- per-phase durations (eager, events around each launch on the launch stream): appends (1 kernel), indexer
-    # (scores + top-k: one launch), sattn (attention, splits merged in-kernel)
+    # ---- per-phase durations (eager, events around each launch on the launch stream): indexer (the step's cache
+    # appends + scores + top-k: one launch; with --separate-appends the appends launch is timed apart), sattn
+    # (attention, splits merged in-kernel)
     E = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    phases = {"appends": [], "indexer": [], "sattn": []}
+    phases = {"indexer": [], "sattn": []} if fused else {"appends": [], "indexer": [], "sattn": []}
     reps = max(2, min(args.steps, 20))
     sel_union = None
     for rep in range(reps):
         for lay in L:
-            ev = [E() for _ in range(4)]
+            ev = [E() for _ in range(len(phases) + 1)]
             ev[0].record(stream)
-            lay.appends(st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos, seq, st["q_idx"],
-                        st["w_idx"])
-            ev[1].record(stream)
-            idx = lay.select(st["q_idx"], st["w_idx"], pos, seq, cl)
-            ev[2].record(stream)
+            if fused:
+                idx = appends_select(lay)
+            else:
+                lay.appends(st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos, seq,
+                            st["q_idx"], st["w_idx"])
+                ev[1].record(stream)
+                idx = lay.select(st["q_idx"], st["w_idx"], pos, seq, cl)
+            ev[-2].record(stream)
             lay.attend(st["q"], idx, pos, seq, pmax, plim=pos)
-            ev[3].record(stream)
+            ev[-1].record(stream)
             torch.cuda.synchronize(dev)
             for i, k in enumerate(phases):
                 phases[k].append(ev[i].elapsed_time(ev[i + 1]) * 1000.0)
@@ -150,9 +168,10 @@ def run_decode(args, dev):
 
     # ---- each heavy kernel alone: a graph of NL launches of it (one per cache copy), replayed; the average launch
     # duration (events on the launch stream around the replays) is the roofline denominator
-    idxs = [lay.select(st["q_idx"], st["w_idx"], pos, seq, cl) for lay in L]
+    idxs = [appends_select(lay).clone() for lay in L]
     torch.cuda.synchronize(dev)
-    only = {"indexer": lambda lay, i: lay.select(st["q_idx"], st["w_idx"], pos, seq, cl),
+    only = {"indexer": lambda lay, i: appends_select(lay) if fused else lay.select(st["q_idx"], st["w_idx"], pos,
+                                                                                 seq, cl),
             "sattn": lambda lay, i: lay.attend(st["q"], idxs[i], pos, seq, pmax, plim=pos)}
     alone_us = {}
     for name, fn in only.items():
@@ -175,9 +194,9 @@ def run_decode(args, dev):
         alone_us[name] = e2.elapsed_time(e3) * 1000.0 / (replays * NL)
         log(f"[bench] {name} kernel alone: {alone_us[name]:.2f} us/launch")
     log(f"[bench] eager per-kernel medians (us): {kern_us}")
-    kb = decode_bytes(cfg, sel_union)
+    kb = decode_bytes(cfg, sel_union, fused)
     return dict(cfg=cfg, step_us=step_us, kern_us=kern_us, kern_bytes=kb, steps=replays * NL, sel_union=sel_union,
-                alone_us=alone_us)
+                alone_us=alone_us, fused=fused)
 
 
 def run_prefill(args, dev):
@@ -307,6 +326,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--separate-appends", action="store_true",
+                    help="decode: the cache appends as their own launch before the indexer (default: one launch)")
     ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--calib-copy", action="store_true", help="one 64 MiB device copy (rocprof counter calibration)")
     ap.add_argument("--prefill-only", action="store_true",
@@ -332,7 +353,8 @@ def main():
     r = run_decode(args, dev)
     cfg = r["cfg"]
     kb, ku = r["kern_bytes"], r["kern_us"]
-    kernel_names = {"indexer": "index_select_kernel (scores + top-k, one launch)",
+    kernel_names = {"indexer": "index_select_kernel<128, true> (cache appends + scores + top-k, one launch)"
+                    if r["fused"] else "index_select_kernel (scores + top-k, one launch)",
                     "sattn": "attn_decode_kernel<576, 512> (splits merged in-kernel)"}
     roof = {}
     for name, us in r["alone_us"].items():

@@ -21,6 +21,7 @@
 // operations, which the hardware keeps coherent across the XCDs' L2 caches, so no cache maintenance is needed.  The
 // epoch of a launch is one more than the one the chunk's count word holds from the previous launch.  A wait gives up
 // after kIsSpinLimit polls and sets the error word, so every wave exits.
+#include "rowop.h"
 #include "score_core.h"
 #include "select_core.h"
 
@@ -44,6 +45,37 @@ DSV41_DEV unsigned long long is_cand_value(uint32_t key, int p, uint32_t tag) {
   return (unsigned long long)key << 32 | tag << kIsTagShift | (~(uint32_t)p & ((1u << kIsTagShift) - 1));
 }
 
+// The decode step's cache appends done inside the launch (dsv41_decode_select; the operations of
+// dsv41_decode_appends): the SWA ring row, the compressed row and the index key of every row, and the e4m3
+// preparation of the index queries.
+struct IsAppend {
+  const uint16_t* kv_raw;  // [R, Dw] pre-norm KV rows, rmsnorm weight kv_norm
+  const uint16_t* kv_norm;
+  uint16_t* ring;          // [S, W, Dw]
+  long ring_sstride;
+  int W, Dw;
+  const uint16_t* latent;  // [R, Dw] pooled latents (may be null: no compressed append)
+  uint16_t* ckv;           // [S, cap, Dw]
+  long ckv_sstride;
+  int cap;
+  const uint16_t* k_raw;   // [R, 128] index-key rows, rmsnorm weight k_norm
+  const uint16_t* k_norm;
+  uint16_t* kbf;           // optional bf16 key table [S, kcap, 128]
+  long kbf_sstride;
+  uint8_t* k8;             // e4m3 key table [S, kcap, 128] + scales (the keys this launch scores)
+  long k8_sstride;
+  float* ks;
+  long ks_sstride;
+  int kcap;
+  const long* pos;
+  int ratio, rd;
+  const float* cos_t;
+  const float* sin_t;
+  float eps;
+  const uint16_t* q_idx;   // [R, HI, 128] bf16 index queries, w_idx [R, HI] bf16 head weights
+  const uint16_t* w_idx;
+};
+
 struct IsArgs {
   ScoreArgs s;                // prepared e4m3 queries, folded weights, e4m3 keys + scales, seq, cl, n_pos; out or null
   int k, offset;
@@ -54,6 +86,7 @@ struct IsArgs {
   unsigned long long* cnt;    // [R, nslots]: epoch << 32 | candidates << 16 | above
   unsigned long long* cand;   // [R, nslots * kIsChunk]
   int* err;
+  IsAppend app;               // FUSED instances only
 };
 
 #ifdef DSV41_TIMING
@@ -62,12 +95,14 @@ __device__ int g_is_spins[1024][2];  // polls of the two waits per workgroup
 
 // MAXC: the largest chunk count per row the instance handles (128: the candidate-prefix gather and the chunk
 // prefix scans fit 4 loads per thread and two waves; kIsMaxChunks: 16 loads per thread and a workgroup scan).
-template <int MAXC>
+template <int MAXC, bool FUSED>
 __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArgs g) {
   static_assert(MAXC <= kIsThreads && MAXC % 64 == 0, "one thread per chunk");
   const ScoreArgs& a = g.s;
   const int R = a.R, ns = g.nslots;
-  const int r = blockIdx.x % R, ch = blockIdx.x / R;
+  const bool extra = FUSED && (int)blockIdx.x >= R * ns;  // (FUSED) an append-only workgroup after the row grid
+  const int bx = extra ? (int)blockIdx.x - R * ns : (int)blockIdx.x;
+  const int r = extra ? bx / 3 : bx % R, ch = extra ? 0 : bx / R;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
   __shared__ int lhist[kHistBins];
@@ -79,6 +114,9 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   __shared__ __align__(16) unsigned long long lc[kIsCand + 2];
   __shared__ RankScratch rs;
   __shared__ __align__(16) uint8_t qs[64 * 128];  // the row's prepared e4m3 queries, staged once
+  __shared__ float wfl[FUSED ? 64 : 1];            // (FUSED) the prepared head weights
+  __shared__ __align__(16) uint8_t knew[FUSED ? 128 : 16];  // (FUSED) the new index key, e4m3, and its scale
+  __shared__ float ksnew, redf[kIsThreads / 64];
 
   // ---- A. row data (independent loads), scores, histogram
   DSV41_PH(0);
@@ -93,18 +131,81 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   if (clr > a.n_pos && ch == 0 && t == 0)  // positions beyond n_pos were promised never to be valid
     __hip_atomic_store(g.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int nht = (a.HI + 15) / 16;
-  // the row's queries (64 heads x 128 e4m3 = 512 chunks of 16 bytes) go to LDS once, one direct load per thread
-  // (every wave needs all of them); heads >= HI are never read back
-  if (t < a.HI * 8) lds_dma16((const uint16_t*)((const uint8_t*)a.q + (long)r * a.q_rstride) + t * 8,
-                              (uint16_t*)qs + wave * 64 * 8);
   i32x8_t qa8[kHT];
   uint4 qa16[kHT][4];  // (bf16 queries: unused here)
   float wl[kHT];
+  // FUSED: the ring row, the compressed row and a spare-row index key are written by 3 append-only workgroups per
+  // row after the row grid (they take no part in the row barriers); the new index key of a row whose group closes
+  // by the chunk holding its position, its operands and the raw index queries loaded ahead of the keys
+  const IsAppend& ap = g.app;
+  long ppos = 0, knew_row = -1;
+  int opmask = 0;
+  Qprep512 qp;
+  RowRegs<kIsThreads> rg;
+  auto make_op = [&](int which) {
+    RowOp o{};
+    o.cos_t = ap.cos_t;
+    o.sin_t = ap.sin_t;
+    o.rd = ap.rd;
+    o.eps = ap.eps;
+    const bool closes = ((ppos + 1) % ap.ratio) == 0;
+    if (which == 0) {
+      o.x = ap.kv_raw + (long)r * ap.Dw;
+      o.D = ap.Dw;
+      o.norm_w = ap.kv_norm;
+      o.pos = ppos < 0 ? 0 : ppos;
+      o.qmode = 0;
+      o.group = 32;
+      o.out = ap.ring + slot * ap.ring_sstride + (o.pos % ap.W) * (long)ap.Dw;
+    } else if (which == 1) {
+      const long row = closes ? (ppos + 1) / ap.ratio - 1 : ap.cap - 1;
+      o.x = ap.latent + (long)r * ap.Dw;
+      o.D = ap.Dw;
+      o.pos = ppos + 1 - ap.ratio;
+      o.qmode = 2;
+      o.group = 16;
+      o.out = ap.ckv + slot * ap.ckv_sstride + row * (long)ap.Dw;
+    } else {
+      const long row = closes ? (ppos + 1) / ap.ratio - 1 : ap.kcap - 1;
+      o.x = ap.k_raw + (long)r * 128;
+      o.D = 128;
+      o.norm_w = ap.k_norm;
+      o.pos = ppos + 1 - ap.ratio;
+      o.qmode = 1;
+      o.group = 32;
+      o.out = ap.kbf ? ap.kbf + slot * ap.kbf_sstride + row * 128L : nullptr;
+      o.k8 = ap.k8 + slot * ap.k8_sstride + row * 128L;
+      o.ks = ap.ks + slot * ap.ks_sstride + row;
+      o.k8_lds = knew;
+      o.ks_lds = &ksnew;
+    }
+    return o;
+  };
+  if constexpr (FUSED) {
+    ppos = ap.pos[r];
+    const bool closes = ((ppos + 1) % ap.ratio) == 0;
+    if (extra) {  // the ring row, the compressed row, or (no group closes) the index key's spare row; then done
+      const int which = bx % 3;
+      if ((which == 1 && !(ap.latent && ap.ckv)) || (which == 2 && closes)) return;
+      row_op<kIsThreads>(make_op(which), redf);
+      return;
+    }
+    // the chunk holding the new key's position computes it (and scores it from the computed values)
+    if (closes) knew_row = (ppos + 1) / ap.ratio - 1;
+    opmask = closes && ch == (int)(knew_row / kIsChunk) ? 4 : 0;
+    if (opmask) row_load<kIsThreads>(make_op(__builtin_ctz(opmask)), rg);
+    qprep512_load(ap.q_idx + (long)r * a.HI * 128, ap.w_idx + (long)r * a.HI, a.HI, qp);
+  } else {
+    // the row's queries (64 heads x 128 e4m3 = 512 chunks of 16 bytes) go to LDS once, one direct load per thread
+    // (every wave needs all of them); heads >= HI are never read back
+    if (t < a.HI * 8) lds_dma16((const uint16_t*)((const uint8_t*)a.q + (long)r * a.q_rstride) + t * 8,
+                                (uint16_t*)qs + wave * 64 * 8);
 #pragma unroll
-  for (int ht = 0; ht < kHT; ++ht) {
-    const int h = ht * 16 + l16;
-    const bool hv = ht < nht && h < a.HI;
-    wl[ht] = hv ? a.w[(long)r * a.w_rstride + h] : 0.0f;
+    for (int ht = 0; ht < kHT; ++ht) {
+      const int h = ht * 16 + l16;
+      const bool hv = ht < nht && h < a.HI;
+      wl[ht] = hv ? a.w[(long)r * a.w_rstride + h] : 0.0f;
+    }
   }
 #ifdef DSV41_TIMING
   __builtin_amdgcn_s_waitcnt(0);
@@ -130,6 +231,34 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   __builtin_amdgcn_s_waitcnt(0);
   DSV41_TS(51);
 #endif
+  if constexpr (FUSED) {
+    if (opmask) {  // (the operands were loaded ahead of the keys)
+      const int first = __builtin_ctz(opmask);
+      row_compute<kIsThreads, true>(make_op(first), rg, redf);  // (LDS-only barriers: the keys stay in flight)
+#pragma unroll 1
+      for (int which = first + 1; which < 3; ++which)
+        if (opmask >> which & 1) row_op<kIsThreads>(make_op(which), redf);
+    }
+    qprep512_store(qp, a.HI, qs, wfl);
+    lds_barrier();  // queries, weights and the new key staged
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht) {
+      const int h = ht * 16 + l16;
+      wl[ht] = ht < nht && h < a.HI ? wfl[h] : 0.0f;
+    }
+    // the new key's position is scored with the key computed here (its row in the table was read before it was
+    // written)
+    if (knew_row >= pw && knew_row < pw + kIsKeysPerWave && (opmask & 4)) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        if (pw + nt * 16 + l16 == knew_row) {
+          k0[nt] = *(const uint4*)(knew + g4 * 32);
+          k1[nt] = *(const uint4*)(knew + g4 * 32 + 16);
+          ksc[nt] = ksnew;
+        }
+      }
+    }
+  }
   float wr[kHT][4];  // weights of the heads this lane's accumulators hold: ht*16 + 4g + i
 #pragma unroll
   for (int ht = 0; ht < kHT; ++ht)
@@ -412,17 +541,19 @@ long dsv41_index_select_workspace_bytes(int R, int n_pos) {
   return (long)R * kHistBins * 4 + (long)R * ns * 8 + (long)R * ns * kIsChunk * 8 + (long)R * ns * 8 + 16;
 }
 
-int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_rstride, int R, int HI,
-                       const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
-                       const long* cl, int n_pos, int k, int offset, void* ws, long ws_bytes, float* score_out,
-                       long score_rstride, int* out, long out_rstride, const void* cand, long cand_rstride,
-                       void* stream) {
-  if (R <= 0 || k <= 0) return 0;
+}  // extern "C"
+
+namespace {
+
+// Shared set-up of dsv41_index_select / dsv41_decode_select (q8 / wf: prepared queries, or null when FUSED).
+int select_setup(IsArgs& g, const void* q8, long q_rstride, const float* wf, long w_rstride, int R, int HI,
+                 const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
+                 const long* cl, int n_pos, int k, int offset, void* ws, long ws_bytes, float* score_out,
+                 long score_rstride, int* out, long out_rstride, const void* cand, long cand_rstride) {
   const int ns = is_slots(n_pos);
   if (n_pos <= 0 || HI <= 0 || HI > 64 || !cl || !kscale || ns > kIsMaxChunks || (long)R * ns > kIsMaxWG)
     return (int)hipErrorInvalidValue;
   if (!ws || ws_bytes < dsv41_index_select_workspace_bytes(R, n_pos)) return (int)hipErrorInvalidValue;
-  IsArgs g{};
   ScoreArgs& a = g.s;
   a.q = (const uint16_t*)q8;
   a.q_rstride = q_rstride;
@@ -454,12 +585,59 @@ int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_r
   g.cnt = (unsigned long long*)(w + (long)R * kHistBins * 4);
   g.cand = g.cnt + (long)R * ns;
   g.err = (int*)(g.cand + (long)R * ns * kIsChunk + (long)R * ns);  // (after a spare [R, nslots] u64 region)
-  if (ns <= 128)
-    index_select_kernel<128><<<R * ns, kIsThreads, 0, (hipStream_t)stream>>>(g);
+  return 0;
+}
+
+template <bool FUSED>
+int select_launch(const IsArgs& g, hipStream_t st) {
+  const int grid = g.s.R * g.nslots + (FUSED ? 3 * g.s.R : 0);  // (FUSED: the append-only workgroups last)
+  if (g.nslots <= 128)
+    index_select_kernel<128, FUSED><<<grid, kIsThreads, 0, st>>>(g);
   else
-    index_select_kernel<kIsMaxChunks><<<R * ns, kIsThreads, 0, (hipStream_t)stream>>>(g);
+    index_select_kernel<kIsMaxChunks, FUSED><<<grid, kIsThreads, 0, st>>>(g);
   DSV41_CHECK_LAUNCH();
   return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_rstride, int R, int HI,
+                       const void* keys, long k_sstride, const float* kscale, long ks_sstride, const long* seq,
+                       const long* cl, int n_pos, int k, int offset, void* ws, long ws_bytes, float* score_out,
+                       long score_rstride, int* out, long out_rstride, const void* cand, long cand_rstride,
+                       void* stream) {
+  if (R <= 0 || k <= 0) return 0;
+  IsArgs g{};
+  const int e = select_setup(g, q8, q_rstride, wf, w_rstride, R, HI, keys, k_sstride, kscale, ks_sstride, seq, cl,
+                             n_pos, k, offset, ws, ws_bytes, score_out, score_rstride, out, out_rstride, cand,
+                             cand_rstride);
+  return e ? e : select_launch<false>(g, (hipStream_t)stream);
+}
+
+int dsv41_decode_select(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
+                        const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
+                        const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
+                        long ks_sstride, int kcap, const long* pos, const long* seq, int R, int ratio,
+                        const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
+                        const void* w_idx, int HI, const long* cl, int n_pos, int k, int offset, void* ws,
+                        long ws_bytes, float* score_out, long score_rstride, int* out, long out_rstride,
+                        const void* cand, long cand_rstride, void* stream) {
+  if (R <= 0 || k <= 0) return 0;
+  if (!row_ok(Dw, 32) || ratio <= 0 || rd < 0 || rd % 2 != 0 || rd > Dw || rd > 128 || W <= 0 || !kv_raw ||
+      !kv_norm || !ring || !k_raw || !k_norm || !k8 || !ks || !pos || !seq || !q_idx || !w_idx || kcap <= 0 ||
+      (latent && (!ckv || cap <= 0)) || (rd > 0 && (!cos_t || !sin_t)))
+    return (int)hipErrorInvalidValue;
+  IsArgs g{};
+  const int e = select_setup(g, nullptr, 0, nullptr, 0, R, HI, k8, k8_sstride, ks, ks_sstride, seq, cl, n_pos, k,
+                             offset, ws, ws_bytes, score_out, score_rstride, out, out_rstride, cand, cand_rstride);
+  if (e) return e;
+  g.app = IsAppend{(const uint16_t*)kv_raw, (const uint16_t*)kv_norm, (uint16_t*)ring, ring_sstride, W, Dw,
+                   (const uint16_t*)latent, (uint16_t*)ckv, ckv_sstride, cap, (const uint16_t*)k_raw,
+                   (const uint16_t*)k_norm, (uint16_t*)kbf, kbf_sstride, (uint8_t*)k8, k8_sstride, ks, ks_sstride,
+                   kcap, pos, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx};
+  return select_launch<true>(g, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -131,6 +131,22 @@ int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_r
                        long score_rstride, int* out, long out_rstride, const void* cand, long cand_rstride,
                        void* stream);
 
+/* The decode step's cache appends and the one-launch indexer in one launch: the operations of dsv41_decode_appends
+ * (the SWA ring row, the compressed row and the index-key row of every row, dsv41/decode.py:129-164, :270-282; the
+ * e4m3 preparation of the index queries q_idx [R, HI, 128] / w_idx [R, HI] bf16) followed by dsv41_index_select over
+ * the e4m3 key table k8 / ks, the new key of a row whose step closes a group included (it is scored from the
+ * values this launch computes).  Same results as dsv41_decode_appends followed by dsv41_index_select.  Every row
+ * must belong to a different sequence (seq distinct: a row's new key is not visible to other rows of the launch);
+ * the index-key width is 128; limits and workspace as dsv41_index_select. */
+int dsv41_decode_select(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
+                        const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
+                        const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
+                        long ks_sstride, int kcap, const long* pos, const long* seq, int R, int ratio,
+                        const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
+                        const void* w_idx, int HI, const long* cl, int n_pos, int k, int offset, void* ws,
+                        long ws_bytes, float* score_out, long score_rstride, int* out, long out_rstride,
+                        const void* cand, long cand_rstride, void* stream);
+
 /* Workspace of dsv41_candidate_blocks (block maxima and the selected blocks of every row). */
 long dsv41_candidate_blocks_workspace_bytes(int R, int n, int topk_blocks, int block_size);
 

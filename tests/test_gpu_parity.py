@@ -660,3 +660,47 @@ def test_compress_pool_chunks(ratio):
         np.testing.assert_array_equal(host(rk_t), rk)
         np.testing.assert_array_equal(host(rs_t), rs)
         start += s
+
+
+def test_decode_appends_select_one_launch():
+    """dsv41_decode_select (the decode step's cache appends and the one-launch indexer in one launch) == the
+    appends launch followed by the indexer launch (dsv41/decode.py:129-164, :270-294): the same top-k indices and
+    index keys / compressed rows / scales bit for bit, the ring rows up to rare one-step fp8 flips (the rmsnorm sum
+    is reduced in another order), over steps that close a compression group (the new key is scored) and steps that
+    do not (spare row), with a candidate mask on one step."""
+    from dsv41_amd.decode import DecodeLayer
+    from dsv41_amd.workloads import DecodeConfig, make_decode_inputs
+    cfg = DecodeConfig("T", [65536, 8192, 40000, 12], topk=2048)
+    layers, st = make_decode_inputs(cfg, DEV, seed=3)
+    rd = 64
+    ang = torch.outer(torch.arange(70000, dtype=torch.float32),
+                      1.0 / (10000.0 ** (torch.arange(0, rd, 2, dtype=torch.float32) / rd)))
+    cos, sin = torch.cos(ang).to(DEV), torch.sin(ang).to(DEV)
+    l0 = layers[0]
+    mk = lambda: DecodeLayer(l0["ring"].clone(), l0["ckv"].clone(), l0["k8"].clone(), l0["ks"].clone(), st["sink"],  # noqa: E731
+                             cos, sin, cfg.ratio, cfg.topk, rd=rd)
+    A, B = mk(), mk()
+    g = torch.Generator(device=DEV).manual_seed(5)
+    for step in range(4):
+        pos = st["pos"] + step  # step 0 closes every row's group, 1-3 do not (spare rows), ...
+        kv_raw = torch.randn(4, 576, generator=g, device=DEV).to(torch.bfloat16)
+        latent = torch.randn(4, 1, 576, generator=g, device=DEV).to(torch.bfloat16)
+        k_raw = (torch.randn(4, 128, generator=g, device=DEV) * 2).to(torch.bfloat16)
+        q_idx = st["q_idx"] * (1 + step)
+        cand = None
+        if step == 3:
+            cand = torch.rand(4, 1, A.k8.shape[1], generator=g, device=DEV) < 0.7
+        print(f"[decode_select] step {step} pos {pos.tolist()}", flush=True)
+        A.appends(kv_raw, st["kv_norm"], latent, k_raw, st["k_norm"], pos, st["seq"], q_idx, st["w_idx"])
+        cl = torch.div(pos + 1, cfg.ratio, rounding_mode="floor")
+        want = A.selector(4, DEV)(q_idx, A.k8, st["w_idx"], st["seq"], cl, k_scale=A.ks, prepared=A._prepared,
+                                  cand=cand).clone()
+        got = B.appends_select(kv_raw, st["kv_norm"], latent, k_raw, st["k_norm"], pos, st["seq"], q_idx,
+                               st["w_idx"], cl=cl, cand=cand).clone()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy(), err_msg=f"step {step}")
+        assert int(B.selector(4, DEV).fws[-4].item()) == 0, "row barrier wait gave up"
+        np.testing.assert_array_equal(B.k8.view(torch.uint8).cpu().numpy(), A.k8.view(torch.uint8).cpu().numpy())
+        np.testing.assert_array_equal(B.ks.cpu().numpy(), A.ks.cpu().numpy())
+        np.testing.assert_array_equal(host(B.ckv), host(A.ckv))
+        _fp8_close(host(B.ring), host(A.ring), f"decode_select ring step {step}")
