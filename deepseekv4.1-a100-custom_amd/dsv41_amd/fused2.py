@@ -51,7 +51,7 @@ def sattn2(q, kv_win, kv_c, idx, pos, attn_sink, cos, sin, rd, softmax_scale, se
     sink = attn_sink.float().contiguous()
     o = torch.empty(b, 1, h, dv, device=dev, dtype=q.dtype)
     nbytes = lib().dsv41_attn_workspace_bytes(b, h, win + t, dv, nsplit)
-    if ws is None:  # the split-arrival counters at its end must start at zero; the library leaves them at zero
+    if ws is None:  # the split-arrival counters at its start must be zero at first use; launches leave them ready
         ws = torch.zeros(max(nbytes, 4) // 4, device=dev, dtype=torch.float32) if nbytes > 0 else None
     else:
         assert ws.numel() * ws.element_size() >= nbytes, "workspace too small"
