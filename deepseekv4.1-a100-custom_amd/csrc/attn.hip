@@ -1633,6 +1633,39 @@ int dsv41_sparse_attn(const void* q, const void* kv, const float* sink, const in
   return dispatch(a, dqk, dv, (hipStream_t)stream);
 }
 
+int dsv41_sparse_attn_kv2(const void* q, const void* kv, const void* kv2, const float* sink, const int* idx, void* out,
+                          int b, int s, int h, int dqk, int dv, int n_kv, long kv_bstride, int n2, long kv2_bstride,
+                          int t, long idx_rstride, float scale, int want_nsplit, void* ws, long ws_bytes,
+                          void* stream) {
+  if (b <= 0 || s <= 0) return 0;
+  if (n_kv <= 0 || n2 < 0 || (n2 > 0 && !kv2) || t < 0 || h <= 0 || idx_rstride < t) return (int)hipErrorInvalidValue;
+  AttnArgs a{};
+  a.q = (const uint16_t*)q;
+  a.q_rstride = (long)h * dqk;
+  a.H = h;
+  a.R = b * s;
+  a.mode = 0;
+  a.kv1 = (const uint16_t*)kv;
+  a.kv1_sstride = kv_bstride;
+  a.n1 = n_kv;
+  a.kv2 = n2 > 0 ? (const uint16_t*)kv2 : nullptr;
+  a.kv2_sstride = kv2_bstride;
+  a.n2 = n2;
+  a.idx = idx;
+  a.idx_rstride = idx_rstride;
+  a.t = t;
+  a.rows_per_slot = s;
+  a.scale = scale;
+  a.sink = sink;
+  a.L = t;
+  a.out = (uint16_t*)out;
+  a.out_rstride = (long)h * dv;
+  a.rd = 0;
+  int rc = finish_plan(a, want_nsplit, ws, ws_bytes, dv);
+  if (rc) return rc;
+  return dispatch(a, dqk, dv, (hipStream_t)stream);
+}
+
 int dsv41_sparse_attn2(const void* q, const void* kv1, const void* kv2, const float* sink, const int* idx, void* out,
                        int b, int h, int d, int n1, long kv1_bstride, int n2, long kv2_bstride, int t, float scale,
                        int want_nsplit, void* ws, long ws_bytes, void* stream) {

@@ -18,6 +18,7 @@ _P, _L, _I, _F = ctypes.c_void_p, ctypes.c_long, ctypes.c_int, ctypes.c_float
 SIGNATURES = {
     "dsv41_attn_workspace_bytes": [_I, _I, _I, _I, _I],
     "dsv41_sparse_attn": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _L, _I, _F, _I, _P, _L, _P],
+    "dsv41_sparse_attn_kv2": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _L, _I, _L, _I, _L, _F, _I, _P, _L, _P],
     "dsv41_sparse_attn2": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _L, _I, _L, _I, _F, _I, _P, _L, _P],
     "dsv41_sattn2": [_P, _P, _L, _I, _P, _L, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _F, _P, _I, _I, _I, _I, _I,
                      _P, _L, _P],

@@ -32,7 +32,8 @@ def _candidate_blocks(score, R, n, width, clp, cl_start, cl_ratio, rows_per_seq,
 
 def index_topk(q: torch.Tensor, weights: torch.Tensor, index_k: torch.Tensor, start_pos: int, ratio: int, topk: int,
                offset: int, k_scale: torch.Tensor | None = None, return_score: bool = False,
-               candidates: torch.Tensor | None = None, candidate_source: tuple | None = None):
+               candidates: torch.Tensor | None = None, candidate_source: tuple | None = None,
+               out: torch.Tensor | None = None):
     """q: bf16 [b, s, H, 128] (rope'd, FP4-rounded index queries); weights: [b, s, H] (already scaled by
     d^-1/2 H^-1/2); index_k: [>= b, >= end//ratio, 128] bf16, or float8_e4m3fn with k_scale [>= b, >= end//ratio]
     fp32; query i sees compressed positions t < (start_pos + i + 1) // ratio.  Returns int32
@@ -40,13 +41,19 @@ def index_topk(q: torch.Tensor, weights: torch.Tensor, index_k: torch.Tensor, st
     Candidate blocks (dsv41/model.py:838-866): candidates = bool [b, s, >= end//ratio] masks a consumer layer's
     scores (non-candidates score -inf and fill the selection last, lowest index first); candidate_source =
     (topk_blocks, block_size) makes this the source layer and also returns its mask, bool [b, s, index_k.shape[1]].
-    With return_score the scores come second: (out, score[, mask])."""
+    With return_score the scores come second: (out, score[, mask]).  out (optional): an int32 [b, s, kk] view with
+    unit column stride (e.g. the compressed columns of a preallocated [window | compressed] index buffer) that
+    receives the selection."""
     b, s, H, D = q.shape
     dev = require_gpu(q, weights, index_k)
     end = start_pos + s
     T = end // ratio
     kk = min(topk, T)
-    out = torch.empty(b, s, kk, device=dev, dtype=torch.int32)
+    if out is None:
+        out = torch.empty(b, s, kk, device=dev, dtype=torch.int32)
+    elif (out.shape != (b, s, kk) or out.dtype != torch.int32 or out.stride(-1) != 1
+          or out.stride(0) != out.stride(1) * s):
+        raise RuntimeError(f"index_topk: out {tuple(out.shape)} {out.dtype} is not an int32 [{b}, {s}, {kk}] row view")
     if b * s == 0 or kk == 0:
         res = (out,) + ((None,) if return_score else ()) + (
             (torch.zeros(b, s, index_k.shape[1], dtype=torch.bool, device=dev),) if candidate_source is not None else ())
@@ -79,7 +86,8 @@ def index_topk(q: torch.Tensor, weights: torch.Tensor, index_k: torch.Tensor, st
     else:
         call("dsv41_index_score", ptr(qc), H * D, ptr(w), H, b * s, H, D, 0, ptr(index_k), index_k.stride(0), None, 0,
              None, s, None, start_pos, ratio, T, 0, ptr(score), T, None, cp, cs, st)
-    call("dsv41_topk_indices", ptr(score), T, b * s, T, kk, None, start_pos, ratio, s, int(offset), ptr(out), kk, st)
+    call("dsv41_topk_indices", ptr(score), T, b * s, T, kk, None, start_pos, ratio, s, int(offset), ptr(out),
+         out.stride(1), st)
     res = (out,)
     if return_score:  # positions at or past a row's causal limit are not written (the top-k never reads them)
         res += (score.view(b, s, T),)

@@ -34,6 +34,14 @@ int dsv41_sparse_attn(const void* q, const void* kv, const float* sink, const in
                       int dqk, int dv, int n_kv, long kv_bstride, int t, float scale, int want_nsplit, void* ws,
                       long ws_bytes, void* stream);
 
+/* dsv41_sparse_attn over two KV sources without concatenating them: index i < n_kv reads kv[i], n_kv <= i < n_kv + n2
+ * reads kv2[i - n_kv] (the reference's torch.cat of the window and compressed rows and of their index lists before
+ * kernels.sparse_attn, dsv41/model.py:1442-1443); idx rows have stride idx_rstride >= t. */
+int dsv41_sparse_attn_kv2(const void* q, const void* kv, const void* kv2, const float* sink, const int* idx, void* out,
+                          int b, int s, int h, int dqk, int dv, int n_kv, long kv_bstride, int n2, long kv2_bstride,
+                          int t, long idx_rstride, float scale, int want_nsplit, void* ws, long ws_bytes,
+                          void* stream);
+
 /* fused.sparse_attn_decode2 / sparse_attn_decode_split (dsv41/fused.py:352-403, :406-472): one query per batch
  * row; index < n1 reads kv1[b, index], otherwise kv2[b, index - n1]. */
 int dsv41_sparse_attn2(const void* q, const void* kv1, const void* kv2, const float* sink, const int* idx, void* out,

@@ -704,3 +704,37 @@ def test_decode_appends_select_one_launch():
         np.testing.assert_array_equal(B.ks.cpu().numpy(), A.ks.cpu().numpy())
         np.testing.assert_array_equal(host(B.ckv), host(A.ckv))
         _fp8_close(host(B.ring), host(A.ring), f"decode_select ring step {step}")
+
+
+def test_sparse_attn_two_sources_and_topk_view():
+    """kernels.sparse_attn over [window | compressed] read in place (kv2) with the index list in a preallocated
+    buffer whose compressed columns index_topk fills (out=) == the reference's torch.cat of both
+    (dsv41/model.py:1442-1443), bit for bit; also against the oracle."""
+    import dsv41_amd
+    from dsv41_amd.indexer import index_topk
+    from dsv41_amd.workloads import encode_e4m3_rows, fp4_round
+    r = rng(19)
+    g = torch.Generator(device=DEV).manual_seed(19)
+    h, dqk, dv, s, start, ratio, k = 64, 576, 512, 256, 4000, 4, 300
+    n_w, n_c = 200, (start + s) // ratio
+    q = bf(r.standard_normal((1, s, h, dqk)).astype(np.float32))
+    win = bf(r.standard_normal((1, n_w, dqk)).astype(np.float32) * 0.1)
+    ckv = bf(r.standard_normal((1, n_c + 5, dqk)).astype(np.float32) * 0.1)
+    sink = f32(r.standard_normal(h).astype(np.float32))
+    k8, ks = encode_e4m3_rows(fp4_round(torch.randn(1, n_c + 5, 128, generator=g, device=DEV) * 0.1))
+    qi = fp4_round(torch.randn(1, s, 64, 128, generator=g, device=DEV))
+    wi = torch.randn(1, s, 64, generator=g, device=DEV) * 0.01
+    widx = torch.from_numpy(r.integers(-1, n_w, (1, s, 128)).astype(np.int32)).to(DEV)
+    want_c = index_topk(qi, wi, k8, start, ratio, k, n_w, k_scale=ks)
+    buf = torch.full((1, s, 128 + k + 9), 12345, dtype=torch.int32, device=DEV)  # wider rows than the index list
+    index_topk(qi, wi, k8, start, ratio, k, n_w, k_scale=ks, out=buf[:, :, 128:128 + k])
+    buf[:, :, :128] = widx
+    np.testing.assert_array_equal(buf[:, :, 128:128 + k].cpu().numpy(), want_c.cpu().numpy())
+    idx_cat = torch.cat([widx, want_c], dim=-1)
+    scale = dqk ** -0.5
+    want = dsv41_amd.sparse_attn(q, torch.cat([win, ckv[:, :n_c]], dim=1), sink, idx_cat, scale, d_v=dv)
+    got = dsv41_amd.sparse_attn(q, win, sink, buf[:, :, :128 + k], scale, d_v=dv, kv2=ckv[:, :n_c])
+    np.testing.assert_array_equal(host(got), host(want))
+    kvc = np.concatenate([host(win), host(ckv)[:, :n_c]], axis=1)
+    attn_close(host(got), O.sparse_attn(host(q), kvc, host(sink), idx_cat.cpu().numpy(), scale, dv=dv),
+               "sparse_attn two sources")
