@@ -304,6 +304,63 @@ def run_prefill(args, dev):
                                              (MFMA_BF16_TFLOPS * 1e12)) / (t_graph * 1e-6), 4)}}
 
 
+# The attention layer's FP8 projections at the reference's decode shapes (results/dense_chain_report.md, table 1:
+# dim 5120, q rank 1280, 64 heads x 512, 8 output groups x rank 1024) and its isolated A100 times (us, M = 1).
+PROJ_SHAPES = [("wq_a", 1280, 5120, 0, 8.1), ("wq_b", 32768, 1280, 0, 33.4), ("wkv", 512, 5120, 0, 4.9),
+               ("wo_a", 8192, 4096, 1024, None), ("wo_b", 5120, 8192, 0, 32.1)]
+
+
+def run_projections(args, dev):
+    """dsv41_fp8_gemm at the projection shapes, M = 1 (the reference's decode) and M = 4 (C2's rows): each weight
+    in enough copies to exceed the 256 MB last-level cache, a graph of one launch per copy, replayed; algorithmic
+    bytes = weights + scales + x + out."""
+    import torch
+    from dsv41_amd.w8 import fp8_gemm_tc
+    res = {}
+    for name, N, K, gc, ref_us in PROJ_SHAPES:
+        wbytes = N * K + ((N + 31) // 32) * (K // 32)
+        copies = max(2, -(-600_000_000 // wbytes))
+        ws = []
+        for c in range(copies):
+            w = torch.randint(0, 256, (N, K), dtype=torch.uint8, device=dev)
+            w = torch.where((w & 0x7F) == 0x7F, torch.full_like(w, 0x38), w)
+            sc = torch.randint(117, 131, ((N + 31) // 32, K // 32), dtype=torch.uint8, device=dev)
+            ws.append((w, sc))
+        for M in (1, 4):
+            G = N // gc if gc else 1
+            x = (torch.randn(M * G, K, device=dev) * 0.1).to(torch.bfloat16)
+            s2 = torch.cuda.Stream(dev)
+            s2.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(s2):
+                for w, sc in ws:
+                    fp8_gemm_tc(x, w, sc, gc)
+            torch.cuda.synchronize(dev)
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=s2):
+                for w, sc in ws:
+                    fp8_gemm_tc(x, w, sc, gc)
+            gr.replay()
+            torch.cuda.synchronize(dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 5
+            e0.record()
+            for _ in range(reps):
+                gr.replay()
+            e1.record()
+            torch.cuda.synchronize(dev)
+            us = e0.elapsed_time(e1) * 1000.0 / (reps * copies)
+            b = wbytes + M * G * K * 2 + M * N * 2
+            gbs = b / (us * 1e-6) / 1e9
+            res[f"{name}_M{M}"] = {"N": N, "K": K, "group_cols": gc, "us": round(us, 2), "GB_s": round(gbs, 1),
+                                   "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
+                                   "reference_a100_us": ref_us if M == 1 else None}
+            log(f"[bench] fp8 projection {name} [{N} x {K}] M={M}: {us:.2f} us, {gbs:.0f} GB/s "
+                f"({100 * gbs / HBM_PEAK_GBS:.1f} % of 8 TB/s)")
+        del ws
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(cfg, budget_s: float):
     """The oracle (numpy port of the reference's decode path) on the host: index score + top-k + sattn2 for one
     slot of the workload, repeated until the budget is spent; scaled to a full layer-step (x slots)."""
@@ -352,6 +409,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-proj", action="store_true", help="skip the FP8 projection GEMVs")
+    ap.add_argument("--proj-only", action="store_true", help="only the FP8 projection GEMVs (for profiling)")
     ap.add_argument("--separate-appends", action="store_true",
                     help="decode: the cache appends as their own launch before the indexer (default: one launch)")
     ap.add_argument("--prefill-reps", type=int, default=5)
@@ -376,6 +435,9 @@ def main():
     if args.prefill_only:
         print(json.dumps({"prefill": run_prefill(args, dev)}), flush=True)
         return
+    if args.proj_only:
+        print(json.dumps({"projections": run_projections(args, dev)}), flush=True)
+        return
     r = run_decode(args, dev)
     cfg = r["cfg"]
     kb, ku = r["kern_bytes"], r["kern_us"]
@@ -397,6 +459,7 @@ def main():
     alg = survey_bytes(cfg)
     frac_step = alg / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS
     pre = None if args.no_prefill else run_prefill(args, dev)
+    proj = None if args.no_proj else run_projections(args, dev)
     cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_budget)
     out = {
         "metric": "attn decode us/layer-step + % HBM roofline @128Kx4 slots; prefill tok/s @2K chunk",
@@ -420,6 +483,7 @@ def main():
         "roofline": roof[dom],
         "roofline_other": {k: v for k, v in roof.items() if k != dom},
         "prefill": pre,
+        "projections": proj,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

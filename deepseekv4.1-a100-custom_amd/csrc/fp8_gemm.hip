@@ -1,0 +1,254 @@
+// FP8 block-scaled projections around the attention path (wq_a, wq_b, wkv, wo_a block-diagonal, wo_b; the
+// fp8_gemm_tc / fp8_gemv_m1 operators of dsv41/cukern.py:116-200 with the weight format of dsv41/w8.py:19-60):
+//   out[m, n] = sum_k x[row(m, n), k] * e4m3(W[n, k]) * 2^(S[n / 32, k / 32] - 127)
+// x bf16, fp32 accumulation, bf16 output (optionally fp32 too).  W is stored with the bytes of every 16-k group
+// permuted (position p holds k = 16 (p / 16) + kPermK[p % 16]); S is E8M0 per [32 n x 32 k] block.  row(m, n) = m,
+// or with group_cols > 0 (block-diagonal o-projection) m * (N / group_cols) + n / group_cols.
+//
+// A weight stream: every weight byte is read once per 64 output rows.  Workgroup = 4 waves x 16 columns (64
+// columns) over a K slice; a lane loads 16 weight bytes (one 16-k group, inside one scale block) per 64-k window and
+// converts them to bf16 with the block scale applied by the hardware (v_cvt_scalef32_pk_bf16_fp8: exact, the e4m3
+// values times a power of two); the x slice is staged in LDS in the weights' byte order, so a bf16 MFMA (16 rows x
+// 16 columns x 32 k) pairs every weight with its x element.  Split K: each slice writes fp32 partials with
+// device-scope stores, and the last slice of a column tile to arrive (device-scope counter) sums them in slice order
+// (deterministic) and writes the output.
+#include "common.h"
+
+namespace {
+
+constexpr int kGemmThreads = 256;             // 4 waves, 16 columns each
+constexpr int kGemmCols = 64;                 // columns per workgroup
+constexpr int kGemmLdsBf16 = 32 * 1024;       // staged x elements at most (64 KB of dynamic LDS)
+constexpr int kPermK[16] = {0, 1, 8, 9, 2, 3, 10, 11, 4, 5, 12, 13, 6, 7, 14, 15};  // dsv41/w8.py:23
+
+typedef __bf16 bf16x2g_t __attribute__((ext_vector_type(2)));
+
+struct GemmArgs {
+  const uint16_t* x;  // bf16 rows, row stride ldx
+  long ldx;
+  const uint8_t* w8;  // [N, K] e4m3 bits, 16-k groups permuted
+  const uint8_t* s8;  // [ceil(N / 32), Kc] E8M0
+  int M, N, K, Kc, group_cols;
+  int m0;             // first output row of this launch (rows m0 .. m0 + M - 1)
+  int splits, kslice; // K slices (kslice: multiple of 64)
+  uint16_t* out;      // bf16 [rows, ldo]
+  long ldo;
+  float* outf;        // optional fp32 copy [rows, ldo]
+  float* part;        // [splits, 16 * MT, N] fp32 partials (splits > 1)
+  int* cnt;           // [column tiles] arrival counters (zero between launches)
+};
+
+DSV41_DEV float e8m0_scale(uint32_t s) { return s ? __uint_as_float(s << 23) : __uint_as_float(0x00400000u); }
+
+// 4 e4m3 bytes -> 4 bf16 (2 words) times the scale.
+DSV41_DEV void cvt4(uint32_t w, float sc, uint32_t& lo, uint32_t& hi) {
+  lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, sc, false));
+  hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, sc, true));
+}
+
+template <int MT>
+__global__ void __launch_bounds__(kGemmThreads) fp8_gemm_kernel(const GemmArgs a) {
+  extern __shared__ __align__(16) uint16_t xs[];  // [M rows][kl] in weight byte order (dynamic: M x kslice)
+  __shared__ int s_last;
+  constexpr int MR = 16 * MT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int ct = blockIdx.x, sp = blockIdx.y;
+  const int n0 = ct * kGemmCols;
+  const int k0 = sp * a.kslice, k1 = min(a.K, k0 + a.kslice), kl = k1 - k0;  // kl: multiple of 64
+  const int xr_off = a.group_cols > 0 ? n0 / a.group_cols : 0;
+  const int xr_mul = a.group_cols > 0 ? a.N / a.group_cols : 1;
+
+  // ---- weight stream: lane (l16, g) owns column n0 + 16 wave + l16, bytes 16 g .. 16 g + 15 of every 64-k window;
+  // the first windows' loads go out before x is staged (independent round trips overlap)
+  const int n = n0 + wave * 16 + l16;
+  const int nc = n < a.N ? n : a.N - 1;
+  const uint8_t* wrow = a.w8 + (long)nc * a.K + k0 + 16 * g;
+  const uint8_t* srow = a.s8 + (long)(nc >> 5) * a.Kc + ((k0 + 16 * g) >> 5);
+  const int nw = kl / 64;
+  constexpr int U = 4;  // windows per batch; two batches in flight
+  uint4 wv[U];
+  uint32_t sv[U];
+  auto load_batch = [&](int w0, uint4 (&dw)[U], uint32_t (&ds)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int w = w0 + u < nw ? w0 + u : nw - 1;
+      dw[u] = *(const uint4*)(wrow + 64 * w);
+      ds[u] = srow[2 * w];
+    }
+  };
+  load_batch(0, wv, sv);
+
+  // ---- stage x[rows, k0..k1) into LDS in the weights' byte order (16-byte units: 8 elements = one half group)
+  {
+    const int units = a.M * (kl / 8);
+#pragma unroll 1
+    for (int u = tid; u < units; u += kGemmThreads) {
+      const int m = u / (kl / 8), p8 = (u - m * (kl / 8)) * 8;  // byte position p8 .. p8 + 7
+      const int gm = a.m0 + m;
+      uint32_t v[4];
+      const uint16_t* xrow = a.x + (long)(gm * xr_mul + xr_off) * a.ldx + k0 + (p8 & ~15);
+      const int h = (p8 & 8) ? 8 : 0;  // positions h..h+7 of the group hold k = kPermK[h..h+7]: pairs (2j, 2j+1)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = *(const uint32_t*)(xrow + kPermK[h + 2 * j]);
+      *(uint4*)(xs + m * kl + p8) = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+  }
+  __syncthreads();
+
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+  for (int w0 = 0; w0 < nw; w0 += U) {
+    uint4 wn[U];
+    uint32_t sn[U];
+    if (w0 + U < nw) load_batch(w0 + U, wn, sn);  // the next batch in flight while this one is used
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (w0 + u >= nw) break;
+      const float sc = e8m0_scale(sv[u]);
+      uint32_t b[8];
+      cvt4(wv[u].x, sc, b[0], b[1]);
+      cvt4(wv[u].y, sc, b[2], b[3]);
+      cvt4(wv[u].z, sc, b[4], b[5]);
+      cvt4(wv[u].w, sc, b[6], b[7]);
+      const uint4 b0 = make_uint4(b[0], b[1], b[2], b[3]), b1 = make_uint4(b[4], b[5], b[6], b[7]);
+      const int p = 64 * (w0 + u) + 16 * g;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {  // (rows past M: zero operands, nothing staged)
+        const bool rv = 16 * mt + l16 < a.M;
+        const uint16_t* xa = xs + (rv ? 16 * mt + l16 : 0) * kl + p;
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        acc[mt] = mfma_bf16_16x16x32(rv ? *(const uint4*)xa : z, b0, acc[mt]);
+        acc[mt] = mfma_bf16_16x16x32(rv ? *(const uint4*)(xa + 8) : z, b1, acc[mt]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      wv[u] = wn[u];
+      sv[u] = sn[u];
+    }
+  }
+  // lane (l16, g) holds out[16 mt + 4 g + i][n]
+  auto store = [&](int m, float v) {
+    if (m < a.M && n < a.N) {
+      const long o = (long)(a.m0 + m) * a.ldo + n;
+      a.out[o] = f2bf(v);
+      if (a.outf) a.outf[o] = v;
+    }
+  };
+  if (a.splits == 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) store(16 * mt + 4 * g + i, acc[mt][i]);
+    return;
+  }
+  // ---- split K: partials out with device-scope stores, the last slice of the column tile reduces
+  float* pb = a.part + (long)sp * MR * a.N;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (n < a.N)
+        __hip_atomic_store(pb + (long)(16 * mt + 4 * g + i) * a.N + n, acc[mt][i], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const int old = __hip_atomic_fetch_add(a.cnt + ct, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == a.splits - 1;
+    if (s_last) __hip_atomic_store(a.cnt + ct, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // thread t: column n0 + t % 64, rows t / 64, + 4, ...
+  const int cn = n0 + (tid & 63);
+  if (cn >= a.N) return;
+#pragma unroll 1
+  for (int m = tid >> 6; m < min(MR, a.M); m += 4) {
+    float v = 0.0f;
+#pragma unroll 4
+    for (int s = 0; s < a.splits; ++s)
+      v += __hip_atomic_load(a.part + ((long)s * MR + m) * a.N + cn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const long o = (long)(a.m0 + m) * a.ldo + cn;
+    a.out[o] = f2bf(v);
+    if (a.outf) a.outf[o] = v;
+  }
+}
+
+// Plan: row tiles of up to 64 rows (MT = 1, 2, 4), K slices so that the grid holds >= 512 workgroups when K allows
+// (slices >= 256 k) and the staged x fits LDS.
+struct GemmPlan {
+  int MT, splits, kslice, ctiles;
+};
+
+GemmPlan gemm_plan(int M, int N, int K) {
+  GemmPlan p{};
+  const int mrows = M < 64 ? M : 64;
+  p.MT = mrows <= 16 ? 1 : mrows <= 32 ? 2 : 4;
+  p.ctiles = (N + kGemmCols - 1) / kGemmCols;
+  const int kmax = kGemmLdsBf16 / mrows / 64 * 64;  // staged elements per row
+  int s = (K + kmax - 1) / kmax;
+  while ((long)p.ctiles * s < 512 && K / (2 * s) >= 256) s *= 2;
+  int ks = (K + s - 1) / s;
+  ks = (ks + 63) / 64 * 64;
+  p.kslice = ks;
+  p.splits = (K + ks - 1) / ks;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+long dsv41_fp8_gemm_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const GemmPlan p = gemm_plan(M, N, K);
+  if (p.splits == 1) return 0;
+  return (long)p.ctiles * 4 + 12 + (long)p.splits * 16 * p.MT * N * 4;  // counters, pad, partials
+}
+
+int dsv41_fp8_gemm(const void* x, long ldx, const void* w8, const void* s8, int M, int N, int K, int Kc,
+                   int group_cols, void* out, long ldo, float* out_f32, void* ws, long ws_bytes, void* stream) {
+  if (M <= 0 || N <= 0) return 0;
+  if (K <= 0 || K % 64 != 0 || Kc < K / 32 || !x || !w8 || !s8 || !out || ldo < N || ldx < K || ldx % 2 != 0 ||
+      ((uintptr_t)x & 3) != 0 || ((uintptr_t)w8 & 15) != 0 ||
+      (group_cols > 0 && (group_cols % kGemmCols != 0 || N % group_cols != 0)) || group_cols < 0)
+    return (int)hipErrorInvalidValue;
+  const GemmPlan p = gemm_plan(M, N, K);
+  if (p.splits > 1 && (!ws || ws_bytes < dsv41_fp8_gemm_workspace_bytes(M, N, K))) return (int)hipErrorInvalidValue;
+  GemmArgs a{};
+  a.x = (const uint16_t*)x;
+  a.ldx = ldx;
+  a.w8 = (const uint8_t*)w8;
+  a.s8 = (const uint8_t*)s8;
+  a.N = N;
+  a.K = K;
+  a.Kc = Kc;
+  a.group_cols = group_cols;
+  a.splits = p.splits;
+  a.kslice = p.kslice;
+  a.out = (uint16_t*)out;
+  a.ldo = ldo;
+  a.outf = out_f32;
+  if (p.splits > 1) {
+    a.cnt = (int*)ws;
+    a.part = (float*)((char*)ws + ((long)p.ctiles * 4 + 15) / 16 * 16);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(p.ctiles, p.splits);
+  for (int m0 = 0; m0 < M; m0 += 16 * p.MT) {  // row tiles (more than 64 rows: the weights stream once per 64)
+    a.m0 = m0;
+    a.M = M - m0 < 16 * p.MT ? M - m0 : 16 * p.MT;
+    const size_t lds = (size_t)a.M * p.kslice * 2;
+    if (p.MT == 1) fp8_gemm_kernel<1><<<grid, kGemmThreads, lds, st>>>(a);
+    else if (p.MT == 2) fp8_gemm_kernel<2><<<grid, kGemmThreads, lds, st>>>(a);
+    else fp8_gemm_kernel<4><<<grid, kGemmThreads, lds, st>>>(a);
+    DSV41_CHECK_LAUNCH();
+  }
+  return 0;
+}
+
+}  // extern "C"

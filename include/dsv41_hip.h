@@ -222,6 +222,21 @@ int dsv41_decode_appends(const void* kv_raw, const void* kv_norm, void* ring, lo
                          const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
                          const void* w_idx, int HI, void* q8, float* wf, int B, void* stream);
 
+/* ------------------------------------------------------------------------------------------------ projections */
+
+/* Workspace bytes of dsv41_fp8_gemm for M rows, N columns, K (0 when no K split is planned).  Allocate it zeroed
+ * once per shape: every launch leaves its arrival counters at zero (launches sharing it must be stream-ordered). */
+long dsv41_fp8_gemm_workspace_bytes(int M, int N, int K);
+
+/* fp8_gemm_tc / fp8_gemv_m1 (dsv41/cukern.py:116-200; weight format dsv41/w8.py:19-60): out[m, n] =
+ * sum_k x[row(m, n), k] * e4m3(w8[n, k]) * 2^(s8[n / 32, k / 32] - 127), bf16 x (row stride ldx), fp32
+ * accumulation, bf16 out [M, ldo] (and fp32 out_f32 [M, ldo] when not null).  w8: e4m3 bits [N, K] with every 16-k
+ * group in the PERM_K byte order; s8: E8M0 [ceil(N / 32), Kc], Kc >= K / 32.  row(m, n) = m, or with group_cols > 0
+ * (block-diagonal, dsv41/w8.py oproj_a) m * (N / group_cols) + n / group_cols.  K % 64 == 0; group_cols % 64 == 0;
+ * x 4-byte and w8 16-byte aligned.  The weights stream once per 64 rows of M. */
+int dsv41_fp8_gemm(const void* x, long ldx, const void* w8, const void* s8, int M, int N, int K, int Kc,
+                   int group_cols, void* out, long ldo, float* out_f32, void* ws, long ws_bytes, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ numerics */
 
 /* fake_quant_fp8 / fake_quant_fp4 (dsv41/fused.py:46-87, dsv41/quant.py:45-87) on rows of D bf16 values. */

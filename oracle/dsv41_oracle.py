@@ -36,6 +36,9 @@ PINNING = {
     "compress_pool": "fed as any mix of prefill chunks and single decode rows, every closed group's latent equals the "
                      "one-call start_pos 0 result; equal gate scores give the group mean, one dominant score gives that "
                      "member; vs torch.softmax composition (library routine)",
+    "e4m3_decode": "all 256 codes vs torch.float8_e4m3fn -> float32 cast (library routine)",
+    "fp8_gemm": "vs torch matmul of the dequantised weight (library routine, exact products); PERM_K round trip "
+                "(known list dsv41/w8.py:23); block-diagonal == the dense product with the off-group blocks zeroed",
     "select_candidate_blocks": "properties of the top blocks (forced last block, count, every kept block max >= every "
                                "dropped finite one, whole blocks); indexer with candidates chunked == full exactly "
                                "(dsv41/test_long_prefill.py:66-96)",
@@ -492,6 +495,51 @@ def compress_pool_decode(kv, score, pos, seq, ratio: int, ring_kv, ring_sc, norm
     lat = bf16(rmsnorm(bf16(np.stack(lat)), norm_w, eps))
     should = np.array([(p + 1) % ratio == 0 for p in pos])
     return lat, should, ring_kv, ring_sc
+
+
+# ----------------------------------------------------------------------------------------------- projections
+PERM_K = [0, 1, 8, 9, 2, 3, 10, 11, 4, 5, 12, 13, 6, 7, 14, 15]  # byte order of a 16-k group, dsv41/w8.py:23
+
+
+def e4m3_decode(bits) -> np.ndarray:
+    """Value of e4m3 (fn) bit patterns: s eeee mmm, bias 7, subnormals at e = 0, 0x7f / 0xff NaN (OCP FP8)."""
+    b = np.asarray(bits, np.uint8).astype(np.int64)
+    sign = np.where(b & 0x80, -1.0, 1.0)
+    e = (b >> 3) & 15
+    m = b & 7
+    v = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * 2.0 ** (e - 7.0))
+    v = np.where((b & 0x7F) == 0x7F, np.nan, v)
+    return (sign * v).astype(np.float32)
+
+
+def fp8_dequant(w8, s8, permuted: bool = True) -> np.ndarray:
+    """dsv41/w8.py W8.bf16 / quant.dequant_fp8_block: e4m3 [N, K] (PERM_K byte order when permuted) times
+    2^(s8[n // 32, k // 32] - 127) -> fp32 [N, K] (exact)."""
+    w8 = np.asarray(w8, np.uint8)
+    N, K = w8.shape
+    if permuted:
+        inv = [PERM_K.index(i) for i in range(16)]
+        w8 = w8.reshape(N, K // 16, 16)[:, :, inv].reshape(N, K)
+    sc = np.ldexp(np.float64(1.0), np.asarray(s8, np.int64) - 127)
+    sc = np.repeat(np.repeat(sc, 32, 0)[:N], 32, 1)[:, :K]
+    return (e4m3_decode(w8).astype(np.float64) * sc).astype(np.float32)
+
+
+def fp8_gemm(x, w8, s8, group_cols: int = 0) -> np.ndarray:
+    """dsv41/cukern.py fp8_gemm_tc (:164-200): x [M, K] (bf16 values) @ dequant(w8, s8)^T, accumulated exactly
+    (float64) and returned as fp32 [Mo, N]; group_cols > 0: output row b, column n uses x row
+    b * (N // group_cols) + n // group_cols."""
+    x = np.asarray(x, np.float64)
+    W = fp8_dequant(w8, s8).astype(np.float64)
+    N = W.shape[0]
+    if not group_cols:
+        return (x @ W.T).astype(np.float32)
+    G = N // group_cols
+    Mo = x.shape[0] // G
+    out = np.zeros((Mo, N), np.float64)
+    for g in range(G):
+        out[:, g * group_cols:(g + 1) * group_cols] = x[g::G] @ W[g * group_cols:(g + 1) * group_cols].T
+    return out.astype(np.float32)
 
 
 def compress_row(latent, cos, sin, pos, rd) -> np.ndarray:

@@ -738,3 +738,34 @@ def test_sparse_attn_two_sources_and_topk_view():
     kvc = np.concatenate([host(win), host(ckv)[:, :n_c]], axis=1)
     attn_close(host(got), O.sparse_attn(host(q), kvc, host(sink), idx_cat.cpu().numpy(), scale, dv=dv),
                "sparse_attn two sources")
+
+
+@pytest.mark.parametrize("M,N,K,gc", [(1, 1280, 5120, 0), (4, 512, 5120, 0), (1, 4096, 1280, 0), (16, 384, 2048, 0),
+                                      (20, 200, 640, 0), (70, 256, 1024, 0), (1, 2048, 1024, 256), (3, 1024, 512, 128)])
+def test_fp8_gemm(M, N, K, gc):
+    """fp8_gemm_tc / fp8_gemv_m1 (dsv41/cukern.py:116-200): fp32 result within fp32 summation-order error of the
+    exact (float64) oracle, bf16 result its rounding; e4m3 codes over the whole range (subnormals included), E8M0
+    scales incl. the smallest, column tails (N % 64 != 0), split K, more than 64 rows, block-diagonal."""
+    from dsv41_amd.w8 import fp8_gemm_tc
+    r = rng(43)
+    codes = r.integers(0, 256, (N, K)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x01  # NaN codes -> the smallest subnormal
+    s8 = r.integers(100, 140, ((N + 31) // 32, K // 32)).astype(np.uint8)
+    s8[0, 0] = 1  # 2^-126
+    perm = codes.reshape(N, K // 16, 16)[:, :, O.PERM_K].reshape(N, K)
+    G = N // gc if gc else 1
+    x = O.bf16(r.standard_normal((M * G, K)).astype(np.float32))
+    print(f"[fp8_gemm] M {M} N {N} K {K} group_cols {gc}", flush=True)
+    w8 = torch.from_numpy(perm).to(DEV)
+    s8t = torch.from_numpy(s8).to(DEV)
+    got32 = fp8_gemm_tc(bf(x), w8, s8t, gc, out_dtype=torch.float32).cpu().numpy()
+    got16 = host(fp8_gemm_tc(bf(x), w8, s8t, gc))
+    want = O.fp8_gemm(x, perm, s8, gc)
+    Wd = O.fp8_dequant(perm, s8).astype(np.float64)
+    if gc:
+        mag = np.concatenate([np.abs(x[g::G]) @ np.abs(Wd[g * gc:(g + 1) * gc]).T for g in range(G)], axis=1)
+    else:
+        mag = np.abs(x).astype(np.float64) @ np.abs(Wd).T
+    err = np.abs(got32 - want)
+    assert (err <= 1e-5 * mag + 1e-30).all(), (err / (mag + 1e-30)).max()
+    np.testing.assert_array_equal(got16, O.bf16(got32))

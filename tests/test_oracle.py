@@ -411,3 +411,41 @@ def test_compress_pool_closed_forms():
     t = (torch.from_numpy(kv).view(3, ratio, D) * torch.from_numpy(sc).view(3, ratio, D).softmax(dim=1)).sum(dim=1)
     np.testing.assert_allclose(O._pool(kv.reshape(3, ratio, D), sc.reshape(3, ratio, D)), t.numpy(), rtol=1e-6,
                                atol=1e-6)
+
+
+def test_e4m3_decode_all_codes():
+    """e4m3 decode of all 256 bit patterns == torch.float8_e4m3fn -> float32 (NaN codes included)."""
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(O.e4m3_decode(codes), want)
+
+
+def test_fp8_gemm_oracle():
+    """fp8_gemm (dsv41/cukern.py:164-200) == torch matmul of the dequantised weight (exact products, float64);
+    PERM_K is the byte order of dsv41/w8.py:23 (permute -> unpermute round trip); the block-diagonal form == the dense
+    product with the off-group blocks zeroed."""
+    import torch
+    r = np.random.default_rng(41)
+    N, K, M = 96, 256, 3
+    codes = r.integers(0, 256, (N, K)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x3C  # no NaN codes
+    s8 = r.integers(118, 136, (N // 32, K // 32)).astype(np.uint8)
+    perm = codes.reshape(N, K // 16, 16)[:, :, O.PERM_K].reshape(N, K)
+    assert O.PERM_K == [0, 1, 8, 9, 2, 3, 10, 11, 4, 5, 12, 13, 6, 7, 14, 15]
+    W = torch.from_numpy(codes).view(torch.float8_e4m3fn).double() * torch.from_numpy(
+        np.repeat(np.repeat(np.ldexp(1.0, s8.astype(np.int64) - 127), 32, 0), 32, 1))
+    np.testing.assert_array_equal(O.fp8_dequant(perm, s8), W.float().numpy())
+    x = O.bf16(r.standard_normal((M, K)).astype(np.float32))
+    want = (torch.from_numpy(x).double() @ W.T).float().numpy()
+    np.testing.assert_array_equal(O.fp8_gemm(x, perm, s8), want)
+    # block-diagonal: 3 groups of 32 columns, x rows b * 3 + g
+    xb = O.bf16(r.standard_normal((2 * 3, K)).astype(np.float32))
+    got = O.fp8_gemm(xb, perm, s8, group_cols=32)
+    for b in range(2):
+        for g in range(3):
+            Wz = W.clone()
+            Wz[:g * 32] = 0
+            Wz[(g + 1) * 32:] = 0
+            dense = (torch.from_numpy(xb[b * 3 + g]).double() @ Wz.T).float().numpy()
+            np.testing.assert_array_equal(got[b, g * 32:(g + 1) * 32], dense[g * 32:(g + 1) * 32])
