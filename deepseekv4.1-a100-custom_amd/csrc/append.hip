@@ -212,6 +212,39 @@ __global__ void __launch_bounds__(kRowThreads) decode_appends_kernel(const DecAp
   row_op(o, red);
 }
 
+// Index-key table conversion (the reference's bf16 table <-> this build's e4m3 + per-row scale, for cache snapshots
+// taken by either, dsv41/engine.py:1072-1230): one wave per 128-wide row, two elements per lane; the encoding is the
+// one of the key appends (row_compute's e4m3 copy).
+__global__ void __launch_bounds__(256) index_keys_encode_kernel(const uint16_t* kbf, long n_rows, uint8_t* k8,
+                                                                float* ks) {
+  const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= n_rows) return;
+  const uint32_t w = *(const uint32_t*)(kbf + r * 128 + 2 * lane);
+  const float v0 = __uint_as_float(w << 16), v1 = __uint_as_float(w & 0xffff0000u);
+  float a = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) a = fmaxf(a, wave_shfl_xor(a, m));
+  int ex = ceil_log2_f(__fdiv_rn(fmaxf(a, 1e-30f), 448.0f));
+  ex = ex < -126 ? -126 : ex;
+  const float inv = pow2i(-ex);
+  const uint32_t b0 = e4m3_bits(round_e4m3(fminf(fmaxf(v0 * inv, -448.0f), 448.0f)));
+  const uint32_t b1 = e4m3_bits(round_e4m3(fminf(fmaxf(v1 * inv, -448.0f), 448.0f)));
+  *(uint16_t*)(k8 + r * 128 + 2 * lane) = (uint16_t)(b0 | b1 << 8);
+  if (lane == 0) ks[r] = pow2i(ex);
+}
+
+__global__ void __launch_bounds__(256) index_keys_decode_kernel(const uint8_t* k8, const float* ks, long n_rows,
+                                                                uint16_t* kbf) {
+  const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= n_rows) return;
+  const uint32_t b = *(const uint16_t*)(k8 + r * 128 + 2 * lane);
+  const float s = ks[r];
+  *(uint32_t*)(kbf + r * 128 + 2 * lane) =
+      (uint32_t)f2bf(e4m3_value(b & 0xffu) * s) | (uint32_t)f2bf(e4m3_value(b >> 8) * s) << 16;
+}
+
 __global__ void __launch_bounds__(kRowThreads) qprep_kernel(const uint16_t* q, const float* w, int HI, uint8_t* q8,
                                                             float* wf) {
   const int r = blockIdx.x;
@@ -330,6 +363,24 @@ int dsv41_decode_appends(const void* kv_raw, const void* kv_norm, void* ring, lo
                Dk, pos, seq, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx, HI,
                (uint8_t*)q8, wf};
   decode_appends_kernel<<<dim3(B, q_idx ? 4 : 3), kRowThreads, 0, (hipStream_t)stream>>>(a);
+  DSV41_CHECK_LAUNCH();
+  return 0;
+}
+
+int dsv41_index_keys_encode(const void* kbf, long n_rows, void* k8, float* ks, void* stream) {
+  if (n_rows <= 0) return 0;
+  if (!kbf || !k8 || !ks) return (int)hipErrorInvalidValue;
+  index_keys_encode_kernel<<<(unsigned)((n_rows + 3) / 4), 256, 0, (hipStream_t)stream>>>((const uint16_t*)kbf, n_rows,
+                                                                                          (uint8_t*)k8, ks);
+  DSV41_CHECK_LAUNCH();
+  return 0;
+}
+
+int dsv41_index_keys_decode(const void* k8, const float* ks, long n_rows, void* kbf, void* stream) {
+  if (n_rows <= 0) return 0;
+  if (!kbf || !k8 || !ks) return (int)hipErrorInvalidValue;
+  index_keys_decode_kernel<<<(unsigned)((n_rows + 3) / 4), 256, 0, (hipStream_t)stream>>>((const uint8_t*)k8, ks,
+                                                                                          n_rows, (uint16_t*)kbf);
   DSV41_CHECK_LAUNCH();
   return 0;
 }

@@ -44,6 +44,8 @@ SIGNATURES = {
     "dsv41_rmsnorm": [_P, _P, _P, _L, _I, _F, _P],
     "dsv41_decode_select": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _I,
                             _I, _P, _P, _I, _F, _P, _P, _I, _P, _I, _I, _I, _P, _L, _P, _L, _P, _L, _P, _L, _P],
+    "dsv41_index_keys_encode": [_P, _L, _P, _P, _P],
+    "dsv41_index_keys_decode": [_P, _P, _L, _P, _P],
     "dsv41_fp8_gemm_workspace_bytes": [_I, _I, _I],
     "dsv41_fp8_gemm": [_P, _L, _P, _P, _I, _I, _I, _I, _I, _P, _L, _P, _P, _L, _P],
     "dsv41_compress_pool_decode": [_P, _P, _L, _P, _P, _L, _I, _P, _P, _I, _I, _I, _P, _F, _P, _L, _P, _P],

@@ -183,3 +183,29 @@ def decode_appends(kv_raw, kv_norm, ring, latent, ckv, k_raw, k_norm, kbf, k8, k
          ptr(q_idx.contiguous()) if q_idx is not None else None,
          ptr(w_idx.to(torch.bfloat16).contiguous()) if q_idx is not None else None,
          q_idx.shape[-2] if q_idx is not None else 0, ptr(q8), ptr(wf), B, stream(dev))
+
+
+def index_keys_to_e4m3(kbf16: torch.Tensor):
+    """Snapshot conversion (dsv41/engine.py:1072-1230 stores the cache tensors as they are): the reference's bf16
+    index-key table [..., 128] -> (e4m3 bytes as float8_e4m3fn [..., 128], fp32 per-row scale [...]), the encoding
+    of the key appends.  Exact for the FP4-grid rows the reference writes."""
+    dev = require_gpu(kbf16)
+    assert kbf16.shape[-1] == 128
+    x = kbf16.to(torch.bfloat16).contiguous()
+    n = x.numel() // 128
+    k8 = torch.empty(x.shape, dtype=torch.uint8, device=dev)
+    ks = torch.empty(x.shape[:-1], dtype=torch.float32, device=dev)
+    call("dsv41_index_keys_encode", ptr(x), n, ptr(k8), ptr(ks), stream(dev))
+    return k8.view(torch.float8_e4m3fn), ks
+
+
+def index_keys_to_bf16(k8: torch.Tensor, k_scale: torch.Tensor) -> torch.Tensor:
+    """The inverse: e4m3 table [..., 128] + per-row scales [...] -> the reference's bf16 table (e4m3 x scale)."""
+    dev = require_gpu(k8, k_scale)
+    assert k8.shape[-1] == 128 and tuple(k_scale.shape) == tuple(k8.shape[:-1])
+    k = k8.contiguous().view(torch.uint8)
+    s = k_scale.float().contiguous()
+    out = torch.empty(k.shape, dtype=torch.bfloat16, device=dev)
+    call("dsv41_index_keys_decode", ptr(k), ptr(s), k.numel() // 128, ptr(out), stream(dev))
+    return out
+

@@ -222,6 +222,13 @@ int dsv41_decode_appends(const void* kv_raw, const void* kv_norm, void* ring, lo
                          const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
                          const void* w_idx, int HI, void* q8, float* wf, int B, void* stream);
 
+/* Index-key table conversion for cache snapshots (dsv41/engine.py:1072-1230 copies the cache tensors as they are;
+ * the reference's index_k is bf16 [.., 128], this build's e4m3 + fp32 per-row power-of-two scale): encode rows of
+ * 128 bf16 (the key appends' encoding: scale 2^ceil(log2(amax / 448)), amax >= 1e-30, exponent >= -126) and decode
+ * (e4m3 x scale, rounded to bf16).  decode(encode(k)) == k for the FP4-grid rows the reference stores. */
+int dsv41_index_keys_encode(const void* kbf, long n_rows, void* k8, float* ks, void* stream);
+int dsv41_index_keys_decode(const void* k8, const float* ks, long n_rows, void* kbf, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ projections */
 
 /* Workspace bytes of dsv41_fp8_gemm for M rows, N columns, K (0 when no K split is planned).  Allocate it zeroed

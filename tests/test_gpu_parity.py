@@ -769,3 +769,24 @@ def test_fp8_gemm(M, N, K, gc):
     err = np.abs(got32 - want)
     assert (err <= 1e-5 * mag + 1e-30).all(), (err / (mag + 1e-30)).max()
     np.testing.assert_array_equal(got16, O.bf16(got32))
+
+
+def test_index_key_snapshot_conversion():
+    """Cache snapshots (dsv41/engine.py:1072-1230): the reference's bf16 index-key table -> e4m3 + per-row scale ==
+    the oracle's key encoding bit for bit, and back == the original table exactly for FP4-grid rows (the reference's
+    keys, dsv41/model.py:726); arbitrary bf16 rows round-trip to bf16(e4m3 x scale)."""
+    from dsv41_amd.cache import index_keys_to_bf16, index_keys_to_e4m3
+    r = rng(47)
+    grid = _fp4_rows(r, (3, 40, 128))
+    grid[0, 5] = 0.0  # an all-zero row
+    any_rows = O.bf16(r.standard_normal((2, 33, 128)).astype(np.float32) * np.float32(3e-3))
+    for tag, rows in (("fp4-grid", grid), ("arbitrary", any_rows)):
+        k8, ks = index_keys_to_e4m3(bf(rows))
+        q, s = O.key_encode_fp8(rows)
+        want8 = torch.from_numpy(q).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        np.testing.assert_array_equal(k8.view(torch.uint8).cpu().numpy(), want8, err_msg=tag)
+        np.testing.assert_array_equal(ks.cpu().numpy(), s[..., 0], err_msg=tag)
+        back = host(index_keys_to_bf16(k8, ks))
+        np.testing.assert_array_equal(back, O.bf16(q * s), err_msg=tag)
+        if tag == "fp4-grid":
+            np.testing.assert_array_equal(back, rows)
