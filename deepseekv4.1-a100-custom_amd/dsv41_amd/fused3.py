@@ -80,7 +80,7 @@ def topk_indices(score: torch.Tensor, k: int, cl: torch.Tensor) -> torch.Tensor:
 
 class DecodeSelector:
     """index_score + topk_indices of the graph decode (dsv41/decode.py:289-294) for a fixed (rows, n_pos, k).  With
-    e4m3 keys and a grid that fits (rows * ceil(n_sel / 512) <= 512 workgroups, n_sel <= 262144) both run in one
+    e4m3 keys and a grid that fits (rows * ceil(n_sel / 512) <= 512 workgroups, n_sel <= 65536) both run in one
     launch (dsv41_index_select); otherwise the score kernel builds a 4096-bin histogram of the score keys and the
     top-k follows from it (one workgroup per row up to 36864 positions, else a compaction pass plus a finalize).
     Holds the score buffer and the zero-initialised workspaces, which every call leaves ready for the next
@@ -89,7 +89,8 @@ class DecodeSelector:
     covers, dsv41/decode.py:176-181, 287); the one-launch path scores and selects positions < n_sel = min(n_pos,
     max_cl) only."""
 
-    def __init__(self, rows: int, n_pos: int, k: int, device, keep_scores: bool = False, max_cl: int | None = None):
+    def __init__(self, rows: int, n_pos: int, k: int, device, keep_scores: bool = False, max_cl: int | None = None,
+                 one_launch_max_chunks: int = 128):
         self.rows, self.n_pos, self.k = rows, n_pos, k
         self.n_sel = n_pos if max_cl is None else max(1, min(n_pos, int(max_cl)))
         nbytes = lib().dsv41_select_workspace_bytes(rows, n_pos)
@@ -99,7 +100,9 @@ class DecodeSelector:
         self.score = torch.empty(rows, ld, dtype=torch.float32, device=device)[:, :n_pos]
         self.out = torch.empty(rows, 1, k, dtype=torch.int32, device=device)
         ns = (self.n_sel + 511) // 512
-        self.one_launch = ns <= 512 and rows * ns <= 512
+        # one launch up to 128 chunks per row: every chunk's workgroup gathers all chunks' counts and candidate
+        # prefixes, so past that the multi-launch path is faster (C4, 512 chunks: 82 us one launch vs ~49 us)
+        self.one_launch = ns <= min(int(one_launch_max_chunks), 512) and rows * ns <= 512
         self.keep_scores = keep_scores
         if self.one_launch:
             self.fnbytes = lib().dsv41_index_select_workspace_bytes(rows, self.n_sel)

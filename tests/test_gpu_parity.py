@@ -467,8 +467,10 @@ def test_decode_selector_end_to_end(cls):
 
 @pytest.mark.parametrize("n,cl", [(262145, 262144), (200001, 150000)])
 def test_decode_selector_long_row(n, cl):
-    """One long row (C4 shape: up to 512 chunks of 512 positions) through the one-launch indexer: selection bit-exact
-    against the oracle on the kernel's own scores, scores within 1e-2 of the oracle, workspace reusable."""
+    """One long row (C4 shape: up to 512 chunks of 512 positions) through the one-launch indexer (forced: by default
+    rows past 128 chunks take the multi-launch path) and the multi-launch path: selection bit-exact against the
+    oracle on the kernel's own scores, the two paths identical, scores within 1e-2 of the oracle, workspace
+    reusable."""
     from dsv41_amd.fused3 import DecodeSelector
     from dsv41_amd.workloads import encode_e4m3_rows, fp4_round
     g = torch.Generator(device=DEV).manual_seed(17)
@@ -479,8 +481,8 @@ def test_decode_selector_long_row(n, cl):
     q = fp4_round(torch.randn(1, 1, H, 128, generator=g, device=DEV))
     w = (torch.randn(1, H, generator=g, device=DEV) * 0.01).to(torch.bfloat16)
     seq = i64([1])
-    sel = DecodeSelector(1, n, 2048, DEV, keep_scores=True, max_cl=n - 1)  # the last row is the spare row
-    assert sel.one_launch
+    sel = DecodeSelector(1, n, 2048, DEV, keep_scores=True, max_cl=n - 1, one_launch_max_chunks=512)
+    assert sel.one_launch  # (the last row is the spare row)
     for rep in range(2):
         print(f"[selector long row] n {n} cl {cl} call {rep}", flush=True)
         idx = sel(q, k8, w, seq, i64([cl]), k_scale=ks)
@@ -488,6 +490,9 @@ def test_decode_selector_long_row(n, cl):
         assert int(sel.fws[-4].item()) == 0, "row barrier wait gave up"
         sc = sel.score.cpu().numpy()
         np.testing.assert_array_equal(idx.cpu().numpy()[:, 0], O.topk_indices(sc, 2048, [cl]))
+    multi = DecodeSelector(1, n, 2048, DEV, max_cl=n - 1)
+    assert not multi.one_launch
+    np.testing.assert_array_equal(multi(q, k8, w, seq, i64([cl]), k_scale=ks).cpu().numpy(), idx.cpu().numpy())
     want = O.index_score(q.float().cpu().numpy(), k8.float().cpu().numpy(), w.float().cpu().numpy(), [1], [cl],
                          k_scale=ks.cpu().numpy())
     err = np.abs(sc[0, :cl] - want[0, :cl]).max() / np.abs(want[0, :cl]).max()
