@@ -31,7 +31,10 @@ constexpr int kIsThreads = 512;                // 8 waves: two per SIMD
 constexpr int kIsChunk = 512;                  // positions per workgroup
 constexpr int kIsKeysPerWave = kIsChunk / 8;   // 4 column tiles of 16 keys
 constexpr int kIsPer = kIsChunk / kIsThreads;  // positions per thread in the selection
-constexpr int kIsSpec = 16;                    // candidates per chunk read together with the counts
+// candidates per chunk read together with the counts: 16 up to 128 chunks per row, 1 beyond (every workgroup of a
+// row reads every chunk's prefix; a long row's threshold bin holds well under one candidate per chunk on average)
+template <int MAXC>
+constexpr int is_spec() { return MAXC <= 128 ? 16 : 1; }
 constexpr int kIsCand = 2048;                  // candidates staged in LDS (more: read from the workspace)
 constexpr int kIsMaxChunks = 512;              // chunks per row (rows up to 262144 positions)
 constexpr int kIsMaxWG = 512;                  // resident workgroups: 2 per CU
@@ -400,6 +403,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   // ---- D. counts of all chunks + speculative candidate prefixes, read until every count word carries this epoch
   // and every speculative candidate below its chunk's count carries this epoch's tag (row barrier and gather in one)
   DSV41_PH(4);
+  constexpr int kIsSpec = is_spec<MAXC>();
   constexpr int kSpecPer = MAXC * kIsSpec / kIsThreads;
   unsigned long long sv[kSpecPer];
   {
@@ -486,11 +490,20 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     const int id = u * kIsThreads + t, q = id / kIsSpec, e = id % kIsSpec;
     if (staged && q < ns && e < nc_q[q]) lc[pc[q] + e] = sv[u];
   }
-  if (staged && s_over) {  // chunks with more than kIsSpec candidates
+  if (staged && s_over) {  // chunks with more than kIsSpec candidates: the rest, one candidate per thread
 #pragma unroll 1
-    for (int q = 0; q < ns; ++q)
-      for (int e = kIsSpec + t; e < nc_q[q]; e += kIsThreads)
-        lc[pc[q] + e] = __hip_atomic_load(crow + q * kIsChunk + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = t; i < m; i += kIsThreads) {
+      int lo = 0, hi = ns;  // the chunk q with pc[q] <= i < pc[q + 1]: the largest q with pc[q] <= i
+#pragma unroll 1
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pc[mid] <= i) lo = mid;
+        else hi = mid;
+      }
+      const int e = i - pc[lo];
+      if (e >= kIsSpec)
+        lc[i] = __hip_atomic_load(crow + lo * kIsChunk + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __syncthreads();
   auto cand_at = [&](int i) -> unsigned long long {
