@@ -1543,8 +1543,9 @@ void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
   *nsplit = (tiles + per - 1) / per;
 }
 
-// The decode kernel merges its own splits (XCD-local units) when there are enough units to occupy every XCD.
-bool fuse_merge(int R, int H, int ns) { return ns > 1 && ns <= kFuseMaxSplits && (long)R * ((H + 15) / 16) >= kXcds; }
+// The decode kernel merges its own splits (XCD-local units): cooperatively when every workgroup is resident at
+// once, else by the last arrival of each unit (any unit count; with fewer units than XCDs some XCDs idle).
+bool fuse_merge(int R, int H, int ns) { (void)R; (void)H; return ns > 1 && ns <= kFuseMaxSplits; }
 
 // Decode-kernel workspace: the split arrival counters first (their size depends on R and H only, so calls with any
 // split count find them where the previous call left them at rest), then m, l (fp32) and the bf16 partials.
