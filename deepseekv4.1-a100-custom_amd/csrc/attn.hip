@@ -1095,13 +1095,16 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
 
   const int W = a.n1;
   const int* irow = a.t > 0 ? a.idx + (long)r * a.idx_rstride : nullptr;
-  const int L = a.L;
-  const int ntiles = (L + TILE - 1) / TILE;
+  // key split sp = blockIdx.x takes tiles [sp * T / ns, (sp + 1) * T / ns) of the row's T tiles (keys jb .. jend)
+  const int sp = blockIdx.x, all_tiles = (a.L + TILE - 1) / TILE;
+  const int tb = (int)((long)sp * all_tiles / a.nsplit), te = (int)((long)(sp + 1) * all_tiles / a.nsplit);
+  const int jb = tb * TILE, jend = min(a.L, te * TILE);
+  const int ntiles = te - tb;
   // wave 0 loads index entries for two tiles at a time (tile 2u + (lane >> 5), key lane & 31) ...
   auto load_ix2 = [&](int u) {
-    const int j = (2 * u + (lane >> 5)) * TILE + (lane & 31);
+    const int j = jb + (2 * u + (lane >> 5)) * TILE + (lane & 31);
     const int jj = a.mode == 1 ? j - W : j;
-    return wave == 0 && j < L && jj >= 0 && irow ? irow[jj] : -1;
+    return wave == 0 && j < jend && jj >= 0 && irow ? irow[jj] : -1;
   };
   long slot, pos = 0, pmax = 0, plim = 0;
   if (a.mode == 1) {
@@ -1117,9 +1120,9 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   // ... and the lanes holding tile ti (half ti & 1 of the wave) resolve its row pointers
   auto resolve = [&](int ti, int ix) {
     if (wave == 0 && (lane >> 5) == (ti & 1)) {
-      const int j = ti * TILE + (lane & 31);
+      const int j = jb + ti * TILE + (lane & 31);
       const uint16_t* p = nullptr;
-      if (j < L) {
+      if (j < jend) {
         if (a.mode == 1 && j < W) {
           int m = (int)(pmax - j) % W;
           m = m < 0 ? m + W : m;
@@ -1253,7 +1256,16 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
         float l = 0.0f;
 #pragma unroll
         for (int u = 0; u < 8; ++u) l += xmax[u >> 2][u & 3][hl];
-        hfac[hl] = 1.0f / (l + exp2f(a.sink[h < H ? h : H - 1] * kLog2e - m_ref[b]));
+        if (a.nsplit > 1) {  // split partial: normalised by its own sum; m (natural-log units) and l for the merge
+          hfac[hl] = l > 0.0f ? 1.0f / l : 0.0f;
+          if (h < H) {
+            const long pi = ((long)r * H + h) * a.nsplit + sp;
+            a.pm[pi] = m_ref[b] * 0.6931471805599453f;
+            a.pl[pi] = l;
+          }
+        } else {
+          hfac[hl] = 1.0f / (l + exp2f(a.sink[h < H ? h : H - 1] * kLog2e - m_ref[b]));
+        }
       }
     }
     __syncthreads();  // E3
@@ -1384,9 +1396,12 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
     if (h >= H) continue;
     const float f = hfac[hl];
     const float4 x0 = *(const float4*)(stg + hl * DV + c), x1 = *(const float4*)(stg + hl * DV + c + 4);
-    *(uint4*)(a.out + (long)r * a.out_rstride + (long)h * DV + c) =
-        make_uint4(pack_bf16x2(x0.x * f, x0.y * f), pack_bf16x2(x0.z * f, x0.w * f), pack_bf16x2(x1.x * f, x1.y * f),
-                   pack_bf16x2(x1.z * f, x1.w * f));
+    const uint4 v = make_uint4(pack_bf16x2(x0.x * f, x0.y * f), pack_bf16x2(x0.z * f, x0.w * f),
+                               pack_bf16x2(x1.x * f, x1.y * f), pack_bf16x2(x1.z * f, x1.w * f));
+    if (a.nsplit > 1)  // bf16 partial [R, H, nsplit, DV] (merged by attn_decode_combine_kernel)
+      *(uint4*)((uint16_t*)a.pacc + (((long)r * H + h) * a.nsplit + sp) * DV + c) = v;
+    else
+      *(uint4*)(a.out + (long)r * a.out_rstride + (long)h * DV + c) = v;
   }
 }
 
@@ -1455,9 +1470,13 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const AttnArgs
   }
 }
 
-// Kernel choice: few (row, 64-head) pairs -> decode kernel (16-head workgroups, key splits, bf16 partials);
-// otherwise the 64-head kernel with one split per row when there are enough rows to fill the chip.
-bool use_decode_kernel(int R, int H) { return (long)R * ((H + 63) / 64) < 128; }
+// Kernel choice: few (row, 64-head) pairs -> decode kernel (16-head workgroups, key splits merged in the launch);
+// otherwise the 64-head kernel, with key splits (bf16 partials + the combine kernel) when the rows alone do not
+// fill the chip.
+// Measured (one layer-step, 576/512, 64 heads, 2176 keys per row): 1 row (C4) decode kernel 18.5 us vs 64-head
+// kernel + splits 30.5 us; 4 rows (C2) 19.8 vs 32.5 us; 48 rows (C5) 85.2 vs 57.3 us (the decode kernel's four
+// 16-head workgroups per row each gather every row: at many rows that redundancy dominates).
+bool use_decode_kernel(int R, int H) { return (long)R * ((H + 63) / 64) < 16; }
 
 template <int DQK, int DV>
 int launch_attn(AttnArgs& a, hipStream_t st) {
@@ -1472,9 +1491,13 @@ int launch_attn(AttnArgs& a, hipStream_t st) {
     return 0;
   }
   dim3 grid(a.nsplit, (a.H + 63) / 64, a.R);
-  if (a.nsplit == 1 && a.rd == 0) {  // (rows padded to a multiple of 8: contiguous row ranges per XCD)
-    attn_prefill_ws_kernel<DQK, DV><<<dim3(1, grid.y, (a.R + kXcds - 1) / kXcds * kXcds), 512, 0, st>>>(a);
+  if (a.rd == 0) {  // (rows padded to a multiple of 8: contiguous row ranges per XCD)
+    attn_prefill_ws_kernel<DQK, DV><<<dim3(a.nsplit, grid.y, (a.R + kXcds - 1) / kXcds * kXcds), 512, 0, st>>>(a);
     DSV41_CHECK_LAUNCH();
+    if (a.nsplit > 1) {  // bf16 partials merged with the sink
+      attn_decode_combine_kernel<DV><<<dim3((a.H + 3) / 4, a.R), 256, 0, st>>>(a);
+      DSV41_CHECK_LAUNCH();
+    }
     return 0;
   }
   attn_split_kernel<DQK, DV><<<grid, 256, 0, st>>>(a);
@@ -1522,8 +1545,7 @@ void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
     per = (tiles + want - 1) / want;
   } else if (dec) {
     // <= 192 workgroups (three quarters of the CUs; each holds one), >= 2 tiles per split; the decode kernel balances
-    // the tiles over the splits.  Measured at C2 (16 units, cooperative merge): 12 splits 19.5 us, 16 splits 20.2 us;
-    // at C5 (192 units): 1 split 39.7 us, 2 splits 49.1 us (a second round of workgroups).
+    // the tiles over the splits.  Measured at C2 (16 units, cooperative merge): 12 splits 19.5 us, 16 splits 20.2 us.
     const long wgs = (long)R * ((H + 15) / 16);
     const int cap = tiles / 2 < 1 ? 1 : tiles / 2;
     int ns = (int)(wgs >= 192 ? 1 : 192 / wgs);
