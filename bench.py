@@ -479,7 +479,7 @@ def main():
                    "cache_copies": args.layers},
         "hbm_roofline_pct": round(100.0 * frac_step, 2),
         "algorithmic_bytes_per_step": alg,
-        "kernel_us": {k: round(v, 3) for k, v in ku.items()},
+        "eager_launch_us": {k: round(v, 3) for k, v in ku.items()},  # eager, one launch each, host gaps included
         "roofline": roof[dom],
         "roofline_other": {k: v for k, v in roof.items() if k != dom},
         "prefill": pre,

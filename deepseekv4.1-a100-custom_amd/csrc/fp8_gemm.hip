@@ -178,20 +178,117 @@ __global__ void __launch_bounds__(kGemmThreads) fp8_gemm_kernel(const GemmArgs a
   }
 }
 
+// Narrow variant for few rows and few columns (the decode GEMVs whose weights are too small to fill the chip with
+// 64-column tiles and no split exchange): a workgroup of 16 waves owns 16 columns over the whole K, wave v takes the
+// 64-k windows v, v + 16, ...  Lane (l16, g) loads, per window, its 16 weight bytes and the 16 x elements of the same
+// 16-k group of row l16 (32 contiguous bytes, put into the weights' byte order in registers), all of a batch in
+// flight at once; the waves' partial sums meet in LDS (fixed order: deterministic).  Rows <= 16.
+constexpr int kNarrowWaves = 16;
+constexpr int kNarrowThreads = 64 * kNarrowWaves;
+constexpr int kNarrowU = 6;  // windows per lane per batch (6 x 52 bytes of loads in registers: no spill at 1024 threads)
+// Measured against the 64-column split kernel (M = 1 and 4, graph replay, weights past the last-level cache): narrow
+// wins for N = 1280 (7.6 vs 9.3 us at K 5120), 2048 and 4096 (8.2 vs 10.0 us at K 4096); it loses below 1024 columns
+// (N = 512, K 5120: 7.5 vs 7.2 us; too few workgroups) and from 5120 up (the split kernel's 64-column tiles)
+constexpr int kNarrowMinN = 1024, kNarrowMaxN = 4096;
+
+__global__ void __launch_bounds__(kNarrowThreads) fp8_gemv_narrow_kernel(const GemmArgs a) {
+  __shared__ f32x4_t red[kNarrowWaves][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int xr_off = a.group_cols > 0 ? n0 / a.group_cols : 0;
+  const int xr_mul = a.group_cols > 0 ? a.N / a.group_cols : 1;
+  const int n = n0 + l16;
+  const int nc = n < a.N ? n : a.N - 1;
+  const uint8_t* wrow = a.w8 + (long)nc * a.K + 16 * g;
+  const uint8_t* srow = a.s8 + (long)(nc >> 5) * a.Kc + (g >> 1);
+  const bool rv = l16 < a.M;
+  const uint16_t* xrow = a.x + (long)((a.m0 + (rv ? l16 : 0)) * xr_mul + xr_off) * a.ldx + 16 * g;
+  const int nwin = a.K / 64;
+  const int mine = nwin > wave ? (nwin - wave + kNarrowWaves - 1) / kNarrowWaves : 0;  // this wave's windows
+  uint4 wv[kNarrowU], x0[kNarrowU], x1[kNarrowU];
+  uint32_t sv[kNarrowU];
+  auto load_batch = [&](int j0) {
+#pragma unroll
+    for (int u = 0; u < kNarrowU; ++u) {
+      const int j = j0 + u < mine ? j0 + u : mine - 1;
+      const int w = wave + kNarrowWaves * j;
+      wv[u] = *(const uint4*)(wrow + 64 * w);
+      sv[u] = srow[2 * w];
+      if (rv) {
+        x0[u] = *(const uint4*)(xrow + 64 * w);
+        x1[u] = *(const uint4*)(xrow + 64 * w + 8);
+      }
+    }
+  };
+  if (mine > 0) load_batch(0);
+  f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+  for (int j0 = 0; j0 < mine; j0 += kNarrowU) {
+#pragma unroll
+    for (int u = 0; u < kNarrowU; ++u) {
+      if (j0 + u >= mine) break;
+      const float sc = e8m0_scale(sv[u]);
+      uint32_t b[8];
+      cvt4(wv[u].x, sc, b[0], b[1]);
+      cvt4(wv[u].y, sc, b[2], b[3]);
+      cvt4(wv[u].z, sc, b[4], b[5]);
+      cvt4(wv[u].w, sc, b[6], b[7]);
+      // x element pairs (2i, 2i + 1) of the group: x0 = pairs 0-3, x1 = pairs 4-7; byte order (kPermK) puts
+      // pairs 0 4 1 5 in the first half and 2 6 3 7 in the second
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      const uint4 a0 = rv ? make_uint4(x0[u].x, x1[u].x, x0[u].y, x1[u].y) : z;
+      const uint4 a1 = rv ? make_uint4(x0[u].z, x1[u].z, x0[u].w, x1[u].w) : z;
+      acc = mfma_bf16_16x16x32(a0, make_uint4(b[0], b[1], b[2], b[3]), acc);
+      acc = mfma_bf16_16x16x32(a1, make_uint4(b[4], b[5], b[6], b[7]), acc);
+    }
+    if (j0 + kNarrowU < mine) load_batch(j0 + kNarrowU);
+  }
+  red[wave][lane] = acc;  // lane (l16, g): out[4 g + i][n0 + l16]
+  __syncthreads();
+  if (tid < 256) {
+    const int ln = tid & 63, i = tid >> 6;
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kNarrowWaves; ++w) v += red[w][ln][i];
+    const int m = 4 * (ln >> 4) + i, cn = n0 + (ln & 15);
+    if (m < a.M && cn < a.N) {
+      const long o = (long)(a.m0 + m) * a.ldo + cn;
+      a.out[o] = f2bf(v);
+      if (a.outf) a.outf[o] = v;
+    }
+  }
+}
+
 // Plan: row tiles of up to 64 rows (MT = 1, 2, 4), K slices so that the grid holds >= 512 workgroups when K allows
 // (slices >= 256 k) and the staged x fits LDS.
 struct GemmPlan {
   int MT, splits, kslice, ctiles;
+  bool narrow;  // fp8_gemv_narrow_kernel: 16-column workgroups over the whole K, no split
 };
 
-GemmPlan gemm_plan(int M, int N, int K) {
+GemmPlan gemm_plan(int M, int N, int K, bool narrow_ok) {
   GemmPlan p{};
+  p.narrow = narrow_ok && M <= 16 && N >= kNarrowMinN && N <= kNarrowMaxN;
+#ifdef DSV41_GEMM_PROBE
+  if (const char* e = getenv("DSV41_GEMM_NARROW")) p.narrow = narrow_ok && M <= 16 && atoi(e);
+#endif
+  if (p.narrow) {
+    p.MT = 1;
+    p.ctiles = (N + 15) / 16;
+    p.splits = 1;
+    p.kslice = K;
+    return p;
+  }
   const int mrows = M < 64 ? M : 64;
   p.MT = mrows <= 16 ? 1 : mrows <= 32 ? 2 : 4;
   p.ctiles = (N + kGemmCols - 1) / kGemmCols;
   const int kmax = kGemmLdsBf16 / mrows / 64 * 64;  // staged elements per row
   int s = (K + kmax - 1) / kmax;
   while ((long)p.ctiles * s < 512 && K / (2 * s) >= 256) s *= 2;
+#ifdef DSV41_GEMM_PROBE
+  if (const char* e = getenv("DSV41_GEMM_S")) s = atoi(e);
+#endif
   int ks = (K + s - 1) / s;
   ks = (ks + 63) / 64 * 64;
   p.kslice = ks;
@@ -205,7 +302,7 @@ extern "C" {
 
 long dsv41_fp8_gemm_workspace_bytes(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  const GemmPlan p = gemm_plan(M, N, K);
+  const GemmPlan p = gemm_plan(M, N, K, false);  // the largest need: the narrow kernel uses none
   if (p.splits == 1) return 0;
   return (long)p.ctiles * 4 + 12 + (long)p.splits * 16 * p.MT * N * 4;  // counters, pad, partials
 }
@@ -217,7 +314,8 @@ int dsv41_fp8_gemm(const void* x, long ldx, const void* w8, const void* s8, int 
       ((uintptr_t)x & 3) != 0 || ((uintptr_t)w8 & 15) != 0 ||
       (group_cols > 0 && (group_cols % kGemmCols != 0 || N % group_cols != 0)) || group_cols < 0)
     return (int)hipErrorInvalidValue;
-  const GemmPlan p = gemm_plan(M, N, K);
+  // the narrow kernel loads x in 16-byte units
+  const GemmPlan p = gemm_plan(M, N, K, ((uintptr_t)x & 15) == 0 && ldx % 8 == 0);
   if (p.splits > 1 && (!ws || ws_bytes < dsv41_fp8_gemm_workspace_bytes(M, N, K))) return (int)hipErrorInvalidValue;
   GemmArgs a{};
   a.x = (const uint16_t*)x;
@@ -238,6 +336,13 @@ int dsv41_fp8_gemm(const void* x, long ldx, const void* w8, const void* s8, int 
     a.part = (float*)((char*)ws + ((long)p.ctiles * 4 + 15) / 16 * 16);
   }
   hipStream_t st = (hipStream_t)stream;
+  if (p.narrow) {
+    a.m0 = 0;
+    a.M = M;
+    fp8_gemv_narrow_kernel<<<p.ctiles, kNarrowThreads, 0, st>>>(a);
+    DSV41_CHECK_LAUNCH();
+    return 0;
+  }
   const dim3 grid(p.ctiles, p.splits);
   for (int m0 = 0; m0 < M; m0 += 16 * p.MT) {  // row tiles (more than 64 rows: the weights stream once per 64)
     a.m0 = m0;

@@ -745,8 +745,9 @@ def test_sparse_attn_two_sources_and_topk_view():
                "sparse_attn two sources")
 
 
-@pytest.mark.parametrize("M,N,K,gc", [(1, 1280, 5120, 0), (4, 512, 5120, 0), (1, 4096, 1280, 0), (16, 384, 2048, 0),
-                                      (20, 200, 640, 0), (70, 256, 1024, 0), (1, 2048, 1024, 256), (3, 1024, 512, 128)])
+@pytest.mark.parametrize("M,N,K,gc", [(1, 1280, 5120, 0), (4, 512, 5120, 0), (2, 200, 640, 0), (5, 16, 64, 0),
+                                      (1, 4096, 1280, 0), (16, 384, 2048, 0), (20, 200, 640, 0), (70, 256, 1024, 0),
+                                      (1, 2048, 1024, 256), (3, 1024, 512, 128), (16, 1040, 640, 0)])
 def test_fp8_gemm(M, N, K, gc):
     """fp8_gemm_tc / fp8_gemv_m1 (dsv41/cukern.py:116-200): fp32 result within fp32 summation-order error of the
     exact (float64) oracle, bf16 result its rounding; e4m3 codes over the whole range (subnormals included), E8M0
@@ -774,6 +775,11 @@ def test_fp8_gemm(M, N, K, gc):
     err = np.abs(got32 - want)
     assert (err <= 1e-5 * mag + 1e-30).all(), (err / (mag + 1e-30)).max()
     np.testing.assert_array_equal(got16, O.bf16(got32))
+    if M * G == 1:  # x only 4-byte aligned: the 64-column split kernel instead of the narrow one, same bound
+        xb = torch.zeros(K + 2, dtype=torch.bfloat16, device=DEV)
+        xb[2:] = bf(x)[0]
+        got_u = fp8_gemm_tc(xb[2:].view(1, K), w8, s8t, gc, out_dtype=torch.float32).cpu().numpy()
+        assert (np.abs(got_u - want) <= 1e-5 * mag + 1e-30).all()
 
 
 def test_index_key_snapshot_conversion():
