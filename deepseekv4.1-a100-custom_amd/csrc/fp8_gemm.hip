@@ -12,6 +12,9 @@
 // 16 columns x 32 k) pairs every weight with its x element.  Split K: each slice writes fp32 partials with
 // device-scope stores, and the last slice of a column tile to arrive (device-scope counter) sums them in slice order
 // (deterministic) and writes the output.
+// Few rows over small weights (the decode GEMVs) go to two kernels that need no split exchange: the narrow one
+// (16 columns, 16 waves over the whole K) and the vector one (a few columns per workgroup, fp32 VALU dot products);
+// the plan picks by rows and columns, from measurements.  All three are deterministic.
 #include "common.h"
 
 namespace {
@@ -186,8 +189,8 @@ __global__ void __launch_bounds__(kGemmThreads) fp8_gemm_kernel(const GemmArgs a
 constexpr int kNarrowWaves = 16;
 constexpr int kNarrowThreads = 64 * kNarrowWaves;
 constexpr int kNarrowU = 6;  // windows per lane per batch (6 x 52 bytes of loads in registers: no spill at 1024 threads)
-// Measured against the 64-column split kernel (M = 1 and 4, graph replay, weights past the last-level cache): narrow
-// wins for N = 1280 (7.6 vs 9.3 us at K 5120), 2048 and 4096 (8.2 vs 10.0 us at K 4096); it loses below 1024 columns
+// Measured against the 64-column split kernel (graph replay, weights past the last-level cache): narrow wins for
+// N = 1280 (7.6 vs 9.3 us at K 5120), 2048 and 4096 (8.2 vs 10.0 us at K 4096); it loses below 1024 columns
 // (N = 512, K 5120: 7.5 vs 7.2 us; too few workgroups) and from 5120 up (the split kernel's 64-column tiles)
 constexpr int kNarrowMinN = 1024, kNarrowMaxN = 4096;
 
@@ -260,11 +263,103 @@ __global__ void __launch_bounds__(kNarrowThreads) fp8_gemv_narrow_kernel(const G
   }
 }
 
+// Vector (no MFMA) variant for up to 4 rows: CPW columns per 256-thread workgroup, 256 / CPW threads per column,
+// thread t of a column takes the 16-k groups t, t + 256 / CPW, ... (every load of the thread in flight at once,
+// up to kVecG groups per batch): 16 weight bytes decoded to fp32 with the block scale (v_cvt_scalef32_pk_f32_fp8,
+// exact) against the group's 16 x elements, then the column's threads reduce (wave shuffles, then LDS; fixed
+// order).  Spreads a small weight over every CU: each workgroup streams CPW x K bytes.
+constexpr int kVecThreads = 256;
+constexpr int kVecG = 4;
+constexpr int kVecMaxM = 4;
+typedef float f32x2v_t __attribute__((ext_vector_type(2)));
+
+template <int CPW>
+__global__ void __launch_bounds__(kVecThreads) fp8_gemv_vec_kernel(const GemmArgs a) {
+  constexpr int TPC = kVecThreads / CPW;    // threads per column
+  constexpr int WPC = TPC >= 64 ? TPC / 64 : 1;  // waves per column (a wave holds 64 / TPC columns below 64)
+  constexpr int SH = TPC >= 64 ? 64 : TPC;  // lanes of one column inside a wave
+  __shared__ float red[CPW][WPC][kVecMaxM];
+  const int tid = threadIdx.x;
+  const int cl = tid / TPC, t = tid - cl * TPC;
+  const int n = blockIdx.x * CPW + cl;
+  const int nc = n < a.N ? n : a.N - 1;
+  const int xr_off = a.group_cols > 0 ? nc / a.group_cols : 0;
+  const int xr_mul = a.group_cols > 0 ? a.N / a.group_cols : 1;
+  const uint8_t* wrow = a.w8 + (long)nc * a.K;
+  const uint8_t* srow = a.s8 + (long)(nc >> 5) * a.Kc;
+  const uint16_t* xrow[kVecMaxM];
+#pragma unroll
+  for (int m = 0; m < kVecMaxM; ++m)
+    xrow[m] = a.x + (long)((a.m0 + (m < a.M ? m : 0)) * xr_mul + xr_off) * a.ldx;
+  const int ng = a.K / 16;
+  const int mine = ng > t ? (ng - t + TPC - 1) / TPC : 0;
+  float acc[kVecMaxM] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+  for (int j0 = 0; j0 < mine; j0 += kVecG) {
+    uint4 wv[kVecG], xv[kVecG][kVecMaxM][2];
+    uint32_t sv[kVecG];
+#pragma unroll
+    for (int u = 0; u < kVecG; ++u) {
+      const int j = j0 + u < mine ? j0 + u : mine - 1;
+      const int grp = t + TPC * j;
+      wv[u] = *(const uint4*)(wrow + 16 * grp);
+      sv[u] = srow[grp >> 1];
+#pragma unroll
+      for (int m = 0; m < kVecMaxM; ++m)
+        if (m < a.M) {
+          xv[u][m][0] = *(const uint4*)(xrow[m] + 16 * grp);
+          xv[u][m][1] = *(const uint4*)(xrow[m] + 16 * grp + 8);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kVecG; ++u) {
+      if (j0 + u >= mine) break;
+      const float sc = e8m0_scale(sv[u]);
+      // weight word i (bytes 4i .. 4i + 3) holds k = (2i, 2i + 1) and (2i + 8, 2i + 9) of the group
+      const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x2v_t lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(ww[i], sc, false);
+        const f32x2v_t hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(ww[i], sc, true);
+#pragma unroll
+        for (int m = 0; m < kVecMaxM; ++m) {
+          if (m >= a.M) break;
+          const uint32_t* xw0 = (const uint32_t*)&xv[u][m][0];
+          const uint32_t* xw1 = (const uint32_t*)&xv[u][m][1];
+          const uint32_t pl = xw0[i], ph = xw1[i];  // x pairs (2i, 2i + 1) and (2i + 8, 2i + 9)
+          acc[m] += lo.x * bf2f((uint16_t)pl) + lo.y * bf2f((uint16_t)(pl >> 16)) + hi.x * bf2f((uint16_t)ph) +
+                    hi.y * bf2f((uint16_t)(ph >> 16));
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kVecMaxM; ++m) {
+    float v = acc[m];
+#pragma unroll
+    for (int o = SH / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    acc[m] = v;
+  }
+  if ((t & (SH - 1)) == 0)
+#pragma unroll
+    for (int m = 0; m < kVecMaxM; ++m) red[cl][t / SH][m] = acc[m];
+  __syncthreads();
+  if (t < kVecMaxM && t < a.M && n < a.N) {
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WPC; ++w) v += red[cl][w][t];
+    const long o = (long)(a.m0 + t) * a.ldo + n;
+    a.out[o] = f2bf(v);
+    if (a.outf) a.outf[o] = v;
+  }
+}
+
 // Plan: row tiles of up to 64 rows (MT = 1, 2, 4), K slices so that the grid holds >= 512 workgroups when K allows
 // (slices >= 256 k) and the staged x fits LDS.
 struct GemmPlan {
   int MT, splits, kslice, ctiles;
   bool narrow;  // fp8_gemv_narrow_kernel: 16-column workgroups over the whole K, no split
+  int vec_cpw;  // > 0: fp8_gemv_vec_kernel with this many columns per workgroup
 };
 
 GemmPlan gemm_plan(int M, int N, int K, bool narrow_ok) {
@@ -273,6 +368,24 @@ GemmPlan gemm_plan(int M, int N, int K, bool narrow_ok) {
 #ifdef DSV41_GEMM_PROBE
   if (const char* e = getenv("DSV41_GEMM_NARROW")) p.narrow = narrow_ok && M <= 16 && atoi(e);
 #endif
+  // vector kernel (measured, graph replay, K 5120 / 4096): one row N <= 1024 two columns per workgroup (N = 512:
+  // 4.2 us; 64-column split 7.2), <= 2048 four (N = 1280: 6.3 us; narrow 7.6), <= 4096 eight (7.6; narrow 8.3);
+  // 2-4 rows N <= 1024 two (N = 512, 4 rows: 5.6 us; split 7.8), beyond that narrow (N = 1280, 4 rows: 8.8; vector 9.6)
+  p.vec_cpw = 0;
+  if (narrow_ok && M == 1) p.vec_cpw = N <= 1024 ? 2 : N <= 2048 ? 4 : N <= 4096 ? 8 : 0;
+  else if (narrow_ok && M <= kVecMaxM && N <= 1024) p.vec_cpw = 2;
+#ifdef DSV41_GEMM_PROBE
+  if (const char* e = getenv("DSV41_GEMM_VEC")) p.vec_cpw = narrow_ok && M <= kVecMaxM ? atoi(e) : 0;
+  if (p.vec_cpw != 0 && p.vec_cpw != 1 && p.vec_cpw != 2 && p.vec_cpw != 4 && p.vec_cpw != 8) p.vec_cpw = 0;
+#endif
+  if (p.vec_cpw) {
+    p.narrow = false;
+    p.MT = 1;
+    p.ctiles = (N + p.vec_cpw - 1) / p.vec_cpw;
+    p.splits = 1;
+    p.kslice = K;
+    return p;
+  }
   if (p.narrow) {
     p.MT = 1;
     p.ctiles = (N + 15) / 16;
@@ -336,6 +449,16 @@ int dsv41_fp8_gemm(const void* x, long ldx, const void* w8, const void* s8, int 
     a.part = (float*)((char*)ws + ((long)p.ctiles * 4 + 15) / 16 * 16);
   }
   hipStream_t st = (hipStream_t)stream;
+  if (p.vec_cpw) {
+    a.m0 = 0;
+    a.M = M;
+    if (p.vec_cpw == 1) fp8_gemv_vec_kernel<1><<<p.ctiles, kVecThreads, 0, st>>>(a);
+    else if (p.vec_cpw == 2) fp8_gemv_vec_kernel<2><<<p.ctiles, kVecThreads, 0, st>>>(a);
+    else if (p.vec_cpw == 4) fp8_gemv_vec_kernel<4><<<p.ctiles, kVecThreads, 0, st>>>(a);
+    else fp8_gemv_vec_kernel<8><<<p.ctiles, kVecThreads, 0, st>>>(a);
+    DSV41_CHECK_LAUNCH();
+    return 0;
+  }
   if (p.narrow) {
     a.m0 = 0;
     a.M = M;

@@ -747,11 +747,13 @@ def test_sparse_attn_two_sources_and_topk_view():
 
 @pytest.mark.parametrize("M,N,K,gc", [(1, 1280, 5120, 0), (4, 512, 5120, 0), (2, 200, 640, 0), (5, 16, 64, 0),
                                       (1, 4096, 1280, 0), (16, 384, 2048, 0), (20, 200, 640, 0), (70, 256, 1024, 0),
-                                      (1, 2048, 1024, 256), (3, 1024, 512, 128), (16, 1040, 640, 0)])
+                                      (1, 2048, 1024, 256), (3, 1024, 512, 128), (16, 1040, 640, 0), (1, 3000, 640, 0),
+                                      (1, 100, 2048, 0), (4, 700, 1024, 0), (1, 1024, 256, 128)])
 def test_fp8_gemm(M, N, K, gc):
     """fp8_gemm_tc / fp8_gemv_m1 (dsv41/cukern.py:116-200): fp32 result within fp32 summation-order error of the
     exact (float64) oracle, bf16 result its rounding; e4m3 codes over the whole range (subnormals included), E8M0
-    scales incl. the smallest, column tails (N % 64 != 0), split K, more than 64 rows, block-diagonal."""
+    scales incl. the smallest, column tails (N % 64 != 0), split K, more than 64 rows, block-diagonal; the narrow
+    (16-column) and vector (1-4 rows) kernels and, for one row, the split kernel on a 4-byte aligned x."""
     from dsv41_amd.w8 import fp8_gemm_tc
     r = rng(43)
     codes = r.integers(0, 256, (N, K)).astype(np.uint8)
