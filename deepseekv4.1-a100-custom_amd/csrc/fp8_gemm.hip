@@ -365,19 +365,12 @@ struct GemmPlan {
 GemmPlan gemm_plan(int M, int N, int K, bool narrow_ok) {
   GemmPlan p{};
   p.narrow = narrow_ok && M <= 16 && N >= kNarrowMinN && N <= kNarrowMaxN;
-#ifdef DSV41_GEMM_PROBE
-  if (const char* e = getenv("DSV41_GEMM_NARROW")) p.narrow = narrow_ok && M <= 16 && atoi(e);
-#endif
   // vector kernel (measured, graph replay, K 5120 / 4096): one row N <= 1024 two columns per workgroup (N = 512:
   // 4.2 us; 64-column split 7.2), <= 2048 four (N = 1280: 6.3 us; narrow 7.6), <= 4096 eight (7.6; narrow 8.3);
   // 2-4 rows N <= 1024 two (N = 512, 4 rows: 5.6 us; split 7.8), beyond that narrow (N = 1280, 4 rows: 8.8; vector 9.6)
   p.vec_cpw = 0;
   if (narrow_ok && M == 1) p.vec_cpw = N <= 1024 ? 2 : N <= 2048 ? 4 : N <= 4096 ? 8 : 0;
   else if (narrow_ok && M <= kVecMaxM && N <= 1024) p.vec_cpw = 2;
-#ifdef DSV41_GEMM_PROBE
-  if (const char* e = getenv("DSV41_GEMM_VEC")) p.vec_cpw = narrow_ok && M <= kVecMaxM ? atoi(e) : 0;
-  if (p.vec_cpw != 0 && p.vec_cpw != 1 && p.vec_cpw != 2 && p.vec_cpw != 4 && p.vec_cpw != 8) p.vec_cpw = 0;
-#endif
   if (p.vec_cpw) {
     p.narrow = false;
     p.MT = 1;
@@ -399,9 +392,6 @@ GemmPlan gemm_plan(int M, int N, int K, bool narrow_ok) {
   const int kmax = kGemmLdsBf16 / mrows / 64 * 64;  // staged elements per row
   int s = (K + kmax - 1) / kmax;
   while ((long)p.ctiles * s < 512 && K / (2 * s) >= 256) s *= 2;
-#ifdef DSV41_GEMM_PROBE
-  if (const char* e = getenv("DSV41_GEMM_S")) s = atoi(e);
-#endif
   int ks = (K + s - 1) / s;
   ks = (ks + 63) / 64 * 64;
   p.kslice = ks;
