@@ -240,7 +240,9 @@ long dsv41_fp8_gemm_workspace_bytes(int M, int N, int K);
  * accumulation, bf16 out [M, ldo] (and fp32 out_f32 [M, ldo] when not null).  w8: e4m3 bits [N, K] with every 16-k
  * group in the PERM_K byte order; s8: E8M0 [ceil(N / 32), Kc], Kc >= K / 32.  row(m, n) = m, or with group_cols > 0
  * (block-diagonal, dsv41/w8.py oproj_a) m * (N / group_cols) + n / group_cols.  K % 64 == 0; group_cols % 64 == 0;
- * x 4-byte and w8 16-byte aligned.  The weights stream once per 64 rows of M. */
+ * x 4-byte and w8 16-byte aligned.  The weights stream once per 64 rows of M.  With x 16-byte aligned and ldx % 8 ==
+ * 0, up to 16 rows over 1024-4096 columns (up to 4 rows over at most 4096 columns) run without a K split (faster for
+ * the decode GEMVs; the workspace is then unused). */
 int dsv41_fp8_gemm(const void* x, long ldx, const void* w8, const void* s8, int M, int N, int K, int Kc,
                    int group_cols, void* out, long ldo, float* out_f32, void* ws, long ws_bytes, void* stream);
 
