@@ -54,8 +54,8 @@ def decode_bytes(cfg, idx_sets=None, fused=True):
     return per_kernel
 
 
-def survey_bytes(cfg):
-    """The per-step algorithmic byte count as the survey defines it (keys incl. scale, gathered rows, ring, q,
+def step_algorithmic_bytes(cfg):
+    """The per-step algorithmic byte count (keys incl. scale, gathered rows, ring, q,
     index q, output, idx write + read), used for the headline roofline fraction."""
     from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN
     tot = 0
@@ -456,7 +456,7 @@ def main():
                       "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                       "traffic": traffic, "algorithmic_bytes": kb[name], "kernel_us": round(us, 3)}
     dom = max(r["alone_us"], key=r["alone_us"].get)  # the kernel with the longest launch
-    alg = survey_bytes(cfg)
+    alg = step_algorithmic_bytes(cfg)
     frac_step = alg / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS
     pre = None if args.no_prefill else run_prefill(args, dev)
     proj = None if args.no_proj else run_projections(args, dev)
