@@ -276,6 +276,67 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_kernel(const uint16_t* x,
   row_op(o, red);
 }
 
+// rmsnorm + per-32 fp8 fake quantisation of rows of up to kNqMaxD elements (dsv41/fused2.py:251-272 norm_quant;
+// without a weight, the fake quantisation alone: dsv41/fused.py:83-84 fake_quant_fp8 on any row length).  Thread t
+// owns the 32-element groups t, t + 256: y = bf16(x * (1 / sqrt(mean(x^2) + eps)) * w), then e4m3 on the group's
+// power-of-two scale, bf16 out.
+constexpr int kNqMaxD = 2 * kRowThreads * 32;
+
+__global__ void __launch_bounds__(kRowThreads) norm_quant_kernel(const uint16_t* x, const uint16_t* w, float eps,
+                                                                 uint16_t* y, int D) {
+  __shared__ float red[kRowThreads / 64];
+  const uint16_t* xr = x + (long)blockIdx.x * D;
+  uint16_t* yr = y + (long)blockIdx.x * D;
+  const int ng = D / 32;
+  float v[2][32];
+  float ss = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int grp = threadIdx.x + kRowThreads * q;
+    uint4 raw[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) raw[u] = grp < ng ? ((const uint4*)(xr + 32 * grp))[u] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t ww[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[q][8 * u + 2 * e] = __uint_as_float(ww[e] << 16);
+        v[q][8 * u + 2 * e + 1] = __uint_as_float(ww[e] & 0xffff0000u);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 32; ++e) ss += v[q][e] * v[q][e];
+  }
+  if (w) {
+    ss = block_sum<kRowThreads>(ss, red);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)D) + eps));
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int grp = threadIdx.x + kRowThreads * q;
+      if (grp >= ng) break;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) v[q][e] = round_bf16(v[q][e] * inv * bf2f(w[32 * grp + e]));
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int grp = threadIdx.x + kRowThreads * q;
+    if (grp >= ng) break;
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[q][e]));
+    const float sc = fq_scale(amax, 0);
+    uint32_t o[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      o[e] = (uint32_t)f2bf(fq_value(v[q][2 * e], sc, 0)) | ((uint32_t)f2bf(fq_value(v[q][2 * e + 1], sc, 0)) << 16);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      ((uint4*)(yr + 32 * grp))[u] = make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]);
+  }
+}
+
 // Row r of x ([n_rows, D], rows ordered (b, s, h)): position = base(b) + ((r / H) % S) * pos_stride, with
 // base(b) = pos[b] + add (device positions) or pos0 (host position).
 __global__ void __launch_bounds__(64) rope_kernel(uint16_t* __restrict__ x, const float* __restrict__ cos_t,
@@ -407,6 +468,16 @@ int dsv41_rope(void* x, const float* cos_t, const float* sin_t, const long* pos,
   if (rd <= 0 || rd % 2 != 0 || rd > D || rd / 2 > 64 || H <= 0 || S <= 0) return (int)hipErrorInvalidValue;
   rope_kernel<<<n_rows, 64, 0, (hipStream_t)stream>>>((uint16_t*)x, cos_t, sin_t, pos, pos0, add, pos_stride, H, S, D,
                                                       rd, inverse);
+  DSV41_CHECK_LAUNCH();
+  return 0;
+}
+
+int dsv41_norm_quant(const void* x, const void* w, float eps, void* y, long n_rows, int D, void* stream) {
+  if (n_rows <= 0) return 0;
+  if (D <= 0 || D % 32 != 0 || D > kNqMaxD || ((uintptr_t)x & 15) != 0 || ((uintptr_t)y & 15) != 0)
+    return (int)hipErrorInvalidValue;
+  norm_quant_kernel<<<n_rows, kRowThreads, 0, (hipStream_t)stream>>>((const uint16_t*)x, (const uint16_t*)w, eps,
+                                                                     (uint16_t*)y, D);
   DSV41_CHECK_LAUNCH();
   return 0;
 }

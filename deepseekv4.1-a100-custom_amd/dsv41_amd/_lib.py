@@ -42,6 +42,7 @@ SIGNATURES = {
     "dsv41_fake_quant": [_P, _P, _L, _I, _I, _I, _P],
     "dsv41_rope": [_P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P],
     "dsv41_rmsnorm": [_P, _P, _P, _L, _I, _F, _P],
+    "dsv41_norm_quant": [_P, _P, _F, _P, _L, _I, _P],
     "dsv41_decode_select": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _I,
                             _I, _P, _P, _I, _F, _P, _P, _I, _P, _I, _I, _I, _P, _L, _P, _L, _P, _L, _P, _L, _P],
     "dsv41_index_keys_encode": [_P, _L, _P, _P, _P],

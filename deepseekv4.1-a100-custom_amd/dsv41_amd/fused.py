@@ -40,6 +40,22 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     return y
 
 
+def norm_quant(x: torch.Tensor, w: torch.Tensor | None, eps: float) -> torch.Tensor:
+    """dsv41/fused2.py:264-272: rmsnorm of each bf16 row then the per-32 fp8 fake quantisation -> bf16, rows of up to
+    16384 (D % 32 == 0); w None: the fake quantisation alone (dsv41/fused.py:83-84 at any such row length)."""
+    dev = require_gpu(x) if w is None else require_gpu(x, w)
+    D = x.shape[-1]
+    xc = x.contiguous()
+    if xc.dtype != torch.bfloat16:
+        xc = xc.to(torch.bfloat16)
+    if xc.data_ptr() % 16:
+        xc = xc.clone()
+    y = torch.empty_like(xc)
+    wc = None if w is None else w.to(torch.bfloat16).contiguous()
+    call("dsv41_norm_quant", ptr(xc), ptr(wc), float(eps), ptr(y), xc.numel() // D, D, stream(dev))
+    return y
+
+
 def _rope_shape(x):
     if x.ndim == 3:
         b, s, d = x.shape

@@ -106,10 +106,11 @@ def fp8_gemv_m1(x: torch.Tensor, w8: torch.Tensor, s8: torch.Tensor, group_cols:
 def fp8_gemv_m1_pre(x_raw: torch.Tensor, w8: torch.Tensor, s8: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
                     mode: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """dsv41/cukern.py:137-158: the GEMV with its activation prologue: mode 1 = rmsnorm(x_raw) * norm_w then per-32
-    fp8 fake quant, mode 2 = fake quant only."""
-    from .fused import fake_quant_fp8, rmsnorm
-    x = x_raw.reshape(1, -1)
-    if mode == 1:
-        x = rmsnorm(x, norm_w, eps)
-    x = fake_quant_fp8(x, 32)
+    fp8 fake quant, mode 2 = fake quant only (one prologue launch, dsv41_norm_quant, then the GEMV)."""
+    from .fused import norm_quant
+    if mode not in (1, 2):
+        raise ValueError(f"fp8_gemv_m1_pre: mode {mode} (1: rmsnorm + fake quant, 2: fake quant)")
+    if mode == 1 and norm_w is None:
+        raise ValueError("fp8_gemv_m1_pre: mode 1 needs norm_w")
+    x = norm_quant(x_raw.reshape(1, -1), norm_w if mode == 1 else None, eps)
     return fp8_gemv_m1(x, w8, s8, 0, out)

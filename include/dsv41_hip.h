@@ -248,6 +248,11 @@ int dsv41_fp8_gemm(const void* x, long ldx, const void* w8, const void* s8, int 
 
 /* ------------------------------------------------------------------------------------------------ numerics */
 
+/* norm_quant (dsv41/fused2.py:251-272): per row of D bf16 values (D % 32 == 0, D <= 16384; x and y 16-byte aligned,
+ * rows contiguous) y = fake_quant_fp8(bf16(rmsnorm(x) * w), 32); with w null the fake quantisation alone
+ * (dsv41/fused.py:83-84 at any such D).  The activation prologue of fp8_gemv_m1_pre (dsv41/cukern.py:137-158). */
+int dsv41_norm_quant(const void* x, const void* w, float eps, void* y, long n_rows, int D, void* stream);
+
 /* fake_quant_fp8 / fake_quant_fp4 (dsv41/fused.py:46-87, dsv41/quant.py:45-87) on rows of D bf16 values. */
 int dsv41_fake_quant(const void* x, void* y, long n_rows, int D, int group, int mode, void* stream);
 

@@ -784,6 +784,43 @@ def test_fp8_gemm(M, N, K, gc):
         assert (np.abs(got_u - want) <= 1e-5 * mag + 1e-30).all()
 
 
+@pytest.mark.parametrize("mode,N,K", [(1, 1024, 1280), (2, 512, 8192), (1, 4096, 16384), (2, 300, 128), (1, 5120, 2048)])
+def test_fp8_gemv_m1_pre(mode, N, K):
+    """fp8_gemv_m1_pre (dsv41/cukern.py:137-158): its prologue (norm_quant, dsv41/fused2.py:251-272; mode 2 the
+    fake quantisation alone) equals the oracle's bf16(rmsnorm) -> fake_quant_fp8(32) -> bf16 bit for bit in mode 2
+    and up to the last ulp of the fp32 variance sum in mode 1 (at most 0.5 % of the elements, one e4m3 step each);
+    the result is the GEMV of that prologue, bit for bit, and within the fp8_gemm bound of the oracle's GEMV."""
+    from dsv41_amd.fused import norm_quant
+    from dsv41_amd.w8 import fp8_gemm_tc, fp8_gemv_m1_pre
+    r = rng(53)
+    codes = r.integers(0, 256, (N, K)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x01
+    s8 = r.integers(110, 130, ((N + 31) // 32, K // 32)).astype(np.uint8)
+    perm = codes.reshape(N, K // 16, 16)[:, :, O.PERM_K].reshape(N, K)
+    x = O.bf16(r.standard_normal((1, K)).astype(np.float32) * np.float32(3.0))
+    x[0, :32] *= np.float32(1e-3)  # a small-magnitude group
+    x = O.bf16(x)
+    w = O.bf16(1.0 + 0.1 * r.standard_normal(K).astype(np.float32))
+    eps = 1e-6
+    print(f"[fp8_gemv_m1_pre] mode {mode} N {N} K {K}", flush=True)
+    w8, s8t = torch.from_numpy(perm).to(DEV), torch.from_numpy(s8).to(DEV)
+    xq = host(norm_quant(bf(x), bf(w) if mode == 1 else None, eps))
+    y = O.bf16(O.rmsnorm(x, w, eps)) if mode == 1 else x
+    want_q = O.bf16(O.fake_quant_fp8(y, 32))
+    diff = xq != want_q
+    if mode == 2:
+        np.testing.assert_array_equal(xq, want_q)
+    else:
+        assert diff.mean() <= 5e-3, diff.mean()
+        step = np.abs(want_q[diff]) * np.float32(2.0 ** -3) + 1e-30
+        assert (np.abs(xq[diff] - want_q[diff]) <= step * 1.01).all()
+    got = host(fp8_gemv_m1_pre(bf(x), w8, s8t, bf(w) if mode == 1 else None, eps, mode))
+    np.testing.assert_array_equal(got, host(fp8_gemm_tc(bf(xq), w8, s8t)))
+    want = O.fp8_gemm(xq, perm, s8)
+    mag = np.abs(xq).astype(np.float64) @ np.abs(O.fp8_dequant(perm, s8).astype(np.float64)).T
+    assert (np.abs(got - want) <= 1e-5 * mag + np.abs(want) * 2.0 ** -8 + 1e-30).all()
+
+
 def test_index_key_snapshot_conversion():
     """Cache snapshots (dsv41/engine.py:1072-1230): the reference's bf16 index-key table -> e4m3 + per-row scale ==
     the oracle's key encoding bit for bit, and back == the original table exactly for FP4-grid rows (the reference's
