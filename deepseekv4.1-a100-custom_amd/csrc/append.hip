@@ -279,11 +279,11 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_kernel(const uint16_t* x,
 // rmsnorm + per-32 fp8 fake quantisation of rows of up to kNqMaxD elements (dsv41/fused2.py:251-272 norm_quant;
 // without a weight, the fake quantisation alone: dsv41/fused.py:83-84 fake_quant_fp8 on any row length).  Thread t
 // owns the 32-element groups t, t + 256: y = bf16(x * (1 / sqrt(mean(x^2) + eps)) * w), then e4m3 on the group's
-// power-of-two scale, bf16 out.
+// power-of-two scale, bf16 out.  quant = 0: the rmsnorm alone (dsv41_rmsnorm for rows past the row kernels' 1024).
 constexpr int kNqMaxD = 2 * kRowThreads * 32;
 
 __global__ void __launch_bounds__(kRowThreads) norm_quant_kernel(const uint16_t* x, const uint16_t* w, float eps,
-                                                                 uint16_t* y, int D) {
+                                                                 uint16_t* y, int D, int quant) {
   __shared__ float red[kRowThreads / 64];
   const uint16_t* xr = x + (long)blockIdx.x * D;
   uint16_t* yr = y + (long)blockIdx.x * D;
@@ -329,8 +329,11 @@ __global__ void __launch_bounds__(kRowThreads) norm_quant_kernel(const uint16_t*
     const float sc = fq_scale(amax, 0);
     uint32_t o[16];
 #pragma unroll
-    for (int e = 0; e < 16; ++e)
-      o[e] = (uint32_t)f2bf(fq_value(v[q][2 * e], sc, 0)) | ((uint32_t)f2bf(fq_value(v[q][2 * e + 1], sc, 0)) << 16);
+    for (int e = 0; e < 16; ++e) {
+      const float lo = quant ? fq_value(v[q][2 * e], sc, 0) : v[q][2 * e];
+      const float hi = quant ? fq_value(v[q][2 * e + 1], sc, 0) : v[q][2 * e + 1];
+      o[e] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       ((uint4*)(yr + 32 * grp))[u] = make_uint4(o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]);
@@ -477,13 +480,19 @@ int dsv41_norm_quant(const void* x, const void* w, float eps, void* y, long n_ro
   if (D <= 0 || D % 32 != 0 || D > kNqMaxD || ((uintptr_t)x & 15) != 0 || ((uintptr_t)y & 15) != 0)
     return (int)hipErrorInvalidValue;
   norm_quant_kernel<<<n_rows, kRowThreads, 0, (hipStream_t)stream>>>((const uint16_t*)x, (const uint16_t*)w, eps,
-                                                                     (uint16_t*)y, D);
+                                                                     (uint16_t*)y, D, 1);
   DSV41_CHECK_LAUNCH();
   return 0;
 }
 
 int dsv41_rmsnorm(const void* x, const void* w, void* y, long n_rows, int D, float eps, void* stream) {
   if (n_rows <= 0) return 0;
+  if (D > kRowMaxD && D % 32 == 0 && D <= kNqMaxD && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0 && w) {
+    norm_quant_kernel<<<n_rows, kRowThreads, 0, (hipStream_t)stream>>>((const uint16_t*)x, (const uint16_t*)w, eps,
+                                                                       (uint16_t*)y, D, 0);
+    DSV41_CHECK_LAUNCH();
+    return 0;
+  }
   if (!row_ok(D, 0)) return (int)hipErrorInvalidValue;
   rmsnorm_kernel<<<n_rows, kRowThreads, 0, (hipStream_t)stream>>>((const uint16_t*)x, (const uint16_t*)w, (uint16_t*)y,
                                                                   D, eps);

@@ -12,9 +12,11 @@ def fake_quant(x: torch.Tensor, group: int, mode: int) -> torch.Tensor:
     dev = require_gpu(x)
     if x.dtype != torch.bfloat16:
         raise RuntimeError("fake_quant: bf16 input expected")
+    D = x.shape[-1]
+    if mode == 0 and group == 32 and D > 1024:  # long rows (e.g. a hidden state): the norm_quant kernel, no norm
+        return norm_quant(x, None, 0.0)
     xc = x.contiguous()
     y = torch.empty_like(xc)
-    D = xc.shape[-1]
     call("dsv41_fake_quant", ptr(xc), ptr(y), xc.numel() // D, D, group, mode, stream(dev))
     return y
 

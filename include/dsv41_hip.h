@@ -261,7 +261,8 @@ int dsv41_fake_quant(const void* x, void* y, long n_rows, int D, int group, int 
 int dsv41_rope(void* x, const float* cos_t, const float* sin_t, const long* pos, long pos0, long add, long pos_stride,
                long n_rows, int H, int S, int D, int rd, int inverse, void* stream);
 
-/* rmsnorm (dsv41/fused.py:91-109): y = x / sqrt(mean(x^2) + eps) * w, bf16 rows. */
+/* rmsnorm (dsv41/fused.py:91-109): y = x / sqrt(mean(x^2) + eps) * w, bf16 rows of D <= 1024, or of D <= 16384 with
+ * D % 32 == 0 and x, y 16-byte aligned. */
 int dsv41_rmsnorm(const void* x, const void* w, void* y, long n_rows, int D, float eps, void* stream);
 
 #ifdef __cplusplus

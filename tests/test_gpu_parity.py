@@ -47,8 +47,6 @@ def rng(seed):
                                           (576, 32, 1)])
 def test_fake_quant(D, group, mode):
     import dsv41_amd
-    if D > 1024:
-        pytest.skip("rows wider than 1024 are outside the path")
     x = O.bf16(rng(1).standard_normal((37, D)).astype(np.float32) * 4)
     y = host(dsv41_amd.fake_quant(bf(x), group, mode))
     if mode == 0:
@@ -66,6 +64,10 @@ def test_rmsnorm_and_rope():
     y = host(dsv41_amd.rmsnorm(bf(x), bf(w), 1e-6))
     want = O.bf16(O.rmsnorm(x, w, 1e-6))
     np.testing.assert_allclose(y, want, rtol=8e-3, atol=1e-6)
+    xw = O.bf16(r.standard_normal((3, 5120)).astype(np.float32) * 4)  # a hidden-state row (past 1024 elements)
+    ww = O.bf16(r.standard_normal(5120).astype(np.float32))
+    np.testing.assert_allclose(host(dsv41_amd.rmsnorm(bf(xw), bf(ww), 1e-6)), O.bf16(O.rmsnorm(xw, ww, 1e-6)),
+                               rtol=8e-3, atol=1e-6)
     cos, sin = O.rope_tables(64, 4096, 65536, 160000.0, 16.0, 32, 1)
     cs, sn = f32(cos), f32(sin)
     q = O.bf16(r.standard_normal((1, 3, 64, 512)).astype(np.float32))
