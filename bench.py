@@ -308,6 +308,7 @@ def run_prefill(args, dev):
 # dim 5120, q rank 1280, 64 heads x 512, 8 output groups x rank 1024) and its isolated A100 times (us, M = 1).
 PROJ_SHAPES = [("wq_a", 1280, 5120, 0, 8.1), ("wq_b", 32768, 1280, 0, 33.4), ("wkv", 512, 5120, 0, 4.9),
                ("wo_a", 8192, 4096, 1024, None), ("wo_b", 5120, 8192, 0, 32.1)]
+PRE_MODES = {"wq_b": 1, "wo_b": 2}  # fp8_gemv_m1_pre uses (dsv41/cukern.py:137-158): q_norm before wq_b, quant before wo_b
 
 
 def run_projections(args, dev):
@@ -315,7 +316,7 @@ def run_projections(args, dev):
     in enough copies to exceed the 256 MB last-level cache, a graph of one launch per copy, replayed; algorithmic
     bytes = weights + scales + x + out."""
     import torch
-    from dsv41_amd.w8 import fp8_gemm_tc
+    from dsv41_amd.w8 import fp8_gemm_tc, fp8_gemv_m1_pre
     res = {}
     for name, N, K, gc, ref_us in PROJ_SHAPES:
         wbytes = N * K + ((N + 31) // 32) * (K // 32)
@@ -356,6 +357,33 @@ def run_projections(args, dev):
                                    "reference_a100_us": ref_us if M == 1 else None}
             log(f"[bench] fp8 projection {name} [{N} x {K}] M={M}: {us:.2f} us, {gbs:.0f} GB/s "
                 f"({100 * gbs / HBM_PEAK_GBS:.1f} % of 8 TB/s)")
+        if name in PRE_MODES:  # the reference's one-launch GEMV with its activation prologue, one row
+            mode = PRE_MODES[name]
+            xr = (torch.randn(1, K, device=dev) * 2.0).to(torch.bfloat16)
+            nw = (1.0 + 0.1 * torch.randn(K, device=dev)).to(torch.bfloat16)
+            s2 = torch.cuda.Stream(dev)
+            s2.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(s2):
+                for w, sc in ws:
+                    fp8_gemv_m1_pre(xr, w, sc, nw, 1e-6, mode)
+            torch.cuda.synchronize(dev)
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=s2):
+                for w, sc in ws:
+                    fp8_gemv_m1_pre(xr, w, sc, nw, 1e-6, mode)
+            gr.replay()
+            torch.cuda.synchronize(dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(5):
+                gr.replay()
+            e1.record()
+            torch.cuda.synchronize(dev)
+            us = e0.elapsed_time(e1) * 1000.0 / (5 * copies)
+            gbs = (wbytes + K * 2 + N * 2) / (us * 1e-6) / 1e9
+            res[f"{name}_pre{mode}_M1"] = {"N": N, "K": K, "us": round(us, 2), "GB_s": round(gbs, 1),
+                                           "hbm_frac": round(gbs / HBM_PEAK_GBS, 3)}
+            log(f"[bench] fp8_gemv_m1_pre mode {mode} {name}: {us:.2f} us")
         del ws
         torch.cuda.empty_cache()
     return res

@@ -16,12 +16,14 @@
 // (16 columns, 16 waves over the whole K) and the vector one (a few columns per workgroup, fp32 VALU dot products);
 // the plan picks by rows and columns, from measurements.  All three are deterministic.
 #include "common.h"
+#include "rowop.h"
 
 namespace {
 
 constexpr int kGemmThreads = 256;             // 4 waves, 16 columns each
 constexpr int kGemmCols = 64;                 // columns per workgroup
 constexpr int kGemmLdsBf16 = 32 * 1024;       // staged x elements at most (64 KB of dynamic LDS)
+constexpr int kPreMaxK = 2 * kGemmThreads * 32;  // prologue rows: two 32-element groups per thread
 constexpr int kPermK[16] = {0, 1, 8, 9, 2, 3, 10, 11, 4, 5, 12, 13, 6, 7, 14, 15};  // dsv41/w8.py:23
 
 typedef __bf16 bf16x2g_t __attribute__((ext_vector_type(2)));
@@ -39,6 +41,9 @@ struct GemmArgs {
   float* outf;        // optional fp32 copy [rows, ldo]
   float* part;        // [splits, 16 * MT, N] fp32 partials (splits > 1)
   int* cnt;           // [column tiles] arrival counters (zero between launches)
+  int pre;            // activation prologue on the one x row: 1 rmsnorm (norm_w, eps) + fp8 fake quant, 2 quant
+  const uint16_t* norm_w;
+  float eps;
 };
 
 DSV41_DEV float e8m0_scale(uint32_t s) { return s ? __uint_as_float(s << 23) : __uint_as_float(0x00400000u); }
@@ -49,7 +54,7 @@ DSV41_DEV void cvt4(uint32_t w, float sc, uint32_t& lo, uint32_t& hi) {
   hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, sc, true));
 }
 
-template <int MT>
+template <int MT, bool PRE = false>
 __global__ void __launch_bounds__(kGemmThreads) fp8_gemm_kernel(const GemmArgs a) {
   extern __shared__ __align__(16) uint16_t xs[];  // [M rows][kl] in weight byte order (dynamic: M x kslice)
   __shared__ int s_last;
@@ -83,7 +88,89 @@ __global__ void __launch_bounds__(kGemmThreads) fp8_gemm_kernel(const GemmArgs a
   load_batch(0, wv, sv);
 
   // ---- stage x[rows, k0..k1) into LDS in the weights' byte order (16-byte units: 8 elements = one half group)
-  {
+  if constexpr (PRE) {  // one row, the prologue applied while staging (the arithmetic of dsv41_norm_quant)
+    __shared__ float red[kGemmThreads / 64];
+    // 32 x values of global group grp, normalised (mode 1) and fake-quantised, into LDS at dst in the byte order
+    auto finish = [&](float (&v)[32], int grp, float inv, uint16_t* dst) {
+      if (a.pre == 1) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint4 w4 = ((const uint4*)(a.norm_w + 32 * grp))[q];
+          const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[8 * q + 2 * e] = round_bf16(v[8 * q + 2 * e] * inv * __uint_as_float(ww[e] << 16));
+            v[8 * q + 2 * e + 1] = round_bf16(v[8 * q + 2 * e + 1] * inv * __uint_as_float(ww[e] & 0xffff0000u));
+          }
+        }
+      }
+      float amax = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
+      const float sc = fq_scale(amax, 0);
+      const float rs = __fdiv_rn(1.0f, sc);  // sc is a power of two: x * rs == x / sc exactly
+      uint16_t b[32];
+#pragma unroll
+      for (int e = 0; e < 32; ++e) b[e] = f2bf(round_e4m3(fminf(fmaxf(v[e] * rs, -448.0f), 448.0f)) * sc);
+      uint32_t o[16];  // position p of each 16-k group holds k = kPermK[p]
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j2 = 0; j2 < 8; ++j2)
+          o[8 * h + j2] = (uint32_t)b[16 * h + kPermK[2 * j2]] | ((uint32_t)b[16 * h + kPermK[2 * j2 + 1]] << 16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) *(uint4*)(dst + 8 * q) = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+    };
+    auto load32 = [&](int grp, float (&v)[32]) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 r4 = ((const uint4*)(a.x + 32 * grp))[q];
+        const uint32_t ww[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[8 * q + 2 * e] = __uint_as_float(ww[e] << 16);
+          v[8 * q + 2 * e + 1] = __uint_as_float(ww[e] & 0xffff0000u);
+        }
+      }
+    };
+    const int ng = a.K / 32;
+    const bool whole = k0 == 0 && kl == a.K;  // the slice is the row: the groups loaded for the norm are staged
+    float v[2][32];
+    float inv = 1.0f;
+    if (a.pre == 1 || whole) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int grp = tid + kGemmThreads * q;
+        if (grp < ng) load32(grp, v[q]);
+        else
+#pragma unroll
+          for (int e = 0; e < 32; ++e) v[q][e] = 0.0f;
+      }
+    }
+    if (a.pre == 1) {  // whole-row sum of squares, in the order of the norm_quant kernel
+      float ss = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int e = 0; e < 32; ++e) ss += v[q][e] * v[q][e];
+      ss = block_sum<kGemmThreads>(ss, red);
+      inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)a.K) + a.eps));
+    }
+    if (whole) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int grp = tid + kGemmThreads * q;
+        if (grp < ng) finish(v[q], grp, inv, xs + 32 * grp);
+      }
+    } else {
+#pragma unroll 1
+      for (int u = tid; u < kl / 32; u += kGemmThreads) {
+        float w32[32];
+        load32(k0 / 32 + u, w32);
+        finish(w32, k0 / 32 + u, inv, xs + 32 * u);
+      }
+    }
+  } else {
     const int units = a.M * (kl / 8);
 #pragma unroll 1
     for (int u = tid; u < units; u += kGemmThreads) {
@@ -466,6 +553,40 @@ int dsv41_fp8_gemm(const void* x, long ldx, const void* w8, const void* s8, int 
     else fp8_gemm_kernel<4><<<grid, kGemmThreads, lds, st>>>(a);
     DSV41_CHECK_LAUNCH();
   }
+  return 0;
+}
+
+int dsv41_fp8_gemv_m1_pre(const void* x_raw, const void* norm_w, float eps, int mode, const void* w8, const void* s8,
+                          int N, int K, int Kc, void* out, void* ws, long ws_bytes, void* stream) {
+  if (N <= 0) return 0;
+  if ((mode != 1 && mode != 2) || (mode == 1 && !norm_w) || K <= 0 || K % 64 != 0 || K > kPreMaxK || Kc < K / 32 ||
+      !x_raw || !w8 || !s8 || !out || ((uintptr_t)x_raw & 15) != 0 || ((uintptr_t)w8 & 15) != 0 ||
+      (mode == 1 && ((uintptr_t)norm_w & 15) != 0))
+    return (int)hipErrorInvalidValue;
+  const GemmPlan p = gemm_plan(1, N, K, false);  // the 64-column kernel stages x: the prologue runs there
+  if (p.splits > 1 && (!ws || ws_bytes < dsv41_fp8_gemm_workspace_bytes(1, N, K))) return (int)hipErrorInvalidValue;
+  GemmArgs a{};
+  a.x = (const uint16_t*)x_raw;
+  a.ldx = K;
+  a.w8 = (const uint8_t*)w8;
+  a.s8 = (const uint8_t*)s8;
+  a.M = 1;
+  a.N = N;
+  a.K = K;
+  a.Kc = Kc;
+  a.splits = p.splits;
+  a.kslice = p.kslice;
+  a.out = (uint16_t*)out;
+  a.ldo = N;
+  a.pre = mode;
+  a.norm_w = (const uint16_t*)norm_w;
+  a.eps = eps;
+  if (p.splits > 1) {
+    a.cnt = (int*)ws;
+    a.part = (float*)((char*)ws + ((long)p.ctiles * 4 + 15) / 16 * 16);
+  }
+  fp8_gemm_kernel<1, true><<<dim3(p.ctiles, p.splits), kGemmThreads, (size_t)p.kslice * 2, (hipStream_t)stream>>>(a);
+  DSV41_CHECK_LAUNCH();
   return 0;
 }
 

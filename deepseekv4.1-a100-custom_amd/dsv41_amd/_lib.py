@@ -48,6 +48,7 @@ SIGNATURES = {
     "dsv41_index_keys_encode": [_P, _L, _P, _P, _P],
     "dsv41_index_keys_decode": [_P, _P, _L, _P, _P],
     "dsv41_fp8_gemm_workspace_bytes": [_I, _I, _I],
+    "dsv41_fp8_gemv_m1_pre": [_P, _P, _F, _I, _P, _P, _I, _I, _I, _P, _P, _L, _P],
     "dsv41_fp8_gemm": [_P, _L, _P, _P, _I, _I, _I, _I, _I, _P, _L, _P, _P, _L, _P],
     "dsv41_compress_pool_decode": [_P, _P, _L, _P, _P, _L, _I, _P, _P, _I, _I, _I, _P, _F, _P, _L, _P, _P],
     "dsv41_compress_pool_prefill": [_P, _P, _L, _P, _P, _I, _L, _I, _I, _I, _P, _F, _P, _L, _I, _P],

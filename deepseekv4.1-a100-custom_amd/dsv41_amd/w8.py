@@ -106,11 +106,30 @@ def fp8_gemv_m1(x: torch.Tensor, w8: torch.Tensor, s8: torch.Tensor, group_cols:
 def fp8_gemv_m1_pre(x_raw: torch.Tensor, w8: torch.Tensor, s8: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
                     mode: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """dsv41/cukern.py:137-158: the GEMV with its activation prologue: mode 1 = rmsnorm(x_raw) * norm_w then per-32
-    fp8 fake quant, mode 2 = fake quant only (one prologue launch, dsv41_norm_quant, then the GEMV)."""
-    from .fused import norm_quant
+    fp8 fake quant, mode 2 = fake quant only; one launch (the prologue is applied while the x row is staged)."""
     if mode not in (1, 2):
         raise ValueError(f"fp8_gemv_m1_pre: mode {mode} (1: rmsnorm + fake quant, 2: fake quant)")
     if mode == 1 and norm_w is None:
         raise ValueError("fp8_gemv_m1_pre: mode 1 needs norm_w")
-    x = norm_quant(x_raw.reshape(1, -1), norm_w if mode == 1 else None, eps)
-    return fp8_gemv_m1(x, w8, s8, 0, out)
+    dev = require_gpu(x_raw, w8, s8)
+    K = x_raw.shape[-1]
+    N = w8.shape[0]
+    xc = x_raw.reshape(-1).contiguous()
+    if xc.dtype != torch.bfloat16:
+        xc = xc.to(torch.bfloat16)
+    if xc.data_ptr() % 16:
+        xc = xc.clone()
+    assert xc.numel() == K and w8.dtype == torch.uint8 and w8.is_contiguous() and s8.is_contiguous()
+    wn = None
+    if mode == 1:
+        wn = norm_w.to(torch.bfloat16).contiguous()
+        if wn.data_ptr() % 16:
+            wn = wn.clone()
+    direct = out is not None and out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == N
+    y = out if direct else torch.empty(1, N, device=dev, dtype=torch.bfloat16)
+    ws, n = _workspace(dev, 1, N, K)
+    call("dsv41_fp8_gemv_m1_pre", ptr(xc), ptr(wn), float(eps), int(mode), ptr(w8), ptr(s8), N, K, s8.shape[1],
+         ptr(y), ptr(ws), n, stream(dev))
+    if out is not None and not direct:
+        out.copy_(y.view_as(out))
+    return out if out is not None else y

@@ -246,6 +246,14 @@ long dsv41_fp8_gemm_workspace_bytes(int M, int N, int K);
 int dsv41_fp8_gemm(const void* x, long ldx, const void* w8, const void* s8, int M, int N, int K, int Kc,
                    int group_cols, void* out, long ldo, float* out_f32, void* ws, long ws_bytes, void* stream);
 
+/* fp8_gemv_m1_pre (dsv41/cukern.py:137-158): one launch, the activation prologue fused into the x staging of the
+ * 64-column kernel: x = fake_quant_fp8(bf16(rmsnorm(x_raw) * norm_w), 32) (mode 1) or fake_quant_fp8(x_raw, 32)
+ * (mode 2; norm_w unused), then out[0, n] as dsv41_fp8_gemm for one row.  x_raw bf16 [K] and norm_w 16-byte
+ * aligned, K % 64 == 0, K <= 16384; the same results as dsv41_norm_quant followed by dsv41_fp8_gemm on the 64-column
+ * kernel.  Workspace: dsv41_fp8_gemm_workspace_bytes(1, N, K). */
+int dsv41_fp8_gemv_m1_pre(const void* x_raw, const void* norm_w, float eps, int mode, const void* w8, const void* s8,
+                          int N, int K, int Kc, void* out, void* ws, long ws_bytes, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ numerics */
 
 /* norm_quant (dsv41/fused2.py:251-272): per row of D bf16 values (D % 32 == 0, D <= 16384; x and y 16-byte aligned,

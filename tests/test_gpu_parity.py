@@ -791,7 +791,8 @@ def test_fp8_gemv_m1_pre(mode, N, K):
     """fp8_gemv_m1_pre (dsv41/cukern.py:137-158): its prologue (norm_quant, dsv41/fused2.py:251-272; mode 2 the
     fake quantisation alone) equals the oracle's bf16(rmsnorm) -> fake_quant_fp8(32) -> bf16 bit for bit in mode 2
     and up to the last ulp of the fp32 variance sum in mode 1 (at most 0.5 % of the elements, one e4m3 step each);
-    the result is the GEMV of that prologue, bit for bit, and within the fp8_gemm bound of the oracle's GEMV."""
+    the one-launch fp8_gemv_m1_pre (prologue fused into the x staging) equals norm_quant + fp8_gemm_tc bit for bit
+    and is within the fp8_gemm bound of the oracle's GEMV of that prologue."""
     from dsv41_amd.fused import norm_quant
     from dsv41_amd.w8 import fp8_gemm_tc, fp8_gemv_m1_pre
     r = rng(53)
@@ -817,7 +818,9 @@ def test_fp8_gemv_m1_pre(mode, N, K):
         step = np.abs(want_q[diff]) * np.float32(2.0 ** -3) + 1e-30
         assert (np.abs(xq[diff] - want_q[diff]) <= step * 1.01).all()
     got = host(fp8_gemv_m1_pre(bf(x), w8, s8t, bf(w) if mode == 1 else None, eps, mode))
-    np.testing.assert_array_equal(got, host(fp8_gemm_tc(bf(xq), w8, s8t)))
+    xb = torch.zeros(K + 2, dtype=torch.bfloat16, device=DEV)  # 4-byte aligned x: the same (64-column) kernel
+    xb[2:] = bf(xq)[0]
+    np.testing.assert_array_equal(got, host(fp8_gemm_tc(xb[2:].view(1, K), w8, s8t)))  # fused == two launches
     want = O.fp8_gemm(xq, perm, s8)
     mag = np.abs(xq).astype(np.float64) @ np.abs(O.fp8_dequant(perm, s8).astype(np.float64)).T
     assert (np.abs(got - want) <= 1e-5 * mag + np.abs(want) * 2.0 ** -8 + 1e-30).all()
