@@ -90,15 +90,19 @@ __global__ void __launch_bounds__(kGemmThreads) fp8_gemm_kernel(const GemmArgs a
   // ---- stage x[rows, k0..k1) into LDS in the weights' byte order (16-byte units: 8 elements = one half group)
   if constexpr (PRE) {  // one row, the prologue applied while staging (the arithmetic of dsv41_norm_quant)
     __shared__ float red[kGemmThreads / 64];
-    // 32 x values of global group grp, normalised (mode 1) and fake-quantised, into LDS at dst in the byte order
-    auto finish = [&](float (&v)[32], int grp, float inv, uint16_t* dst) {
-      if (a.pre == 1) {
+    // 32 x values (raw bf16 pairs) of one group, normalised with its norm weights (mode 1) and fake-quantised, into
+    // LDS at dst in the weights' byte order
+    auto finish = [&](const uint4 (&rx)[4], const uint4 (&rw)[4], float inv, uint16_t* dst) {
+      float v[32];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint4 w4 = ((const uint4*)(a.norm_w + 32 * grp))[q];
-          const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t xx[4] = {rx[q].x, rx[q].y, rx[q].z, rx[q].w};
+        const uint32_t ww[4] = {rw[q].x, rw[q].y, rw[q].z, rw[q].w};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < 4; ++e) {
+          v[8 * q + 2 * e] = __uint_as_float(xx[e] << 16);
+          v[8 * q + 2 * e + 1] = __uint_as_float(xx[e] & 0xffff0000u);
+          if (a.pre == 1) {
             v[8 * q + 2 * e] = round_bf16(v[8 * q + 2 * e] * inv * __uint_as_float(ww[e] << 16));
             v[8 * q + 2 * e + 1] = round_bf16(v[8 * q + 2 * e + 1] * inv * __uint_as_float(ww[e] & 0xffff0000u));
           }
@@ -121,30 +125,25 @@ __global__ void __launch_bounds__(kGemmThreads) fp8_gemm_kernel(const GemmArgs a
 #pragma unroll
       for (int q = 0; q < 4; ++q) *(uint4*)(dst + 8 * q) = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
     };
-    auto load32 = [&](int grp, float (&v)[32]) {
+    auto load_grp = [&](int grp, uint4 (&rx)[4], uint4 (&rw)[4]) {  // x and (mode 1) norm weights of a group
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const uint4 r4 = ((const uint4*)(a.x + 32 * grp))[q];
-        const uint32_t ww[4] = {r4.x, r4.y, r4.z, r4.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[8 * q + 2 * e] = __uint_as_float(ww[e] << 16);
-          v[8 * q + 2 * e + 1] = __uint_as_float(ww[e] & 0xffff0000u);
-        }
+        rx[q] = ((const uint4*)(a.x + 32 * grp))[q];
+        rw[q] = a.pre == 1 ? ((const uint4*)(a.norm_w + 32 * grp))[q] : make_uint4(0, 0, 0, 0);
       }
     };
     const int ng = a.K / 32;
     const bool whole = k0 == 0 && kl == a.K;  // the slice is the row: the groups loaded for the norm are staged
-    float v[2][32];
+    uint4 rx[2][4], rw[2][4];
     float inv = 1.0f;
     if (a.pre == 1 || whole) {
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int grp = tid + kGemmThreads * q;
-        if (grp < ng) load32(grp, v[q]);
+        if (grp < ng) load_grp(grp, rx[q], rw[q]);
         else
 #pragma unroll
-          for (int e = 0; e < 32; ++e) v[q][e] = 0.0f;
+          for (int e = 0; e < 4; ++e) rx[q][e] = rw[q][e] = make_uint4(0, 0, 0, 0);
       }
     }
     if (a.pre == 1) {  // whole-row sum of squares, in the order of the norm_quant kernel
@@ -152,7 +151,15 @@ __global__ void __launch_bounds__(kGemmThreads) fp8_gemm_kernel(const GemmArgs a
 #pragma unroll
       for (int q = 0; q < 2; ++q)
 #pragma unroll
-        for (int e = 0; e < 32; ++e) ss += v[q][e] * v[q][e];
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t xx[4] = {rx[q][u].x, rx[q][u].y, rx[q][u].z, rx[q][u].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float lo = __uint_as_float(xx[e] << 16), hi = __uint_as_float(xx[e] & 0xffff0000u);
+            ss += lo * lo;
+            ss += hi * hi;
+          }
+        }
       ss = block_sum<kGemmThreads>(ss, red);
       inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)a.K) + a.eps));
     }
@@ -160,14 +167,14 @@ __global__ void __launch_bounds__(kGemmThreads) fp8_gemm_kernel(const GemmArgs a
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int grp = tid + kGemmThreads * q;
-        if (grp < ng) finish(v[q], grp, inv, xs + 32 * grp);
+        if (grp < ng) finish(rx[q], rw[q], inv, xs + 32 * grp);
       }
     } else {
 #pragma unroll 1
       for (int u = tid; u < kl / 32; u += kGemmThreads) {
-        float w32[32];
-        load32(k0 / 32 + u, w32);
-        finish(w32, k0 / 32 + u, inv, xs + 32 * u);
+        uint4 gx[4], gw[4];
+        load_grp(k0 / 32 + u, gx, gw);
+        finish(gx, gw, inv, xs + 32 * u);
       }
     }
   } else {
