@@ -35,8 +35,10 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     """dsv41/fused.py:103-109 (bf16 rows, bf16 weight)."""
     dev = require_gpu(x, w)
     xc = x.contiguous()
-    y = torch.empty_like(xc)
     D = xc.shape[-1]
+    if D > 1024 and xc.data_ptr() % 16:  # long rows go through 16-byte loads
+        xc = xc.clone()
+    y = torch.empty_like(xc)
     call("dsv41_rmsnorm", ptr(xc), ptr(w.to(torch.bfloat16).contiguous()), ptr(y), xc.numel() // D, D, float(eps),
          stream(dev))
     return y
