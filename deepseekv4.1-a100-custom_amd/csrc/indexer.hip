@@ -16,8 +16,8 @@
 
 namespace {
 
-template <int KFMT, bool HIST>
-__global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a, int nx) {
+template <int KFMT, bool HIST, int WV = 4>
+__global__ void __launch_bounds__(64 * WV) index_score_kernel(const ScoreArgs a, int nx) {
   // 1-D grid: block b runs on XCD b % 8 (round-robin dispatch); key chunk x belongs to XCD x % 8 and its R rows
   // follow one another there, so rows of one sequence (MTP drafts) read the chunk's keys from that XCD's L2
   const int bxcd = blockIdx.x % kXcds, bj = blockIdx.x / kXcds;
@@ -31,11 +31,11 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a, int
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (HIST) {
 #pragma unroll 1
-    for (int i = threadIdx.x; i < kHistBins; i += 256) lhist[i] = 0;
+    for (int i = threadIdx.x; i < kHistBins; i += 64 * WV) lhist[i] = 0;
     __syncthreads();
   }
   const int l16 = lane & 15, g = lane >> 4;
-  const int kt0 = bx * kKeysPerWG + wave * kKeysPerWave;
+  const int kt0 = bx * (WV * kKeysPerWave) + wave * kKeysPerWave;
   long cl = row_cl(a, r);
   if (cl > a.n_pos) cl = a.n_pos;
   float* orow = a.out + (long)r * a.out_rstride;
@@ -128,7 +128,7 @@ __global__ void __launch_bounds__(256) index_score_kernel(const ScoreArgs a, int
     __syncthreads();
     int* gh = a.hist + (long)r * kHistBins;
 #pragma unroll 1
-    for (int i = threadIdx.x; i < kHistBins; i += 256) {
+    for (int i = threadIdx.x; i < kHistBins; i += 64 * WV) {
       const int v = lhist[i];
       if (v) atomicAdd(&gh[i], v);
     }
@@ -534,6 +534,17 @@ int launch_score(ScoreArgs& a, hipStream_t st) {
       case 3: index_score_prefill_kernel<3><<<dim3(split, qblocks), 256, 0, st>>>(a, split); break;
       default: index_score_prefill_kernel<4><<<dim3(split, qblocks), 256, 0, st>>>(a, split); break;
     }
+    DSV41_CHECK_LAUNCH();
+    return 0;
+  }
+  // A few long rows with a histogram: 16-wave workgroups (1024 keys each), so a quarter as many workgroups add
+  // their partial histograms to the row's with device-scope atomics (one 262144-key row: 22.7 -> 15.6 us; without
+  // the histogram 11.5 us).  Not for many rows: 48 draft rows of 65536 keys took 117 instead of 110 us.
+  const int nx16 = (a.n_pos + 16 * kKeysPerWave - 1) / (16 * kKeysPerWave);
+  if (a.hist && a.R <= 4 && (long)nx16 * a.R >= 256) {
+    const dim3 grid16((nx16 + kXcds - 1) / kXcds * kXcds * a.R);
+    if (a.kfmt == 1) index_score_kernel<1, true, 16><<<grid16, 1024, 0, st>>>(a, nx16);
+    else index_score_kernel<0, true, 16><<<grid16, 1024, 0, st>>>(a, nx16);
     DSV41_CHECK_LAUNCH();
     return 0;
   }
