@@ -127,10 +127,18 @@ __global__ void __launch_bounds__(64 * WV) index_score_kernel(const ScoreArgs a,
   if (HIST) {
     __syncthreads();
     int* gh = a.hist + (long)r * kHistBins;
+    if (((uintptr_t)gh & 7) == 0) {
 #pragma unroll 1
-    for (int i = threadIdx.x; i < kHistBins; i += 64 * WV) {
-      const int v = lhist[i];
-      if (v) atomicAdd(&gh[i], v);
+      for (int i = threadIdx.x; i < kHistBins / 2; i += 64 * WV) {  // bins in pairs: one 64-bit add (no carry
+        const uint32_t lo = (uint32_t)lhist[2 * i], hi = (uint32_t)lhist[2 * i + 1];  // out of a bin: < 2^32)
+        if (lo | hi) atomicAdd((unsigned long long*)(gh + 2 * i), ((unsigned long long)hi << 32) | lo);
+      }
+    } else {
+#pragma unroll 1
+      for (int i = threadIdx.x; i < kHistBins; i += 64 * WV) {
+        const int v = lhist[i];
+        if (v) atomicAdd(&gh[i], v);
+      }
     }
   }
   if (by == 0) DSV41_PH(4);
