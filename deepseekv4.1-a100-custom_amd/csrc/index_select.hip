@@ -306,9 +306,9 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     return;
   }
 #pragma unroll 1
-  for (int i = t; i < kHistBins; i += kIsThreads) {
-    const int v = lhist[i];
-    if (v) atomicAdd(&gh[i], v);
+  for (int i = t; i < kHistBins / 2; i += kIsThreads) {  // bins in pairs: one 64-bit add (no carry out of a bin)
+    const uint32_t lo = (uint32_t)lhist[2 * i], hi = (uint32_t)lhist[2 * i + 1];
+    if (lo | hi) atomicAdd((unsigned long long*)(gh + 2 * i), ((unsigned long long)hi << 32) | lo);
   }
   // ---- B. the row histogram once it holds all c valid positions (row barrier and data in one read), threshold bin
   DSV41_PH(2);
