@@ -51,6 +51,7 @@ struct AttnArgs {
   int* arrive;  // decode kernel: [R * head groups] split arrival counters (zero between launches), or null
   unsigned long long* coop;  // with arrive, when every workgroup is resident at once: [R * head groups] counters
                              // (launch epoch * 256 + arrivals), every split merges a slice; else null
+  int* err;     // with arrive: the workspace error word (set to 1 when a merge stopped waiting for its unit)
   int units;    // with arrive: (row, 16-head group) units, placed upx per XCD (1-D grid of kXcds * upx * nsplit)
   int upx;
   const float* cos_t;
@@ -776,6 +777,9 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
         while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < base + a.nsplit &&
                ++spins < kCoopSpinLimit)
           __builtin_amdgcn_s_sleep(1);
+        // gave up waiting (the unit's workgroups were not co-resident): the merge below may read unpublished
+        // partials, so the launch reports it through the workspace's error word
+        if (spins >= kCoopSpinLimit) __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
     __syncthreads();
@@ -1569,11 +1573,13 @@ void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
 // once, else by the last arrival of each unit (any unit count; with fewer units than XCDs some XCDs idle).
 bool fuse_merge(int R, int H, int ns) { (void)R; (void)H; return ns > 1 && ns <= kFuseMaxSplits; }
 
-// Decode-kernel workspace: the split arrival counters first (their size depends on R and H only, so calls with any
-// split count find them where the previous call left them at rest), then m, l (fp32) and the bf16 partials.
+// Decode-kernel workspace: the error word (int at byte 0: 1 = a cooperative merge stopped waiting for its unit),
+// then the split arrival counters from byte 256 (their size depends on R and H only, so calls with any split count
+// find them where the previous call left them at rest), then m, l (fp32) and the bf16 partials.
+constexpr long kCounterBase = 256;
 long counter_bytes(int R, int H) {
   const long units = (long)R * ((H + 15) / 16);
-  return (units * 4 + 8 + units * 8 + 255) / 256 * 256;  // int counters, pad, u64 counters
+  return kCounterBase + (units * 4 + 8 + units * 8 + 255) / 256 * 256;  // int counters, pad, u64 counters
 }
 
 long workspace_bytes(int R, int H, int ns, int dv) {
@@ -1598,11 +1604,12 @@ int finish_plan(AttnArgs& a, int want_nsplit, void* ws, long ws_bytes, int dv) {
     if (dec && fuse_merge(a.R, a.H, ns)) {
       a.units = a.R * ((a.H + 15) / 16);
       a.upx = (a.units + kXcds - 1) / kXcds;
-      a.arrive = (int*)ws;
+      a.err = (int*)ws;
+      a.arrive = (int*)((char*)ws + kCounterBase);
       // cooperative merge when every workgroup of the launch can be resident at once (one per CU, the XCDs dealt
       // round-robin): early arrivals wait for the rest of their unit
       if ((long)a.upx * ns <= cus_per_xcd())
-        a.coop = (unsigned long long*)((char*)ws + ((long)a.units * 4 + 7) / 8 * 8);
+        a.coop = (unsigned long long*)((char*)ws + kCounterBase + ((long)a.units * 4 + 7) / 8 * 8);
     }
   }
   return 0;

@@ -567,6 +567,7 @@ int select_setup(IsArgs& g, const void* q8, long q_rstride, const float* wf, lon
   if (n_pos <= 0 || HI <= 0 || HI > 64 || !cl || !kscale || ns > kIsMaxChunks || (long)R * ns > kIsMaxWG)
     return (int)hipErrorInvalidValue;
   if (!ws || ws_bytes < dsv41_index_select_workspace_bytes(R, n_pos)) return (int)hipErrorInvalidValue;
+  if (((uintptr_t)ws & 7) != 0) return (int)hipErrorInvalidValue;  // 64-bit histogram / count atomics
   ScoreArgs& a = g.s;
   a.q = (const uint16_t*)q8;
   a.q_rstride = q_rstride;

@@ -81,6 +81,33 @@ def call(name: str, *args) -> None:
         raise RuntimeError(f"{name}: hip error {rc}")
 
 
+# DSV41_CHECK_ERRORS=1: after launches whose kernels report through a workspace error word (the one-launch indexer's
+# row barriers, the decode attention's in-launch split merge), synchronise, read the word, clear it and raise when it
+# is set.  Off by default: it costs a host synchronisation per launch and is not legal under graph capture.
+CHECK_ERRORS = os.environ.get("DSV41_CHECK_ERRORS", "0") == "1"
+
+_ERR_TEXT = {("index_select", 1): "a row barrier wait gave up (the row's workgroups were not resident together)",
+             ("index_select", 2): "a valid count cl exceeded the positions scored (clamped)",
+             ("attention", 1): "a split merge stopped waiting for its unit (workgroups not resident together)"}
+
+
+def check_error_word(kind: str, word: torch.Tensor) -> None:
+    """Read the int32 error word `word` (a one-element view of a workspace), clear it and raise RuntimeError when it
+    is set.  Synchronises the word's device."""
+    v = int(word.item())
+    if v != 0:
+        word.zero_()
+        raise RuntimeError(f"{kind}: {_ERR_TEXT.get((kind, v), f'error word {v}')}")
+
+
+def attn_error_word(ws: torch.Tensor | None, R: int, H: int, nbytes: int):
+    """The error word of an attention workspace, or None when the launch has none (no split, or the 64-head kernel,
+    whose splits are merged by a separate launch).  The decode kernel runs when R * ceil(H / 64) < 16."""
+    if ws is None or nbytes <= 0 or R * ((H + 63) // 64) >= 16:
+        return None
+    return ws.view(torch.int32)[:1]
+
+
 def ptr(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 

@@ -82,14 +82,26 @@ class DecodeLayer:
         return sel
 
     def attn_workspace(self, B: int, h: int, L: int, device) -> torch.Tensor:
-        """Persistent zero-initialised attention workspace for B rows (split partials + arrival counters, which
-        every launch leaves at zero); allocate it before graph capture.  Calls sharing it must be stream-ordered."""
-        ws = self._attn_ws.get(B)
-        if ws is None:
-            from ._lib import lib
-            n = lib().dsv41_attn_workspace_bytes(B, h, L, self.dv, 0)
-            ws = self._attn_ws[B] = torch.zeros(max(n, 4) // 4, device=device, dtype=torch.float32)
+        """Persistent zero-initialised attention workspace for B rows x h heads over L key positions (split partials
+        + arrival counters, which every launch leaves at zero), reallocated when a wider index list needs more;
+        allocate it before graph capture.  Calls sharing it must be stream-ordered."""
+        from ._lib import lib
+        n = lib().dsv41_attn_workspace_bytes(B, h, L, self.dv, 0)
+        ws = self._attn_ws.get((B, h))
+        if ws is None or ws.numel() * 4 < n:
+            ws = self._attn_ws[(B, h)] = torch.zeros(max(n, 4) // 4, device=device, dtype=torch.float32)
         return ws
+
+    def check(self) -> None:
+        """Raise RuntimeError when a launch of this layer reported an error through a workspace error word (the
+        indexer's row barriers, the attention's in-launch split merge); clears the words.  Synchronises."""
+        from ._lib import attn_error_word, check_error_word
+        for sel in self._selectors.values():
+            sel.check()
+        for (B, h), ws in self._attn_ws.items():
+            w = attn_error_word(ws, B, h, ws.numel() * 4)
+            if w is not None:
+                check_error_word("attention", w)
 
     def attend(self, q, idx, pos, seq, pmax, plim=None):
         ws = self.attn_workspace(q.shape[0], q.shape[2], self.ring.shape[1] + idx.shape[-1], q.device)

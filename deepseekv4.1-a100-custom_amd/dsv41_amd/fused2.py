@@ -4,7 +4,8 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import as_i64, call, lib, ptr, require_gpu, stream
+from . import _lib
+from ._lib import as_i64, attn_error_word, call, check_error_word, lib, ptr, require_gpu, stream
 
 
 def kv_write(x: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor,
@@ -58,4 +59,6 @@ def sattn2(q, kv_win, kv_c, idx, pos, attn_sink, cos, sin, rd, softmax_scale, se
     call("dsv41_sattn2", ptr(qc), ptr(kv_win), kv_win.stride(0), win, ptr(kvc), c_stride, n_c, ptr(ix), t, ptr(pos),
          ptr(seq), ptr(pmax), ptr(plim), ptr(sink), ptr(cos), ptr(sin), int(rd), float(softmax_scale), ptr(o), b, h, d,
          dv, nsplit, ptr(ws), nbytes, stream(dev))
+    if _lib.CHECK_ERRORS and (w := attn_error_word(ws, b, h, nbytes)) is not None:
+        check_error_word("attention", w)
     return o

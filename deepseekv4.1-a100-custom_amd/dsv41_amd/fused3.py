@@ -4,7 +4,8 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import as_i64, call, lib, ptr, require_gpu, stream
+from . import _lib
+from ._lib import as_i64, call, check_error_word, lib, ptr, require_gpu, stream
 
 
 def qprep(q: torch.Tensor, weights: torch.Tensor):
@@ -120,7 +121,16 @@ class DecodeSelector:
         """Top-k from the buffered scores + histogram; leaves the histogram zeroed."""
         call("dsv41_select_topk", ptr(self.score), self.score.stride(0), self.rows, self.n_pos, self.k, ptr(cl), 0,
              ptr(self.ws), self.nbytes, ptr(self.out), self.k, stream(self.score.device))
+        if _lib.CHECK_ERRORS:
+            self.check()
         return self.out
+
+    def check(self) -> None:
+        """Raise RuntimeError (and clear the word) when the last launch reported an error through its workspace: a row
+        barrier that gave up, or a cl clamped to the positions scored.  Synchronises."""
+        check_error_word("index_select", self.ws[-4:-3])
+        if self.one_launch:
+            check_error_word("index_select", self.fws[-4:-3])
 
     def select_one_launch(self, q8, wf, H: int, index_k, k_scale, seq, cl, cand=None) -> torch.Tensor:
         """Scores + top-k in one launch from the prepared e4m3 queries (q8, wf)."""
@@ -130,6 +140,8 @@ class DecodeSelector:
              ptr(ks), ks.stride(0), ptr(seq), ptr(cl), self.n_sel, self.k, 0, ptr(self.fws), self.fnbytes,
              ptr(self.score) if self.keep_scores else None, self.score.stride(0), ptr(self.out), self.k, cp, cs,
              stream(self.score.device))
+        if _lib.CHECK_ERRORS:
+            self.check()
         return self.out
 
     def select_with_appends(self, app: dict, pos, seq, cl, cand=None) -> torch.Tensor:
@@ -160,6 +172,8 @@ class DecodeSelector:
              ptr(w_idx.to(torch.bfloat16).contiguous()), HI, ptr(cl), self.n_sel, self.k, 0, ptr(self.fws),
              self.fnbytes, ptr(self.score) if self.keep_scores else None, self.score.stride(0), ptr(self.out), self.k,
              cp, cs, stream(dev))
+        if _lib.CHECK_ERRORS:
+            self.check()
         return self.out
 
     def __call__(self, q, index_k, weights, seq, cl, k_scale=None, prepared=None, cand=None) -> torch.Tensor:

@@ -8,9 +8,9 @@ C5  ragged batched decode + speculative verify: 8 slots x 6 query rows.
 
 All values N(0,1)*0.1 from torch.Generator seeds (CPU, then copied to the device); index keys and index queries are
 FP4-rounded per 32 like the reference stores them (dsv41/model.py:726, :738) and carry a few x8 outlier channels;
-the index-key table is kept as e4m3 + per-row fp32 scale.  The reference geometry (head_dim 512 with in-row rope,
-32 index heads, ratio 2) is exercised by the parity tests; the BASELINE configs use absorbed-MLA rows (576 = 512
-latent + 64 rope, V = latent)."""
+the index-key table is kept as e4m3 + per-row fp32 scale.  The BASELINE configs use absorbed-MLA rows (576 = 512
+latent + 64 rope, V = latent), 64 index heads and ratio 4; the reference geometry (head_dim 512 with in-row rope,
+32 index heads, ratio 2, top-k 512) is built by the parity tests of tests/test_gpu_coverage.py themselves."""
 from __future__ import annotations
 
 from dataclasses import dataclass, field

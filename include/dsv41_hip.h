@@ -24,7 +24,9 @@ extern "C" {
  * a row).  want_nsplit <= 0 lets the library choose the split count; pass the same value to the launch.  The
  * workspace opens with split arrival counters (placed by R and H only): allocate it zeroed once per (R, H); every
  * launch leaves the counters ready for the next, whatever its split count (launches sharing it must be
- * stream-ordered). */
+ * stream-ordered).  Its first int32 is an error word: a decode-kernel launch whose in-launch split merge stopped
+ * waiting for the other workgroups of its unit (they were not resident at once) sets it to 1 -- that launch's
+ * output is then unreliable; the caller polls and clears it (the Python shims do with DSV41_CHECK_ERRORS=1). */
 long dsv41_attn_workspace_bytes(int R, int H, int L, int dv, int want_nsplit);
 
 /* kernels.sparse_attn (dsv41/kernels.py:172-256) and fused.sparse_attn_decode (dsv41/fused.py:269-280).
@@ -117,7 +119,8 @@ long dsv41_select_workspace_bytes(int R, int n);
 int dsv41_select_topk(const float* score, long ld, int R, int n, int k, const long* cl, int offset, void* ws,
                       long ws_bytes, int* out, long out_rstride, void* stream);
 
-/* Workspace of dsv41_index_select for R rows of n_pos positions.  Allocate it zeroed once per (R, n_pos): every
+/* Workspace of dsv41_index_select for R rows of n_pos positions (8-byte aligned: the histogram and count words take
+ * 64-bit atomics; a misaligned workspace is rejected).  Allocate it zeroed once per (R, n_pos): every
  * call leaves its histogram zeroed and its per-chunk count words (which carry the launch epoch) consistent for the
  * next call (calls sharing it must be stream-ordered). */
 long dsv41_index_select_workspace_bytes(int R, int n_pos);

@@ -117,6 +117,29 @@ def test_rope_against_complex_rotation_and_inverse():
     np.testing.assert_array_equal(sin[0], np.zeros(32, np.float32))
 
 
+def test_rope_tables_yarn_ramp():
+    """The YaRN correction of rope_tables (dsv41/model.py:76-117), from the table's angle at position 1: frequency
+    pairs below the fast correction dimension keep base^(-2i/d), those at or above the slow one are divided by
+    `factor`, and the ratio to base^(-2i/d) falls monotonically from 1 to 1/factor in between (YaRN, Peng et al.
+    2023, section 3.2: the correction dimension of r rotations is d ln(L / (2 pi r)) / (2 ln base))."""
+    import math
+    dim, L, base, factor = 64, 65536, 160000.0, 16.0
+    cos, sin = O.rope_tables(dim, 8, L, base, factor, 32, 1)
+    freq = np.arctan2(sin[1].astype(np.float64), cos[1].astype(np.float64))
+    plain = base ** (-np.arange(0, dim, 2) / dim)
+    ratio = freq / plain
+    cd = lambda rot: dim * math.log(L / (rot * 2 * math.pi)) / (2 * math.log(base))  # noqa: E731
+    low, high = math.floor(cd(32)), math.ceil(cd(1))
+    assert 0 < low < high < dim // 2
+    np.testing.assert_allclose(ratio[:low + 1], 1.0, rtol=1e-5)
+    np.testing.assert_allclose(ratio[high:], 1.0 / factor, rtol=1e-5)
+    mid = ratio[low:high + 1]
+    assert np.all(np.diff(mid) < 0) and 1.0 / factor < mid[1:-1].min() and mid[1:-1].max() < 1.0
+    # no correction without an original length: the plain table
+    cos0, sin0 = O.rope_tables(dim, 8, 0, base, factor, 32, 1)
+    np.testing.assert_allclose(np.arctan2(sin0[1], cos0[1]), plain, rtol=1e-5)
+
+
 @pytest.mark.parametrize("start", [0, 3, 127, 128, 300])
 def test_window_idx_brute_force(start):
     W, S = 128, 7
