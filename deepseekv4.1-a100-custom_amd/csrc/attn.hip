@@ -15,6 +15,8 @@
 //                                         8 key rows), so P never leaves registers; V is read from the same LDS tile.
 // Several splits per row write fp32 partials (m, l, acc); a combine kernel merges them with the sink and applies
 // the inverse rope (dsv41/fused2.py:381-403).  A single split writes the final bf16 output directly.
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -1615,6 +1617,73 @@ int finish_plan(AttnArgs& a, int want_nsplit, void* ws, long ws_bytes, int dv) {
   return 0;
 }
 
+// Arguments of a sattn2 launch (dsv41_sattn2 and its no-allocation variant); returns 0 or a hipError_t.
+int sattn2_args(AttnArgs& a, const void* q, const void* kv_win, long win_sstride, int win, const void* kv_c,
+                long c_sstride, int n_c_rows, const int* idx, int t, const long* pos, const long* seq,
+                const long* pmax, const long* plim, const float* sink, const float* cos_t, const float* sin_t, int rd,
+                float scale, void* out, int B, int h, int dv) {
+  if (win <= 0 || h <= 0 || t < 0 || rd < 0 || rd > dv || (rd & 1)) return (int)hipErrorInvalidValue;
+  if (t > 0 && (!kv_c || !idx)) return (int)hipErrorInvalidValue;
+  a = AttnArgs{};
+  a.q = (const uint16_t*)q;
+  a.H = h;
+  a.R = B;
+  a.mode = 1;
+  a.kv1 = (const uint16_t*)kv_win;
+  a.kv1_sstride = win_sstride;
+  a.n1 = win;
+  a.kv2 = (const uint16_t*)kv_c;
+  a.kv2_sstride = c_sstride;
+  a.n2 = n_c_rows;
+  a.idx = idx;
+  a.idx_rstride = t;
+  a.t = t;
+  a.rows_per_slot = 1;
+  a.pos = pos;
+  a.seq = seq;
+  a.pmax = pmax;
+  a.plim = plim;
+  a.scale = scale;
+  a.sink = sink;
+  a.L = win + t;
+  a.out = (uint16_t*)out;
+  a.out_rstride = (long)h * dv;
+  a.cos_t = cos_t;
+  a.sin_t = sin_t;
+  a.rd = rd;
+  return 0;
+}
+
+// ---- the no-allocation variant's scratch: one static array per device (each GPU the library runs on holds its
+// copy until the process ends), its device address taken once per device with hipGetSymbolAddress
+__device__ __align__(256) unsigned char scratch[DSV41_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {nullptr};
+
+// Device address of `scratch` on the current device (null on failure; *rc gets the hipError_t).
+void* scratch_ptr(int* rc) {
+  int dev = 0;
+  *rc = (int)hipGetDevice(&dev);
+  if (*rc) return nullptr;
+  if (dev < 0 || dev >= 64) {
+    *rc = (int)hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    *rc = (int)hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (*rc) return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+__global__ void zero_words_kernel(unsigned int* p, long n) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1733,39 +1802,44 @@ int dsv41_sattn2(const void* q, const void* kv_win, long win_sstride, int win, c
                  const long* plim, const float* sink, const float* cos_t, const float* sin_t, int rd, float scale,
                  void* out, int B, int h, int dqk, int dv, int want_nsplit, void* ws, long ws_bytes, void* stream) {
   if (B <= 0) return 0;
-  if (win <= 0 || h <= 0 || t < 0 || rd < 0 || rd > dv || (rd & 1)) return (int)hipErrorInvalidValue;
-  if (t > 0 && (!kv_c || !idx)) return (int)hipErrorInvalidValue;
-  AttnArgs a{};
-  a.q = (const uint16_t*)q;
+  AttnArgs a;
+  int rc = sattn2_args(a, q, kv_win, win_sstride, win, kv_c, c_sstride, n_c_rows, idx, t, pos, seq, pmax, plim, sink,
+                       cos_t, sin_t, rd, scale, out, B, h, dv);
+  if (rc) return rc;
   a.q_rstride = (long)h * dqk;
-  a.H = h;
-  a.R = B;
-  a.mode = 1;
-  a.kv1 = (const uint16_t*)kv_win;
-  a.kv1_sstride = win_sstride;
-  a.n1 = win;
-  a.kv2 = (const uint16_t*)kv_c;
-  a.kv2_sstride = c_sstride;
-  a.n2 = n_c_rows;
-  a.idx = idx;
-  a.idx_rstride = t;
-  a.t = t;
-  a.rows_per_slot = 1;
-  a.pos = pos;
-  a.seq = seq;
-  a.pmax = pmax;
-  a.plim = plim;
-  a.scale = scale;
-  a.sink = sink;
-  a.L = win + t;
-  a.out = (uint16_t*)out;
-  a.out_rstride = (long)h * dv;
-  a.cos_t = cos_t;
-  a.sin_t = sin_t;
-  a.rd = rd;
-  int rc = finish_plan(a, want_nsplit, ws, ws_bytes, dv);
+  rc = finish_plan(a, want_nsplit, ws, ws_bytes, dv);
   if (rc) return rc;
   return dispatch(a, dqk, dv, (hipStream_t)stream);
+}
+
+int dsv41_sattn2_noalloc(const void* q, const void* kv_win, long win_sstride, int win, const void* kv_c,
+                         long c_sstride, int n_c_rows, const int* idx, int t, const long* pos, const long* seq,
+                         const long* pmax, const long* plim, const float* sink, const float* cos_t, const float* sin_t,
+                         int rd, float scale, void* out, int B, int h, int dqk, int dv, int want_nsplit,
+                         void* stream) {
+  if (B <= 0) return 0;
+  AttnArgs a;
+  int rc = sattn2_args(a, q, kv_win, win_sstride, win, kv_c, c_sstride, n_c_rows, idx, t, pos, seq, pmax, plim, sink,
+                       cos_t, sin_t, rd, scale, out, B, h, dv);
+  if (rc) return rc;
+  a.q_rstride = (long)h * dqk;
+  const long need = dsv41_attn_workspace_bytes(B, h, win + t, dv, want_nsplit);
+  if (need > DSV41_SCRATCH_BYTES) return (int)hipErrorOutOfMemory;  // past the static scratch: pass fewer splits
+  void* ws = nullptr;
+  if (need > 0) {
+    ws = scratch_ptr(&rc);
+    if (!ws) return rc ? rc : (int)hipErrorInvalidValue;
+  }
+  rc = finish_plan(a, want_nsplit, ws, DSV41_SCRATCH_BYTES, dv);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if (a.arrive) {  // the split counters (and error word) start at zero: a previous call may have used another layout
+    const long words = counter_bytes(a.R, a.H) / 4;
+    zero_words_kernel<<<(int)((words + 255) / 256 < 64 ? (words + 255) / 256 : 64), 256, 0, st>>>(
+        (unsigned int*)ws, words);
+    DSV41_CHECK_LAUNCH();
+  }
+  return dispatch(a, dqk, dv, st);
 }
 
 }  // extern "C"

@@ -22,6 +22,8 @@ SIGNATURES = {
     "dsv41_sparse_attn2": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _L, _I, _L, _I, _F, _I, _P, _L, _P],
     "dsv41_sattn2": [_P, _P, _L, _I, _P, _L, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _F, _P, _I, _I, _I, _I, _I,
                      _P, _L, _P],
+    "dsv41_sattn2_noalloc": [_P, _P, _L, _I, _P, _L, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _F, _P, _I, _I, _I,
+                             _I, _I, _P],
     "dsv41_index_score": [_P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _L, _P, _I, _P, _L, _I, _I, _I, _P, _L, _P,
                           _P, _L, _P],
     "dsv41_select_workspace_bytes": [_I, _I],

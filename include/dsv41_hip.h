@@ -60,6 +60,25 @@ int dsv41_sattn2(const void* q, const void* kv_win, long win_sstride, int win, c
                  const long* plim, const float* sink, const float* cos_t, const float* sin_t, int rd, float scale,
                  void* out, int B, int h, int dqk, int dv, int want_nsplit, void* ws, long ws_bytes, void* stream);
 
+/* Size of the static device scratch of dsv41_sattn2_noalloc (bytes, per device). */
+#define DSV41_SCRATCH_BYTES (16L << 20)
+
+/* No counterpart in the reference: dsv41_sattn2 for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and results as dsv41_sattn2 without the
+ * workspace: the split partials and counters live in a static __device__ array of DSV41_SCRATCH_BYTES per device
+ * (held until the process ends; its address is taken with hipGetSymbolAddress on the first call on each device).
+ * Calls whose workspace (dsv41_attn_workspace_bytes for the same R, H, L, dv, want_nsplit) exceeds
+ * DSV41_SCRATCH_BYTES return hipErrorOutOfMemory: pass a smaller want_nsplit (1 needs none).  Every call on a device
+ * shares that device's array: calls that overlap on one device (different streams, or several threads without
+ * stream order) race.  The split counters are cleared by a fill kernel at the start of every call that uses them;
+ * the cooperative-merge error word of dsv41_attn_workspace_bytes' layout is not reported by this variant.
+ * Allocates nothing (no hipMalloc / hipFree). */
+int dsv41_sattn2_noalloc(const void* q, const void* kv_win, long win_sstride, int win, const void* kv_c,
+                         long c_sstride, int n_c_rows, const int* idx, int t, const long* pos, const long* seq,
+                         const long* pmax, const long* plim, const float* sink, const float* cos_t, const float* sin_t,
+                         int rd, float scale, void* out, int B, int h, int dqk, int dv, int want_nsplit,
+                         void* stream);
+
 /* ------------------------------------------------------------------------------------------------ compressor */
 
 /* Compressor pooling of the decode step, DecodeRuntime.compressor2 (dsv41/decode.py:243-265) after the wkv / wgate
