@@ -37,6 +37,12 @@ PINNING = {
                      "one-call start_pos 0 result; equal gate scores give the group mean, one dominant score gives that "
                      "member; vs torch.softmax composition (library routine)",
     "e4m3_decode": "all 256 codes vs torch.float8_e4m3fn -> float32 cast (library routine)",
+    "AttentionLayer": "composition of the pinned functions above; chunk invariance: a sequence fed as one chunk or as "
+                      "several continuation chunks gives the same outputs and caches (the reference's procedure, "
+                      "dsv41/test_long_prefill.py:66-96), tests/test_oracle.py",
+    "indexer_query": "composition of fake_quant_fp8, rope and fake_quant_fp4 (pinned above); the query side of "
+                     "AttentionLayer's chunk-invariance check",
+    "linear_fp8": "composition of fake_quant_fp8 (pinned) and a library matmul",
     "fp8_gemm": "vs torch matmul of the dequantised weight (library routine, exact products); PERM_K round trip "
                 "(known list dsv41/w8.py:23); block-diagonal == the dense product with the off-group blocks zeroed",
     "select_candidate_blocks": "properties of the top blocks (forced last block, count, every kept block max >= every "
@@ -49,9 +55,12 @@ PINNING = {
 def bf16(x) -> np.ndarray:
     """Round float32 to bfloat16 (RNE), returned as float32.  torch's bf16 cast (library routine)."""
     a = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
-    u = a.view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
-    out = r.astype(np.uint32).view(np.float32)
+    u = a.view(np.uint32)
+    r = (u >> 16) & np.uint32(1)
+    r += u
+    r += np.uint32(0x7FFF)  # wraps only for NaN patterns, which are restored below
+    r &= np.uint32(0xFFFF0000)
+    out = r.view(np.float32)
     nan = np.isnan(a)
     if nan.any():
         out = np.where(nan, a, out)
@@ -555,3 +564,93 @@ def index_key_row(kraw, w, cos, sin, pos, rd, eps) -> np.ndarray:
     y = bf16(rmsnorm(np.asarray(kraw, np.float32), w, eps))
     y = rope(y, cos, sin, pos, rd)
     return bf16(fake_quant_fp4(y, 32))
+
+
+# ----------------------------------------------------------------------------------------------- the layer
+def linear_fp8(x, w) -> np.ndarray:
+    """dsv41/model.py:56-59 with a bf16-valued weight w [N, K]: fq8(x, 32) @ w^T, fp32 accumulation, bf16 result."""
+    return bf16(fake_quant_fp8(np.asarray(x, np.float32), 32) @ np.asarray(w, np.float32).T)
+
+
+def indexer_query(x, qr, wq_b, weights_proj, cos, sin, rd, start_pos: int, n_heads: int, head_dim: int = 128):
+    """Indexer.__call__ query side (dsv41/model.py:734-746) for x [b, s, dim], qr [b, s, q_rank]: q =
+    fq4(rope(linear_fp8(qr, wq_b)), 32) [b, s, n_heads, head_dim]; weights = bf16(bf16(x @ weights_proj^T) * scale),
+    scale = head_dim^-1/2 n_heads^-1/2."""
+    x = np.asarray(x, np.float32)
+    b, s, _ = x.shape
+    q = linear_fp8(qr, wq_b).reshape(b, s, n_heads, head_dim)
+    for i in range(s):
+        q[:, i] = rope(q[:, i], cos, sin, np.int64(start_pos + i), rd)
+    q = bf16(fake_quant_fp4(q, 32))
+    w = bf16(bf16(x @ np.asarray(weights_proj, np.float32).T) * np.float32(head_dim ** -0.5 * n_heads ** -0.5))
+    return q, w
+
+
+class AttentionLayer:
+    """Attention.__call__ up to the o-projection (dsv41/model.py:1350-1573) for a layer that owns its window ring,
+    compressor, index keys and compressed rows: the composition of window_kv, compress_pool, index_key_row,
+    indexer_query, indexer_prefill, compress_row, sparse_attn and the inverse rope, holding the caches as numpy
+    state.  Weights as bf16-valued arrays (c_wkv / c_wgate fp32)."""
+
+    def __init__(self, weights: dict, *, n_heads, head_dim, rope_head_dim, window, ratio, index_n_heads, index_topk_k,
+                 cos, sin, slots, cap, eps=1e-6):
+        self.w = {k: np.asarray(v, np.float32) for k, v in weights.items()}
+        self.H, self.D, self.rd, self.W, self.ratio = n_heads, head_dim, rope_head_dim, window, ratio
+        self.HI, self.topk, self.eps, self.cos, self.sin = index_n_heads, index_topk_k, eps, cos, sin
+        self.ring = np.zeros((slots, window, head_dim), np.float32)
+        self.ckv = np.zeros((slots, cap, head_dim), np.float32)
+        self.index_k = np.zeros((slots, cap, 128), np.float32)
+        self.rk = np.zeros((slots, 8, head_dim), np.float32)
+        self.rs = np.full((slots, 8, head_dim), -np.inf, np.float32)
+        self.last_idx = None
+
+    def attend(self, x, start_pos: int) -> np.ndarray:
+        w, rd, eps, ratio = self.w, self.rd, self.eps, self.ratio
+        x = np.asarray(x, np.float32)
+        b, s, _ = x.shape
+        cos, sin = self.cos, self.sin
+        qr = bf16(rmsnorm(linear_fp8(x, w["wq_a"]), w["q_norm_w"], eps))                      # :1354
+        q = linear_fp8(qr, w["wq_b"]).reshape(b, s, self.H, self.D)                            # :1355
+        for i in range(s):
+            q[:, i] = rope(q[:, i], cos, sin, np.int64(start_pos + i), rd)                     # :1356
+        kv_raw = linear_fp8(x, w["wkv"])
+        end = start_pos + s
+        clen = end // ratio if ratio else 0
+        kk = min(self.topk, clen)
+        out = np.zeros((b, s, self.H, self.D), np.float32)
+        hist, widx = prefill_window_idx(self.W, s, start_pos)
+        if start_pos == 0:
+            widx = window_idx(self.W, s, 0)
+        lat_all = []
+        for bi in range(b):
+            rows, self.ring[bi] = window_kv(kv_raw[bi], w["kv_norm_w"], cos, sin, start_pos, self.ring[bi], rd, eps)
+            if ratio:
+                xf = x[bi]
+                lat, self.rk[bi], self.rs[bi] = compress_pool(xf @ w["c_wkv"].T, xf @ w["c_wgate"].T, start_pos,
+                                                              ratio, self.rk[bi], self.rs[bi], w["c_norm_w"], eps)
+                lat_all.append(lat)
+            off = rows.shape[0]
+            idx = widx
+            if kk:
+                first = start_pos - start_pos % ratio
+                if lat is not None:                                                            # :696-732
+                    kraw = bf16(lat @ w["i_wk"].T)
+                    for i in range(lat.shape[0]):
+                        self.index_k[bi, start_pos // ratio + i] = index_key_row(
+                            kraw[i], w["i_k_norm_w"], cos, sin, np.int64(first + i * ratio), rd, eps)
+                qi, wi = indexer_query(x[bi:bi + 1], qr[bi:bi + 1], w["i_wq_b"], w["i_weights_proj"], cos, sin, rd,
+                                       start_pos, self.HI)
+                cidx = indexer_prefill(qi, wi, self.index_k[bi:bi + 1, :clen], start_pos, ratio, self.topk, off)[0]
+                idx = np.concatenate([widx, cidx], -1)                                         # :1443
+            if ratio and lat is not None:                                                      # :1320-1347
+                first = start_pos - start_pos % ratio
+                for i in range(lat.shape[0]):
+                    self.ckv[bi, start_pos // ratio + i] = compress_row(lat[i], cos, sin,
+                                                                        np.int64(first + i * ratio), rd)
+            kv = np.concatenate([rows, self.ckv[bi, :clen]]) if clen else rows                 # :1442
+            o = sparse_attn(q[bi:bi + 1], kv[None], w["attn_sink"], idx[None], self.D ** -0.5,
+                            prefill_rounding=(s > 1))[0]                                       # :1526-1554
+            for i in range(s):
+                out[bi, i] = rope(o[i], cos, sin, np.int64(start_pos + i), rd, inverse=True)   # :1573
+            self.last_idx = idx
+        return out

@@ -472,3 +472,34 @@ def test_fp8_gemm_oracle():
             Wz[(g + 1) * 32:] = 0
             dense = (torch.from_numpy(xb[b * 3 + g]).double() @ Wz.T).float().numpy()
             np.testing.assert_array_equal(got[b, g * 32:(g + 1) * 32], dense[g * 32:(g + 1) * 32])
+
+
+def test_attention_layer_chunk_invariance():
+    """AttentionLayer (Attention.__call__ up to the o-projection, dsv41/model.py:1350-1573): a sequence fed as one
+    prefill chunk or as a fresh chunk plus continuations (partial compression groups, chunks shorter and longer than
+    the window) gives the same outputs, caches and compressed selections (dsv41/test_long_prefill.py:66-96), and a
+    following decode step agrees; the window and compressed rows of the selection are causal."""
+    from _layer_weights import layer_weights
+    rng = np.random.default_rng(90)
+    dim, q_rank, H, D, rd, W, ratio, HI, topk = 128, 64, 4, 64, 16, 16, 4, 4, 8
+    wts = layer_weights(rng, dim, q_rank, H, D, HI)
+    cos, sin = O.rope_tables(rd, 256, 0, 10000.0, 1.0, 32, 1)
+    kw = dict(n_heads=H, head_dim=D, rope_head_dim=rd, window=W, ratio=ratio, index_n_heads=HI, index_topk_k=topk,
+              cos=cos, sin=sin, slots=1, cap=40)
+    x = O.bf16(rng.standard_normal((1, 61, dim)).astype(np.float32))
+    full = O.AttentionLayer(wts, **kw)
+    o_full = full.attend(x[:, :60], 0)
+    part = O.AttentionLayer(wts, **kw)
+    outs = []
+    for a, b in ((0, 21), (21, 38), (38, 60)):
+        outs.append(part.attend(x[:, a:b], a))
+    np.testing.assert_allclose(np.concatenate(outs, 1), o_full, rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(part.ring, full.ring)
+    np.testing.assert_array_equal(part.ckv, full.ckv)
+    np.testing.assert_array_equal(part.index_k, full.index_k)
+    assert np.abs(full.ckv[0, :15]).sum() > 0 and np.abs(full.ckv[0, 15:]).sum() == 0  # 60 // 4 rows written
+    np.testing.assert_allclose(part.attend(x[:, 60:61], 60), full.attend(x[:, 60:61], 60), rtol=1e-5, atol=1e-6)
+    idx = full.last_idx  # decode step: W window rows then top-k compressed rows + offset, all causal
+    assert idx.shape == (1, W + topk)
+    c = idx[0, W:] - W
+    assert np.all((c >= 0) & (c < 61 // ratio)) and np.all(np.diff(c) > 0)
