@@ -196,7 +196,7 @@ def run_decode(args, dev):
     log(f"[bench] eager per-kernel medians (us): {kern_us}")
     kb = decode_bytes(cfg, sel_union, fused)
     return dict(cfg=cfg, step_us=step_us, kern_us=kern_us, kern_bytes=kb, steps=replays * NL, sel_union=sel_union,
-                alone_us=alone_us, fused=fused)
+                alone_us=alone_us, fused=fused, one_launch=L[0].selector(pos.shape[0], dev).one_launch)
 
 
 def run_prefill(args, dev):
@@ -389,42 +389,115 @@ def run_projections(args, dev):
     return res
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+        return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        return 1
+
+
 def cpu_baseline(cfg, budget_s: float):
-    """The oracle (numpy port of the reference's decode path) on the host: index score + top-k + sattn2 for one
-    slot of the workload, repeated until the budget is spent; scaled to a full layer-step (x slots)."""
+    """The oracle (numpy port of the reference's decode path) on the host, one whole layer-step of the workload per
+    repetition: every row's cache appends (ring row, compressed row, index-key row), index score + top-k and sattn2
+    over ring + selected rows, for every slot; repeated until the budget is spent (at least one repetition); the
+    median repetition is the value."""
     import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import dsv41_oracle as O
     from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        threads = os.cpu_count() or 1
     rng = np.random.default_rng(0)
-    n = cfg.n_c(0)
-    keys = O.fake_quant_fp4(rng.standard_normal((1, n, DI)).astype(np.float32) * 0.1, 32)
-    q8, s8 = O.key_encode_fp8(keys)
-    ckv = O.bf16(rng.standard_normal((1, n + 1, DQK)).astype(np.float32) * 0.1)
-    ring = O.bf16(rng.standard_normal((1, WIN, DQK)).astype(np.float32) * 0.1)
-    q = O.bf16(rng.standard_normal((1, 1, H, DQK)).astype(np.float32) * 0.1)
-    qi = O.fake_quant_fp4(rng.standard_normal((1, 1, HI, DI)).astype(np.float32), 32)
-    w = (rng.standard_normal((1, HI)) * 0.01).astype(np.float32)
+    S, rps = cfg.slots, cfg.rows_per_slot
+    ns = [cfg.n_c(s) for s in range(S)]
+    rd = 64
+    cos, sin = O.rope_tables(rd, max(cfg.ctx) + 8, 0, 10000.0, 1.0, 32, 1)
+    keys = [O.fake_quant_fp4(rng.standard_normal((1, n + 1, DI)).astype(np.float32) * 0.1, 32) for n in ns]
+    enc = [O.key_encode_fp8(k) for k in keys]
+    ckv = [O.bf16(rng.standard_normal((1, n + 1, DQK)).astype(np.float32) * 0.1) for n in ns]
+    ring = O.bf16(rng.standard_normal((S, WIN, DQK)).astype(np.float32) * 0.1)
+    R = S * rps
+    q = O.bf16(rng.standard_normal((R, 1, H, DQK)).astype(np.float32) * 0.1)
+    qi = O.fake_quant_fp4(rng.standard_normal((R, 1, HI, DI)).astype(np.float32), 32)
+    w = (rng.standard_normal((R, HI)) * 0.01).astype(np.float32)
+    x = O.bf16(rng.standard_normal((R, DQK)).astype(np.float32))
+    lat = O.bf16(rng.standard_normal((R, DQK)).astype(np.float32))
+    kraw = O.bf16(rng.standard_normal((R, DI)).astype(np.float32))
+    nw, kn = np.ones(DQK, np.float32), np.ones(DI, np.float32)
     sink = rng.standard_normal(H).astype(np.float32)
-    pos = cfg.ctx[0] - 1
     times = []
     t_end = time.perf_counter() + budget_s
     while time.perf_counter() < t_end or not times:
         t0 = time.perf_counter()
-        sc = O.index_score(qi, q8, w, [0], [n], k_scale=s8[..., 0])
-        idx = O.topk_indices(sc, cfg.topk, [n])
-        O.sattn2(q, ring, ckv, idx[:, None], [pos], [0], [pos], None, sink, None, None, 0, DQK ** -0.5, dv=DV)
+        for s in range(S):
+            for j in range(rps):
+                r = s * rps + j
+                pos = cfg.ctx[s] - rps + j
+                O.kv_write(x[r:r + 1], nw, cos, sin, [pos], [0], ring[s:s + 1], rd, 1e-6)
+                O.compress_row(lat[r], cos, sin, np.int64(pos + 1 - cfg.ratio), rd)
+                O.index_key_row(kraw[r], kn, cos, sin, np.int64(pos + 1 - cfg.ratio), rd, 1e-6)
+                cl = (pos + 1) // cfg.ratio
+                sc = O.index_score(qi[r:r + 1], enc[s][0], w[r:r + 1], [0], [cl], k_scale=enc[s][1][..., 0])
+                idx = O.topk_indices(sc, cfg.topk, [cl])
+                O.sattn2(q[r:r + 1], ring[s:s + 1], ckv[s], idx[:, None], [pos], [0], [cfg.ctx[s] - 1], [pos], sink,
+                         None, None, 0, DQK ** -0.5, dv=DV)
         times.append(time.perf_counter() - t0)
-    per_slot = float(np.median(times))
-    return {"value": per_slot * cfg.slots * cfg.rows_per_slot * 1e6, "unit": "us/layer-step", "cores": threads,
-            "kind": "port",
-            "sample": f"oracle (numpy) index score + top-k + sattn2 for 1 of {cfg.slots} slots ({n} keys, k "
-                      f"{cfg.topk}), {len(times)} reps in {budget_s:.0f} s, median x {cfg.slots} slots"}
+    return {"value": float(np.median(times)) * 1e6, "unit": "us/layer-step", "cores": _blas_threads(),
+            "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(), "kind": "port",
+            "sample": f"oracle (numpy): one whole layer-step of {cfg.name} per repetition ({R} rows over {S} slots: "
+                      f"appends, index score + top-k {cfg.topk}, sattn2), {len(times)} reps in ~{budget_s:.0f} s, "
+                      f"median; cores = BLAS threads"}
+
+
+def cpu_baseline_prefill(budget_s: float, rows: int = 32):
+    """The oracle on the host for C3: `rows` evenly spaced query rows of the 2048-token chunk, each through the
+    indexer (score over its causal compressed keys, top-2048) and the sparse attention over its 128 window + 2048
+    selected rows (the reference's prefill rounding), timed as one batch and scaled to the chunk: tok/s = 2048 /
+    (batch time x 2048 / rows)."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import dsv41_oracle as O
+    from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN, PREFILL
+    cfg = PREFILL["C3"]
+    rng = np.random.default_rng(1)
+    T = cfg.n_c
+    keys = O.fake_quant_fp4(rng.standard_normal((1, T, DI)).astype(np.float32) * 0.1, 32)
+    k8, s8 = O.key_encode_fp8(keys)
+    kv = O.bf16(rng.standard_normal((1, WIN - 1 + cfg.chunk + T, DQK)).astype(np.float32) * 0.1)
+    sel_rows = np.linspace(0, cfg.chunk - 1, rows).astype(int)
+    qi = O.fake_quant_fp4(rng.standard_normal((1, rows, HI, DI)).astype(np.float32), 32)
+    w = (rng.standard_normal((1, rows, HI)) * 0.01).astype(np.float32)
+    q = O.bf16(rng.standard_normal((1, rows, H, DQK)).astype(np.float32) * 0.1)
+    sink = rng.standard_normal(H).astype(np.float32)
+    off = WIN - 1 + cfg.chunk
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or not times:
+        t0 = time.perf_counter()
+        for n, i in enumerate(sel_rows):
+            cl = (cfg.prior + i + 1) // cfg.ratio
+            sc = O.index_score(qi[:, n], k8, w[:, n], [0], [cl], k_scale=s8[..., 0])
+            cidx = O.topk_indices(sc, cfg.topk, [cl])[0]
+            widx = np.arange(i, i + WIN, dtype=np.int32)  # the 127 history rows + the row itself
+            idx = np.concatenate([widx, np.where(cidx >= 0, cidx + off, -1)])[None, None]
+            O.sparse_attn(q[:, n:n + 1], kv, sink, idx, DQK ** -0.5, dv=DV)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times)) * cfg.chunk / rows
+    return {"value": round(cfg.chunk / t, 2), "unit": "tok/s", "cores": _blas_threads(), "host_cpus": os.cpu_count(),
+            "cpu_model": _cpu_model(), "kind": "port",
+            "sample": f"oracle (numpy): {rows} of the chunk's {cfg.chunk} query rows (indexer over {T} keys + top-"
+                      f"{cfg.topk}, sparse attention over {WIN} + {cfg.topk} rows), {len(times)} reps in "
+                      f"~{budget_s:.0f} s, median, scaled to the chunk"}
 
 
 def main():
@@ -469,14 +542,18 @@ def main():
     r = run_decode(args, dev)
     cfg = r["cfg"]
     kb, ku = r["kern_bytes"], r["kern_us"]
-    kernel_names = {"indexer": "index_select_kernel<128, true> (cache appends + scores + top-k, one launch)"
-                    if r["fused"] else "index_select_kernel (scores + top-k, one launch)",
-                    "sattn": "attn_decode_kernel<576, 512> (splits merged in-kernel)"}
+    R = cfg.slots * cfg.rows_per_slot
+    sel_name = ("index_select_kernel<128, true> (cache appends + scores + top-k, one launch)" if r["fused"] else
+                "index_select_kernel (scores + top-k, one launch)" if r["one_launch"] else
+                "index_score_kernel + select kernels (scores with histogram, then the top-k; multi-launch)")
+    att_name = ("attn_decode_kernel<576, 512> (splits merged in-kernel)" if R < 16 else
+                "attn_prefill_ws_kernel<576, 512> + attn_decode_combine_kernel (key splits)")
+    kernel_names = {"indexer": sel_name, "sattn": att_name}
     roof = {}
     for name, us in r["alone_us"].items():
         achieved = kb[name] / (us * 1e-6) / 1e9
         traffic = None
-        tf = os.path.join(ROOT, "profiles", f"{name}_C2_traffic.json")
+        tf = os.path.join(ROOT, "profiles", f"{name}_{cfg.name}_traffic.json")
         if os.path.exists(tf):  # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
             with open(tf) as f:
                 traffic = json.load(f).get("bytes_per_launch")
@@ -489,6 +566,8 @@ def main():
     pre = None if args.no_prefill else run_prefill(args, dev)
     proj = None if args.no_proj else run_projections(args, dev)
     cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_budget)
+    if cpu is not None and pre is not None:
+        cpu["prefill"] = cpu_baseline_prefill(args.cpu_budget)
     out = {
         "metric": "attn decode us/layer-step + % HBM roofline @128Kx4 slots; prefill tok/s @2K chunk",
         "value": round(r["step_us"], 3),
