@@ -89,6 +89,8 @@ def run_decode(args, dev):
     cl = torch.div(pos + 1, cfg.ratio, rounding_mode="floor")  # once per token, shared by every layer
 
     fused = not args.separate_appends and cfg.rows_per_slot == 1  # (the one-launch appends need one row per slot)
+    R = cfg.slots * cfg.rows_per_slot
+    one = fused and args.one_launch and L[0].fused_fits(R, st["q"].shape[2])  # the whole step in one launch
 
     def appends_select(lay):
         if fused:
@@ -99,6 +101,9 @@ def run_decode(args, dev):
         return lay.select(st["q_idx"], st["w_idx"], pos, seq, cl)
 
     def layer_step(lay):
+        if one:
+            return lay.step_fused(st["q"], st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos,
+                                  seq, st["q_idx"], st["w_idx"], pmax, plim=pos, cl=cl)
         idx = appends_select(lay)
         return lay.attend(st["q"], idx, pos, seq, pmax, plim=pos)
 
@@ -112,13 +117,25 @@ def run_decode(args, dev):
     # appends + scores + top-k: one launch; with --separate-appends the appends launch is timed apart), sattn
     # (attention, splits merged in-kernel)
     E = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    phases = {"indexer": [], "sattn": []} if fused else {"appends": [], "indexer": [], "sattn": []}
+    phases = ({"step": []} if one else {"indexer": [], "sattn": []} if fused else
+              {"appends": [], "indexer": [], "sattn": []})
     reps = max(2, min(args.steps, 20))
     sel_union = None
     for rep in range(reps):
         for lay in L:
             ev = [E() for _ in range(len(phases) + 1)]
             ev[0].record(stream)
+            if one:
+                idx = torch.empty(R, cfg.topk, dtype=torch.int32, device=dev)
+                lay.step_fused(st["q"], st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos,
+                               seq, st["q_idx"], st["w_idx"], pmax, plim=pos, cl=cl, idx_out=idx)
+                ev[-1].record(stream)
+                torch.cuda.synchronize(dev)
+                phases["step"].append(ev[0].elapsed_time(ev[1]) * 1000.0)
+                if sel_union is None:
+                    ids = idx.view(cfg.slots, cfg.rows_per_slot, -1).cpu()
+                    sel_union = [int(torch.unique(ids[s][ids[s] >= 0]).numel()) for s in range(cfg.slots)]
+                continue
             if fused:
                 idx = appends_select(lay)
             else:
@@ -168,6 +185,12 @@ def run_decode(args, dev):
 
     # ---- each heavy kernel alone: a graph of NL launches of it (one per cache copy), replayed; the average launch
     # duration (events on the launch stream around the replays) is the roofline denominator
+    if one:  # the step is one kernel: its graph above is the kernel alone
+        alone_us = {"step": step_us}
+        log(f"[bench] eager per-kernel medians (us): {kern_us}")
+        kb = {"step": step_algorithmic_bytes(cfg)}
+        return dict(cfg=cfg, step_us=step_us, kern_us=kern_us, kern_bytes=kb, steps=replays * NL,
+                    sel_union=sel_union, alone_us=alone_us, fused=fused, one_launch=True, one=True)
     idxs = [appends_select(lay).clone() for lay in L]
     torch.cuda.synchronize(dev)
     only = {"indexer": lambda lay, i: appends_select(lay) if fused else lay.select(st["q_idx"], st["w_idx"], pos,
@@ -196,7 +219,7 @@ def run_decode(args, dev):
     log(f"[bench] eager per-kernel medians (us): {kern_us}")
     kb = decode_bytes(cfg, sel_union, fused)
     return dict(cfg=cfg, step_us=step_us, kern_us=kern_us, kern_bytes=kb, steps=replays * NL, sel_union=sel_union,
-                alone_us=alone_us, fused=fused, one_launch=L[0].selector(pos.shape[0], dev).one_launch)
+                alone_us=alone_us, fused=fused, one_launch=L[0].selector(pos.shape[0], dev).one_launch, one=False)
 
 
 def run_prefill(args, dev):
@@ -512,6 +535,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-proj", action="store_true", help="skip the FP8 projection GEMVs")
     ap.add_argument("--proj-only", action="store_true", help="only the FP8 projection GEMVs (for profiling)")
+    ap.add_argument("--one-launch", action="store_true",
+                    help="decode: the whole layer-step as one launch (dsv41_decode_step) instead of indexer + attention")
     ap.add_argument("--separate-appends", action="store_true",
                     help="decode: the cache appends as their own launch before the indexer (default: one launch)")
     ap.add_argument("--prefill-reps", type=int, default=5)
@@ -548,7 +573,8 @@ def main():
                 "index_score_kernel + select kernels (scores with histogram, then the top-k; multi-launch)")
     att_name = ("attn_decode_kernel<576, 512> (splits merged in-kernel)" if R < 16 else
                 "attn_prefill_ws_kernel<576, 512> + attn_decode_combine_kernel (key splits)")
-    kernel_names = {"indexer": sel_name, "sattn": att_name}
+    kernel_names = {"indexer": sel_name, "sattn": att_name,
+                    "step": "decode_step_kernel<576, 512> (appends + scores + top-k + attention, one launch)"}
     roof = {}
     for name, us in r["alone_us"].items():
         achieved = kb[name] / (us * 1e-6) / 1e9

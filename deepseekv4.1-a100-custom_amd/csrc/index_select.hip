@@ -123,6 +123,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
 
   // ---- A. row data (independent loads), scores, histogram
   DSV41_PH(0);
+  DSV41_PX(0);
   DSV41_TS(48);
   const long clr = row_cl(a, r);
   const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
@@ -213,6 +214,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
 #ifdef DSV41_TIMING
   __builtin_amdgcn_s_waitcnt(0);
   DSV41_TS(49);
+  DSV41_PX(1);
 #endif
 #pragma unroll 1
   for (int i = t; i < kHistBins; i += kIsThreads) lhist[i] = 0;
@@ -231,8 +233,10 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   }
 #ifdef DSV41_TIMING
   DSV41_TS(50);
+  DSV41_PX(2);
   __builtin_amdgcn_s_waitcnt(0);
   DSV41_TS(51);
+  DSV41_PX(3);
 #endif
   if constexpr (FUSED) {
     if (opmask) {  // (the operands were loaded ahead of the keys)
@@ -242,8 +246,10 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
       for (int which = first + 1; which < 3; ++which)
         if (opmask >> which & 1) row_op<kIsThreads>(make_op(which), redf);
     }
+    DSV41_PX(4);
     qprep512_store(qp, a.HI, qs, wfl);
     lds_barrier();  // queries, weights and the new key staged
+    DSV41_PX(5);
 #pragma unroll
     for (int ht = 0; ht < kHT; ++ht) {
       const int h = ht * 16 + l16;
@@ -290,6 +296,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     }
   }
   DSV41_TS(53);
+  DSV41_PX(6);
   __syncthreads();
   DSV41_PH(1);
   DSV41_TS(54);
@@ -545,6 +552,7 @@ extern "C" {
 
 #ifdef DSV41_TIMING
 int dsv41_read_spins_is(int* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_is_spins), sizeof(g_is_spins)); }
+int dsv41_read_px_is(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_px), sizeof(g_dsv41_px)); }
 int dsv41_read_ph_is(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ph), sizeof(g_dsv41_ph)); }
 int dsv41_read_ts_is(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
 #endif

@@ -108,6 +108,60 @@ class DecodeLayer:
         return sattn2(q, self.ring, self.ckv, idx, pos, self.sink, self.cos, self.sin, 0 if self.dv < q.shape[-1]
                       else self.rd, self.scale, seq, pmax, plim=plim, d_v=self.dv, ws=ws)
 
+    def fused_fits(self, B: int, h: int) -> bool:
+        """Whether dsv41_decode_step (the whole layer-step in one launch) takes B rows of h heads here."""
+        from ._lib import lib
+        dqk = self.ckv.shape[-1]
+        dv = 512 if dqk == 576 else dqk
+        return bool(lib().dsv41_decode_step_fits(B, self.k8.shape[1] - 1, h, self.topk, self.ring.shape[1], dqk, dv))
+
+    def step_fused(self, q, kv_raw, kv_norm, latent, k_raw, k_norm, pos, seq, q_idx, w_idx, pmax, plim=None,
+                   cl=None, idx_out=None, score_out=None, out=None):
+        """The whole decode layer-step in one launch (dsv41_decode_step): the cache appends, the indexer (scores +
+        top-k) and sattn2 over ring + selected rows -> o [B, 1, h, dv].  The rows' sequences must be distinct and
+        fused_fits(B, h) true.  idx_out (int32 [B, k]) / score_out (fp32 [B, >= n_pos]) optionally receive the
+        selection and the scores."""
+        from ._lib import as_i64, call, lib, ptr, require_gpu, stream
+        dev = require_gpu(q, kv_raw, q_idx)
+        B, _, h, dqk = q.shape
+        dv = 512 if dqk == 576 else dqk
+        n_sel = self.k8.shape[1] - 1  # the tables' spare last row is never valid
+        if not self.fused_fits(B, h):
+            raise RuntimeError(f"step_fused: {B} rows x {h} heads over {n_sel} positions do not fit one launch")
+        pos = as_i64(pos.reshape(-1), dev)
+        seq = as_i64(seq.reshape(-1), dev)
+        pmax = as_i64(pmax.reshape(-1), dev)
+        plim = as_i64(plim.reshape(-1), dev) if plim is not None else None
+        if cl is None:
+            cl = torch.div(pos + 1, self.ratio, rounding_mode="floor")
+        cl = as_i64(cl.reshape(-1), dev)
+        key = ("step", B, n_sel, h, dv)
+        ws = self._attn_ws.get(key)
+        if ws is None:
+            n = lib().dsv41_decode_step_workspace_bytes(B, n_sel, h, dv)
+            ws = self._attn_ws[key] = torch.zeros((n + 255) // 256 * 64, device=dev, dtype=torch.float32)
+        nbytes = ws.numel() * 4
+        o = out if out is not None else torch.empty(B, 1, h, dv, device=dev, dtype=torch.bfloat16)
+        ring, ckv, k8, ks = self.ring, self.ckv, self.k8, self.ks
+        Dw = ring.shape[-1]
+        x = kv_raw.reshape(B, Dw).contiguous()
+        lat = latent.reshape(B, -1).contiguous() if latent is not None else None
+        call("dsv41_decode_step", ptr(x), ptr(kv_norm.to(torch.bfloat16).contiguous()), ptr(ring), ring.stride(0),
+             ring.shape[1], Dw, ptr(lat), ptr(ckv), ckv.stride(0), ckv.shape[1],
+             ptr(k_raw.reshape(B, -1).contiguous()), ptr(k_norm.to(torch.bfloat16).contiguous()), ptr(self.kbf16),
+             self.kbf16.stride(0) if self.kbf16 is not None else 0, ptr(k8), k8.stride(0), ptr(ks), ks.stride(0),
+             k8.shape[1], ptr(pos), ptr(seq), B, int(self.ratio), ptr(self.cos), ptr(self.sin), int(self.rd),
+             float(self.eps), ptr(q_idx.contiguous()), ptr(w_idx.to(torch.bfloat16).contiguous()), q_idx.shape[-2],
+             ptr(cl), n_sel, int(self.topk), 0, ptr(q.contiguous()), h, ptr(pmax), ptr(plim), ptr(self.sink),
+             0 if dv < dqk else int(self.rd), float(self.scale), ptr(o), ptr(idx_out),
+             idx_out.stride(0) if idx_out is not None else 0, ptr(score_out),
+             score_out.stride(0) if score_out is not None else 0, ptr(ws), nbytes, stream(dev))
+        from . import _lib
+        if _lib.CHECK_ERRORS:
+            from ._lib import check_error_word
+            check_error_word("decode_step", ws.view(torch.int32)[:1])
+        return o
+
     def step(self, q, q_idx, w_idx, pos, seq, pmax, plim=None):
         idx = self.select(q_idx, w_idx, pos, seq)
         return self.attend(q, idx, pos, seq, pmax, plim)
