@@ -334,7 +334,18 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   DSV41_TS(10);
   DSV41_PH(0);
   int sp, hg, r, home = -1;
-  if (a.arrive) {  // the nsplit workgroups of a unit share XCD `home` and merge through its L2
+  if (a.coop && a.hg_share) {
+    // cooperative merge (device-scope, any placement): the head groups of one (row, split) share an XCD, so the
+    // rows they all gather come from one L2
+    const int HG = (a.H + 15) / 16;
+    const int x = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+    const int grp = x + kXcds * (j / HG);
+    if (grp >= a.R * a.nsplit) return;
+    hg = j % HG;
+    r = grp / a.nsplit;
+    sp = grp % a.nsplit;
+    if (hg * 16 >= a.H) return;
+  } else if (a.arrive) {  // the nsplit workgroups of a unit share XCD `home` and merge through its L2
     const int x = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
     const int unit = x * a.upx + j / a.nsplit;
     if (unit >= a.units) return;
@@ -1352,7 +1363,10 @@ bool use_decode_kernel(int R, int H) { return (long)R * ((H + 63) / 64) < 16; }
 template <int DQK, int DV>
 int launch_attn(AttnArgs& a, hipStream_t st) {
   if (use_decode_kernel(a.R, a.H)) {
-    const dim3 grid = a.arrive ? dim3(kXcds * a.upx * a.nsplit) : dim3(a.nsplit, (a.H + 15) / 16, a.R);
+    const int HG = (a.H + 15) / 16;
+    const dim3 grid = a.coop && a.hg_share ? dim3(kXcds * HG * ((a.R * a.nsplit + kXcds - 1) / kXcds))
+                      : a.arrive          ? dim3(kXcds * a.upx * a.nsplit)
+                                          : dim3(a.nsplit, HG, a.R);
     attn_decode_kernel<DQK, DV><<<grid, 512, 0, st>>>(a);
     DSV41_CHECK_LAUNCH();
     if (a.nsplit > 1 && !a.arrive) {
@@ -1404,6 +1418,10 @@ int cus_per_xcd() {
 }
 
 constexpr int kFuseMaxSplits = 32;  // splits a decode launch merges itself
+#ifndef DSV41_DEC_WG
+#define DSV41_DEC_WG 192
+#endif
+constexpr int kDecWG = DSV41_DEC_WG;  // decode-kernel workgroups the split plan aims at
 
 // Split plan.  Decode kernel: <= 192 workgroups over (rows x 16-head groups x splits), >= 2 tiles of 64 keys per
 // split.  64-head kernel: >= 512 workgroups when rows are few, >= 2 tiles of 32 keys per split.
@@ -1419,7 +1437,7 @@ void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
     // the tiles over the splits.  Measured at C2 (16 units, cooperative merge): 12 splits 19.5 us, 16 splits 20.2 us.
     const long wgs = (long)R * ((H + 15) / 16);
     const int cap = tiles / 2 < 1 ? 1 : tiles / 2;
-    int ns = (int)(wgs >= 192 ? 1 : 192 / wgs);
+    int ns = (int)(wgs >= kDecWG ? 1 : kDecWG / wgs);
     if (ns > cap) ns = cap;
     *nsplit = ns;
     *chunk = (tiles + ns - 1) / ns * tile;
@@ -1475,8 +1493,12 @@ int finish_plan(AttnArgs& a, int want_nsplit, void* ws, long ws_bytes, int dv) {
       a.arrive = (int*)((char*)ws + kCounterBase);
       // cooperative merge when every workgroup of the launch can be resident at once (one per CU, the XCDs dealt
       // round-robin): early arrivals wait for the rest of their unit
-      if ((long)a.upx * ns <= cus_per_xcd())
+      if ((long)a.upx * ns <= cus_per_xcd()) {
         a.coop = (unsigned long long*)((char*)ws + kCounterBase + ((long)a.units * 4 + 7) / 8 * 8);
+        // head groups of a (row, split) on one XCD when that placement is also resident at once
+        const long per_xcd = (long)((a.H + 15) / 16) * ((a.R * ns + kXcds - 1) / kXcds);
+        a.hg_share = per_xcd <= cus_per_xcd();
+      }
     }
   }
   return 0;

@@ -40,6 +40,7 @@ struct AttnArgs {
                              // (launch epoch * 256 + arrivals), every split merges a slice; else null
   int* err;     // with arrive: the workspace error word (set to 1 when a merge stopped waiting for its unit)
   int units;    // with arrive: (row, 16-head group) units, placed upx per XCD (1-D grid of kXcds * upx * nsplit)
+  int hg_share; // with coop: the head groups of a (row, split) placed on one XCD instead
   int upx;
   const float* cos_t;
   const float* sin_t;

@@ -142,8 +142,8 @@ __device__ long long g_dsv41_wg[4096][2];
 // Per-workgroup phase stamps (1-D grids, first 1024 workgroups).
 __device__ long long g_dsv41_ph[1024][8];
 __device__ long long g_dsv41_ck[1024][8];  // shader clock at the same points
-// Extra per-workgroup stamps (16 slots, 1-D grids, first 1024 workgroups).
-__device__ long long g_dsv41_px[1024][16];
+// Extra per-workgroup stamps (32 slots, 1-D grids, first 1024 workgroups).
+__device__ long long g_dsv41_px[1024][32];
 #define DSV41_PX(k)                                                                       \
   do {                                                                                    \
     if (threadIdx.x == 0 && blockIdx.x < 1024) g_dsv41_px[blockIdx.x][k] = wall_clock64(); \

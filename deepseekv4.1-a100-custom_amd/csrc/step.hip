@@ -158,8 +158,22 @@ __global__ void __launch_bounds__(kStThreads, 1) decode_step_kernel(const StepAr
 
   // ================================================================ A. row data, queries, Q staging, scores
   DSV41_PH(0);
-  const long clr = row_cl(a, r);
   const long slot = a.seq[r];
+  // the chunk's key loads first: they depend on the slot only (positions past the valid count are masked later)
+  constexpr int NT = 64 / 16;  // 16-key column tiles per wave (64 keys per wave, 512 per workgroup)
+  uint4 k0[NT], k1[NT];
+  float ksc[NT];
+  const int pw = ch * kStChunk + wave * 64;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int p = pw + nt * 16 + l16;
+    const bool pv = p < a.n_pos;
+    const uint8_t* krow = (const uint8_t*)a.keys + slot * a.k_sstride + (long)p * 128 + g4 * 32;
+    k0[nt] = pv ? *(const uint4*)krow : make_uint4(0, 0, 0, 0);
+    k1[nt] = pv ? *(const uint4*)(krow + 16) : make_uint4(0, 0, 0, 0);
+    ksc[nt] = pv ? a.kscale[slot * a.ks_sstride + p] : 0.0f;
+  }
+  const long clr = row_cl(a, r);
   const long ppos = g.pos[r];
   const long pmax = at.pmax[r];
   const long plim = at.plim ? at.plim[r] : ppos;
@@ -238,22 +252,11 @@ __global__ void __launch_bounds__(kStThreads, 1) decode_step_kernel(const StepAr
   qprep512_load(g.q_idx + (long)r * a.HI * 128, g.w_idx + (long)r * a.HI, a.HI, qp);
 #pragma unroll 1
   for (int i = t; i < kHistBins; i += kStThreads) lhist[i] = 0;
-  constexpr int NT = 64 / 16;  // 16-key column tiles per wave (64 keys per wave, 512 per workgroup)
-  uint4 k0[NT], k1[NT];
-  float ksc[NT];
-  const int pw = ch * kStChunk + wave * 64;
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int p = pw + nt * 16 + l16;
-    const bool pv = p < c;
-    const uint8_t* krow = (const uint8_t*)a.keys + slot * a.k_sstride + (long)p * 128 + g4 * 32;
-    k0[nt] = pv ? *(const uint4*)krow : make_uint4(0, 0, 0, 0);
-    k1[nt] = pv ? *(const uint4*)(krow + 16) : make_uint4(0, 0, 0, 0);
-    ksc[nt] = pv ? a.kscale[slot * a.ks_sstride + p] : 0.0f;
-  }
+  DSV41_PX(16);
   if (key_here) row_compute<kStThreads, true>(make_op(2, true), kreg, redf);  // (LDS barriers: keys stay in flight)
   qprep512_store(qp, a.HI, qs, wfl);
   lds_barrier();
+  DSV41_PX(17);
   const int nht = (a.HI + 15) / 16;
   i32x8_t qa8[kHT];
   uint4 qa16[kHT][4];
@@ -291,6 +294,7 @@ __global__ void __launch_bounds__(kStThreads, 1) decode_step_kernel(const StepAr
       if (orow && p < a.n_pos) orow[p] = p < c ? v : -__builtin_inff();
     }
   }
+  DSV41_PX(18);
   __builtin_amdgcn_s_waitcnt(0);  // (Q staged)
   __syncthreads();
   DSV41_PH(1);
