@@ -932,18 +932,22 @@ __global__ void __launch_bounds__(512) attn_prefill_kernel(const AttnArgs a) {
   }
 }
 
-// Many query rows, pipelined roles: one workgroup per (query row, 64 heads), whole key list, 32-key tiles, and the
-// two halves of the tile work overlapped across waves:
-//   QK waves 0..3, w = (hb = w & 1: heads 32hb..32hb+31, kb = w >> 1: keys 16kb..16kb+15 of the tile): S for tile t
-//       (16x16x32 bf16 MFMA, Q of 32 heads in VGPRs, each K fragment used for two head blocks), per-lane partial
-//       maxima exchanged with the wave of the other key half through LDS (a flag word per wave, no workgroup
-//       barrier), then the probabilities (bf16, MFMA operand order) and the per-head rescale factor published through
-//       LDS.  Wave 0 also loads the index entries and resolves the row pointers three tiles ahead.
-//   PV waves 4..7, cq = w - 4: O[64 heads x columns cq*DV/4 ..] += P V for tile t - 1 (16x16x32 bf16 MFMA over the
-//       tile's 32 keys, each transposed V fragment used for four head blocks), interleaved with the direct-to-LDS
-//       gathers of tile t + 2 (counted vmcnt waits).
-// Four tile buffers: tile t (QK), t - 1 (PV), t + 1 and t + 2 (in flight).  One workgroup barrier per tile (B0):
-// tile t has landed; P / rescale of tile t - 1 and the row pointers of tile t + 2 are visible.
+// Many query rows, pipelined roles: one workgroup per (query row, 64 heads), whole key list, 32-key tiles, three
+// stages in flight across the waves (iteration t, one workgroup barrier B0 each):
+//   QK waves 0..3, w = (hb = w & 1: heads 32hb..32hb+31, kb = w >> 1: keys 16kb..16kb+15 of the tile): the MFMAs of
+//       S for tile t (16x16x32 bf16, Q of 32 heads in VGPRs, each K fragment used for two head blocks), and while
+//       they run the softmax of tile t - 1: its per-lane partial maxima of both key halves were written to LDS in
+//       iteration t - 1, so B0 publishes them and no wave waits for a partner inside an iteration.  The probabilities
+//       (bf16, MFMA operand order) and the per-head rescale factor of tile t - 1 go to LDS, then the partial maxima of
+//       tile t.  Wave 0 also loads the index entries and resolves the row pointers three tiles ahead.
+//   PV waves 4..7, cq = w - 4: O[64 heads x columns cq*DV/4 ..] += P V for tile t - 2 (16x16x32 bf16 MFMA over the
+//       tile's 32 keys, each transposed V fragment used for four head blocks; the V fragments were read into VGPRs
+//       in iteration t - 1), interleaved with the direct-to-LDS gathers of tile t + 2 (counted vmcnt waits), then
+//       the V fragments of tile t - 1.
+// Four tile buffers: tile t (QK), t - 1 (V read by the PV waves), t + 1 and t + 2 (in flight; tile t + 2 goes into
+// tile t - 2's buffer, whose last read ended before B0).  B0: tile t has landed; P / rescale of tile t - 2, the
+// partial maxima of tile t - 1 and the row pointers of tile t + 2 are visible.  Keep the PV waves free of register
+// spills: a scratch reload waits for every outstanding load (vmcnt(0)), the in-flight gathers included.
 template <int DQK, int DV>
 __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) {
   constexpr int KS = DQK / 32;  // 32-deep k steps of QK^T
@@ -959,8 +963,7 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   __shared__ __align__(16) uint16_t ktile[NBUF * TILE_ELEMS];
   __shared__ const uint16_t* rptr[NBUF][TILE];
   __shared__ uint2 pex[2][4][2][64];  // [tile parity][head block][key block][lane]
-  __shared__ float xmax[2][4][64];    // [key half][lane group][head]: partial maxima; at the end the partial sums
-  __shared__ int xflag[4];            // QK wave w: tiles whose partial maxima are in xmax
+  __shared__ float xmax[2][2][4][64];  // [tile parity][key half][lane group][head]: partial maxima; at the end sums
   __shared__ __align__(16) float salpha[2][64];  // [tile parity][head]: rescale factor (1 when the reference stays)
   __shared__ float hfac[64];
 
@@ -1026,7 +1029,7 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
     resolve(1, p0);
     resolve(2, p1);
   }
-  if (tid < 4) xflag[tid] = 0;
+  (&xmax[1][0][0][0])[tid] = -1e30f;  // (512 entries: the maxima "of tile -1")
   float* stg = (float*)ktile;  // output staging [64 heads][DV] once the tiles are done
 #define PF_TS(k, thr) \
   if (t >= 30 && t < 34) DSV41_TST(16 * (t - 30) + (k), thr)
@@ -1048,11 +1051,16 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
     int ix_cur = load_ix2(1), ix_nxt = load_ix2(2);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int t = 0; t <= ntiles; ++t) {
+    float scp[2][4];  // scaled, masked scores of the previous tile (key 16kb + 4g + i, head 32hb + 16b + l16)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) scp[b][i] = -1e30f;
+    for (int t = 0; t <= ntiles + 1; ++t) {
       PF_TS(0, 0);
       lds_barrier();  // B0
       PF_TS(1, 0);
-      if (t >= ntiles) break;
+      if (t > ntiles) break;
       if (t + 3 < ntiles) {  // wave 0: pointers of tile t + 3 (its slot last served tile t - 1, now done)
         resolve(t + 3, ix_cur);
         if ((t + 3) & 1) {  // pair consumed: the next one moves up, the one after is loaded (two tiles ahead)
@@ -1060,76 +1068,75 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
           ix_nxt = load_ix2((t + 3) / 2 + 2);
         }
       }
+      // One scheduling region (no branches): the partial maxima of tile t - 1 and the K fragments of tile t are
+      // read, the MFMAs of tile t are issued with the softmax of tile t - 1 between them, then the partial maxima of
+      // tile t are written.  At t == ntiles the MFMAs run on a stale buffer and their maxima are never read.
+      const int tp = t - 1;
+      float xm[2][8];
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) xm[b][u] = xmax[tp & 1][u >> 2][u & 3][32 * hb + 16 * b + l16];
       const uint16_t* buf = ktile + (t % NBUF) * TILE_ELEMS;
       const int jr = 16 * kb + l16;
       // chunk (4 ks + g) ^ (jr & 7) = 4 ks + (g ^ (jr & 3)) + (jr & 4) for even ks, - (jr & 4) for odd ks: two
       // base addresses and immediate offsets
       const uint16_t* kre = buf + jr * DQK + ((g ^ (jr & 3)) + (jr & 4)) * 8;
       const uint16_t* kro = kre - (jr & 4) * 16;
-      f32x4_t s[2][2];  // [head block][k-step parity]: four independent accumulator chains
-#pragma unroll
-      for (int b = 0; b < 2; ++b) s[b][0] = s[b][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      uint4 kf[KS];  // the whole tile's K fragments (and the validity of its keys) are read first
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[ks] = *(const uint4*)((ks & 1 ? kro : kre) + ks * 32);
       const uint16_t* const* rp = rptr[t % NBUF];
       bool ok[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) ok[i] = rp[16 * kb + 4 * g + i] != nullptr;
-      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+      uint4 kf[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *(const uint4*)((ks & 1 ? kro : kre) + ks * 32);
+      f32x4_t s[2][2];  // [head block][k-step parity]: four independent accumulator chains
+#pragma unroll
+      for (int b = 0; b < 2; ++b) s[b][0] = s[b][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         s[0][ks & 1] = mfma_bf16_16x16x32(kf[ks], qf[0][ks], s[0][ks & 1]);
         s[1][ks & 1] = mfma_bf16_16x16x32(kf[ks], qf[1][ks], s[1][ks & 1]);
       }
-      // sc[b][i]: key 16kb + 4g + i of the tile, head 32hb + 16b + l16 (scaled to log2 units, masked)
-      float sc[2][4];
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {  // partial maxima of the 4 keys of this lane
-        float tm = -1e30f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sc[b][i] = ok[i] ? (s[b][0][i] + s[b][1][i]) * sl2 : -1e30f;
-          tm = fmaxf(tm, sc[b][i]);
-        }
-        xmax[kb][g][32 * hb + 16 * b + l16] = tm;
-      }
-      PF_TS(2, 0);
-      // pairwise exchange with wave w ^ 2 (same heads, other key half): LDS operations of a wave complete in order,
-      // so the flag is seen after the maxima; the partner read this wave's previous maxima before its B0
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): maxima written
-      if (lane == 0) __hip_atomic_store(&xflag[wave], t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      for (int spin = 0;  // bounded
-           __hip_atomic_load(&xflag[wave ^ 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < t + 1 && spin < (1 << 22);
-           ++spin)
-        __builtin_amdgcn_s_sleep(1);
-      __asm__ volatile("" ::: "memory");  // the partner's maxima are read after the flag
-      PF_TS(3, 0);
+      // softmax of tile t - 1 (at t == 0: scp = -1e30 and the maxima slot holds -1e30, so nothing changes)
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         const int hl = 32 * hb + 16 * b + l16;
-        float tmax = xmax[0][0][hl];
+        float tmax = xm[b][0];
 #pragma unroll
-        for (int u = 1; u < 8; ++u) tmax = fmaxf(tmax, xmax[u >> 2][u & 3][hl]);
+        for (int u = 1; u < 8; ++u) tmax = fmaxf(tmax, xm[b][u]);
         const float m_new = tmax > m_ref[b] + kRescale ? tmax : m_ref[b];
         const float alpha = __builtin_amdgcn_exp2f(m_ref[b] - m_new);  // v_exp_f32: arguments <= 0 here
         l_run[b] *= alpha;
         m_ref[b] = m_new;
-        if (kb == 0 && g == 0) salpha[t & 1][hl] = alpha;
+        if (kb == 0 && g == 0) salpha[tp & 1][hl] = alpha;
         float p[4], psum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          p[i] = __builtin_amdgcn_exp2f(sc[b][i] - m_new);  // masked keys: 2^(-1e30 - m) = 0
+          p[i] = __builtin_amdgcn_exp2f(scp[b][i] - m_new);  // masked keys: 2^(-1e30 - m) = 0
           psum += p[i];
         }
-        pex[t & 1][2 * hb + b][kb][lane] = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
+        pex[tp & 1][2 * hb + b][kb][lane] = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
         l_run[b] += psum;  // this lane's keys only; summed over the lane groups at the end
       }
+      PF_TS(2, 0);
+      // scores of tile t, scaled to log2 units and masked; partial maxima of the 4 keys of this lane
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        float tm = -1e30f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          scp[b][i] = ok[i] ? (s[b][0][i] + s[b][1][i]) * sl2 : -1e30f;
+          tm = fmaxf(tm, scp[b][i]);
+        }
+        xmax[t & 1][kb][g][32 * hb + 16 * b + l16] = tm;
+      }
+      PF_TS(3, 0);
     }
     // per-head sums over both key halves and the 4 lane groups, normalisation factors
     __syncthreads();  // E1: every wave is past its last read of xmax
-    xmax[kb][g][32 * hb + l16] = l_run[0];
-    xmax[kb][g][32 * hb + 16 + l16] = l_run[1];
+    xmax[0][kb][g][32 * hb + l16] = l_run[0];
+    xmax[0][kb][g][32 * hb + 16 + l16] = l_run[1];
     lds_barrier();  // QK waves only see each other's sums after this (the PV waves pass it too)
     if (kb == 0 && g == 0) {
 #pragma unroll
@@ -1137,7 +1144,7 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
         const int hl = 32 * hb + 16 * b + l16, h = hg64 * 64 + hl;
         float l = 0.0f;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) l += xmax[u >> 2][u & 3][hl];
+        for (int u = 0; u < 8; ++u) l += xmax[0][u >> 2][u & 3][hl];
         if (a.nsplit > 1) {  // split partial: normalised by its own sum; m (natural-log units) and l for the merge
           hfac[hl] = l > 0.0f ? 1.0f / l : 0.0f;
           if (h < H) {
@@ -1152,22 +1159,16 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
     }
     __syncthreads();  // E3
   } else {
-    // gathers: LDS chunk position cc = rd*256 + cq*64 + lane holds chunk (cc % U) ^ (row & 7) of row cc / U; the
-    // (row, byte offset) of each load is fixed per lane, packed as row << 16 | offset
-    uint32_t gsrc[kLd];
-#pragma unroll
-    for (int rd = 0; rd < kLd; ++rd) {
-      const int cc = rd * 256 + cq * 64 + lane;
-      const int j = cc / U, cs = cc - j * U;
-      gsrc[rd] = ((uint32_t)j << 16) | (uint32_t)((cs ^ (j & 7)) * 16);
-    }
+    // gathers: LDS chunk position cc = rd*256 + cq*64 + lane holds chunk (cc % U) ^ (row & 7) of row cc / U
     const uint16_t* src[kLd];  // gather sources of a tile, read before the first load (the loads clobber memory)
     auto sources = [&](int ti) {
       const uint16_t* const* rp = rptr[ti % NBUF];
 #pragma unroll
       for (int rd = 0; rd < kLd; ++rd) {
-        const uint16_t* p = rp[gsrc[rd] >> 16];
-        src[rd] = p ? (const uint16_t*)((const char*)p + (gsrc[rd] & 0xffff)) : g_zero_row;
+        const int cc = rd * 256 + cq * 64 + lane;
+        const int j = cc / U, cs = cc - j * U;
+        const uint16_t* p = rp[j];
+        src[rd] = p ? p + (cs ^ (j & 7)) * 8 : g_zero_row;
       }
     };
     auto dma = [&](int ti, int rd) {  // direct-to-LDS 16-byte load (inline assembly: no compiler waits around it)
@@ -1192,7 +1193,14 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
     }
     const int vj = 4 * g + (l16 >> 2);  // key rows vj (first half) and vj + 16 (second half); (vj + 16) & 7 = vj & 7
     const int vsw = vj & 7;
-    for (int t = 0; t <= ntiles; ++t) {
+    uint4 vb[CT];  // V fragments of tile t - 2, read in iteration t - 1
+    // element offsets in a V row of column tiles ct = c4 and c4 + 4: chunk (cq DV/32 + 2 ct + h01) ^ vsw with
+    // h01 = (l16 & 3) >> 1; the swizzle only permutes the low three chunk bits, so tile c4 + 4 lies 8 chunks (64
+    // elements) after tile c4
+    int voff[4];
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) voff[c4] = ((cq * (DV / 32) + 2 * c4 + ((l16 & 3) >> 1)) ^ vsw) * 8;
+    for (int t = 0; t <= ntiles + 1; ++t) {
       PF_TS(8, 256);
       if (t < ntiles) {
         if (t + 1 < ntiles)
@@ -1203,21 +1211,22 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
       PF_TS(9, 256);
       lds_barrier();  // B0
       PF_TS(10, 256);
-      // PV of tile t - 1, interleaved with the gathers of tile t + 2 into buffer (t + 2) % NBUF (free since the PV of
-      // tile t - 2; its pointers were resolved in iteration t - 1)
-      const int tp = t - 1;
-      const bool mm = t >= 1, gather = t + 2 < ntiles;
+      // PV of tile t - 2 (P written in iteration t - 1, V read into registers in iteration t - 1), interleaved with
+      // the gathers of tile t + 2 into buffer (t + 2) % NBUF (tile t - 2's: every read of it ended before B0; its
+      // pointers were resolved in iteration t - 1); then the V fragments of tile t - 1
+      const int tp = t - 2;
+      const bool mm = t >= 2, gather = t + 2 < ntiles;
       if (gather) sources(t + 2);
-      const uint16_t* vrow = ktile + (tp % NBUF) * TILE_ELEMS + vj * DQK + ((l16 & 1) << 2);
-      auto vread = [&](int ct) {
-        const int cch = ((cq * (DV / 4) + ct * 16) >> 3) + ((l16 & 3) >> 1);
-        const uint2 v0 = lds_read_tr16(vrow + ((cch ^ vsw) << 3));
-        const uint2 v1 = lds_read_tr16(vrow + 16 * DQK + ((cch ^ vsw) << 3));
+      const uint16_t* vrow = ktile + ((t + NBUF - 1) % NBUF) * TILE_ELEMS + vj * DQK + ((l16 & 1) << 2);
+      auto vread = [&](int ct) {  // column tile ct: chunk 2 ct + h01 (+ the wave's quarter), swizzled
+        const uint16_t* p = vrow + voff[ct & 3] + (ct >> 2) * 64;
+        const uint2 v0 = lds_read_tr16(p);
+        const uint2 v1 = lds_read_tr16(p + 16 * DQK);
         return make_uint4(v0.x, v0.y, v1.x, v1.y);
       };
-      // every LDS read of the tile first (rescale factors of heads 16b + 4g .. + 3, P fragments, V fragments),
-      // before the gathers (which clobber memory): one LDS latency per tile
-      uint4 pa[4], vb[CT];
+      // the LDS reads of the iteration first (rescale factors of heads 16b + 4g .. + 3, P fragments), before the
+      // gathers (which clobber memory)
+      uint4 pa[4];
       float4 al[4];
       if (mm) {
 #pragma unroll
@@ -1228,8 +1237,6 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
           const uint2 p0 = pex[tp & 1][b][0][lane], p1 = pex[tp & 1][b][1][lane];
           pa[b] = make_uint4(p0.x, p0.y, p1.x, p1.y);
         }
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) vb[ct] = vread(ct);
       }
       __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
       if (mm) {  // rescale by the factors of tile t - 1 (rarely needed: skipped unless some factor differs from 1)
@@ -1257,6 +1264,11 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
 #pragma unroll
           for (int b = 0; b < 4; ++b) o[b][ct] = mfma_bf16_16x16x32(pa[b], vb[ct], o[b][ct]);
         }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // (after the MFMAs: the fragments are overwritten)
+      if (t >= 1 && t <= ntiles) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) vb[ct] = vread(ct);
       }
       PF_TS(11, 256);
     }
