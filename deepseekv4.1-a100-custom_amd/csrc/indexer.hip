@@ -23,6 +23,11 @@ __global__ void __launch_bounds__(64 * WV) index_score_kernel(const ScoreArgs a,
   const int bxcd = blockIdx.x % kXcds, bj = blockIdx.x / kXcds;
   const int by = bj % a.R, bx = (bj / a.R) * kXcds + bxcd;
   if (bx >= nx) return;
+  if (!a.write_masked) {  // a workgroup wholly past its row's valid count has nothing to score or count
+    long cl0 = row_cl(a, by);
+    if (cl0 > a.n_pos) cl0 = a.n_pos;
+    if ((long)bx * (WV * kKeysPerWave) >= cl0) return;
+  }
   DSV41_TS(30);
   DSV41_WG_TS(0);
   if (by == 0) DSV41_PH(0);
