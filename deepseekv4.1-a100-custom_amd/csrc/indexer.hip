@@ -14,6 +14,8 @@
 // Keys at positions >= cl are never read: the scan is bounded by the valid count, not the allocated capacity.
 #include "score_core.h"
 
+#include <type_traits>
+
 namespace {
 
 template <int KFMT, bool HIST, int WV = 4>
@@ -148,6 +150,157 @@ __global__ void __launch_bounds__(64 * WV) index_score_kernel(const ScoreArgs a,
   }
   if (by == 0) DSV41_PH(4);
   DSV41_WG_TS(1);
+}
+
+// Decode rows with e4m3 keys and a histogram, many rows of different lengths (ragged slots, draft rows): the
+// work items are the (row, 256-key chunk) pairs below each row's valid count, numbered per XCD: chunk c of every
+// row belongs to XCD c mod 8 (so the draft rows of one sequence read a chunk's keys through one L2), and workgroup
+// m of an XCD takes that XCD's items m, m + M, ... (M workgroups per XCD).  The grid is sized for the machine, not
+// for the longest row (a one-chunk-per-workgroup grid spends most of its time dispatching workgroups with nothing
+// to score), and the keys and query of a workgroup's next item are loaded while the current one is scored.  Per
+// item: one 256-key chunk against the row's query, the scores, and the LDS histogram added to the row's (the flush
+// clears it for the next item).
+constexpr int kLoopMaxRows = 64;
+__global__ void __launch_bounds__(256) index_score_items_kernel(const ScoreArgs a) {
+  const int x = blockIdx.x % kXcds, m = blockIdx.x / kXcds, M = gridDim.x / kXcds;
+  __shared__ int lhist[kHistBins];
+  __shared__ int pre[kLoopMaxRows + 1];  // items of XCD x in rows < r
+  __shared__ int rlim[kLoopMaxRows];     // valid count of row r (clamped to n_pos)
+  __shared__ long rslot[kLoopMaxRows];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+#pragma unroll 1
+  for (int i = threadIdx.x; i < kHistBins; i += 256) lhist[i] = 0;
+  if (wave == 0) {
+    int cnt = 0;
+    if (lane < a.R) {
+      long cl = row_cl(a, lane);
+      if (cl > a.n_pos) cl = a.n_pos;
+      const int nx = (int)((cl + kKeysPerWG - 1) / kKeysPerWG);
+      cnt = nx > x ? (nx - x + kXcds - 1) / kXcds : 0;
+      rlim[lane] = (int)cl;
+      rslot[lane] = a.seq ? a.seq[lane] : (long)(lane / a.rows_per_slot);
+    }
+    const int inc = wave_incl_scan(cnt);
+    if (lane < a.R) pre[lane + 1] = inc;
+    if (lane == 0) pre[0] = 0;
+  }
+  __syncthreads();
+  const int total = pre[a.R];
+  const int nht = (a.HI + 15) / 16;
+  constexpr int NT = 4;
+  struct Item {
+    int r, kt0, lim;
+    long slot;
+  };
+  auto locate = [&](int j) {  // item j of this XCD (wave-uniform)
+    const bool le = lane < a.R && pre[lane] <= j;
+    Item it;
+    it.r = __popcll(__ballot(le)) - 1;
+    it.kt0 = (x + kXcds * (j - pre[it.r])) * kKeysPerWG + wave * kKeysPerWave;
+    it.lim = rlim[it.r];
+    it.slot = rslot[it.r];
+    return it;
+  };
+  // two item buffers, selected by a compile-time index (constant subscripts keep everything in VGPRs)
+  uint4 k0[2][NT], k1[2][NT];
+  float ksc[2][NT], wl[2][kHT];
+  i32x8_t qa8[2][kHT];
+  auto load = [&](auto bufc, const Item& it) {
+    constexpr int U = decltype(bufc)::value;  // (positions past the row's count read its last valid key)
+    const uint8_t* kbase = (const uint8_t*)a.keys + it.slot * a.k_sstride + g * 32;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      int t = it.kt0 + nt * 16 + l16;
+      t = t < it.lim ? t : it.lim - 1;
+      const uint8_t* krow = kbase + (long)t * 128;
+      k0[U][nt] = *(const uint4*)krow;
+      k1[U][nt] = *(const uint4*)(krow + 16);
+      ksc[U][nt] = a.kscale[it.slot * a.ks_sstride + t];
+    }
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht) {
+      const int h = ht * 16 + l16;
+      const bool hv = ht < nht && h < a.HI;
+      const int hc = hv ? h : 0;
+      const uint4* qrow = (const uint4*)((const uint8_t*)a.q + (long)it.r * a.q_rstride + (long)hc * 128 + g * 32);
+      const uint4 u0 = qrow[0], u1 = qrow[1];
+      qa8[U][ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+      wl[U][ht] = a.w[(long)it.r * a.w_rstride + hc];
+      if (!hv) wl[U][ht] = 0.0f;
+    }
+  };
+  auto process = [&](auto bufc, const Item& it) {
+    constexpr int U = decltype(bufc)::value;
+    uint4 qa16[kHT][4];  // (unused: e4m3 keys)
+    float wr[kHT][4];
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[U][ht], 4 * g + i, 64);
+    float* orow = a.out + (long)it.r * a.out_rstride;
+    float sum[NT];  // (all tiles' MFMAs first: constant indices, nothing dynamic left for scratch)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) sum[nt] = score_tile<1>(qa8[U], qa16, wr, nht, k0[U][nt], k1[U][nt], nullptr);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int t = it.kt0 + nt * 16 + l16;
+      if (g == 0 && t < it.lim) {
+        const float v = is_cand(a, it.r, t) ? sum[nt] * ksc[U][nt] : -__builtin_inff();
+        orow[t] = v;
+        atomicAdd(&lhist[score_key(v) >> 20], 1);
+      }
+    }
+  };
+  auto flush = [&](int r) {  // the LDS histogram into row r's (bins in pairs: one 64-bit add), cleared
+    __syncthreads();
+    int* gh = a.hist + (long)r * kHistBins;
+    if (((uintptr_t)gh & 7) == 0) {
+#pragma unroll 1
+      for (int i = threadIdx.x; i < kHistBins / 2; i += 256) {
+        const uint32_t lo = (uint32_t)lhist[2 * i], hi = (uint32_t)lhist[2 * i + 1];
+        if (lo | hi) {
+          atomicAdd((unsigned long long*)(gh + 2 * i), ((unsigned long long)hi << 32) | lo);
+          lhist[2 * i] = 0;
+          lhist[2 * i + 1] = 0;
+        }
+      }
+    } else {
+#pragma unroll 1
+      for (int i = threadIdx.x; i < kHistBins; i += 256) {
+        const int v = lhist[i];
+        if (v) {
+          atomicAdd(&gh[i], v);
+          lhist[i] = 0;
+        }
+      }
+    }
+    __syncthreads();
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  // workgroup m takes the contiguous items [j0, j1) of its XCD (mostly one row: the histogram is added to the
+  // row's once per row run, not per item); two items in flight: the loads of the next item are issued
+  // (unconditionally; past the last item they repeat it) before the current one is scored, so the compiler's load
+  // counts stay exact
+  const int j0 = (int)((long)m * total / M), j1 = (int)((long)(m + 1) * total / M);
+  if (j0 >= j1) return;
+  Item ia = locate(j0);
+  load(B0{}, ia);
+#pragma unroll 1
+  for (int j = j0; j < j1; j += 2) {
+    const Item ib = locate(j + 1 < j1 ? j + 1 : j);
+    load(B1{}, ib);
+    process(B0{}, ia);
+    if (j + 1 >= j1 || ib.r != ia.r) flush(ia.r);
+    const Item ia2 = locate(j + 2 < j1 ? j + 2 : j);
+    load(B0{}, ia2);
+    if (j + 1 < j1) {
+      process(B1{}, ib);
+      if (j + 2 >= j1 || ia2.r != ib.r) flush(ib.r);
+    }
+    ia = ia2;
+  }
 }
 
 // Prefill score kernel (many query rows of one sequence; e4m3 keys + prepared e4m3 queries): a workgroup owns 8
@@ -533,6 +686,27 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
   }
 }
 
+#ifndef DSV41_SCORE_LOOP
+#define DSV41_SCORE_LOOP 1
+#endif
+constexpr bool kScoreLoop = DSV41_SCORE_LOOP;
+#ifndef DSV41_SCORE_PER_CU
+#define DSV41_SCORE_PER_CU 2
+#endif
+constexpr int kScoreLoopPerCu = DSV41_SCORE_PER_CU;  // workgroups per CU of the looped decode score grid
+
+// Compute units of the current device (queried once per device; 256 when the query fails).
+int score_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
+}
+
 int launch_score(ScoreArgs& a, hipStream_t st) {
   if (a.R <= 0 || a.n_pos <= 0) return 0;
   if (a.HI <= 0 || a.HI > 64) return (int)hipErrorInvalidValue;
@@ -562,6 +736,20 @@ int launch_score(ScoreArgs& a, hipStream_t st) {
     return 0;
   }
   const int nx = (a.n_pos + kKeysPerWG - 1) / kKeysPerWG;
+  if (a.hist && a.kfmt == 1 && !a.write_masked && a.R > 4 && a.R <= kLoopMaxRows && kScoreLoop) {
+    // many rows: the valid (row, chunk) items spread over a machine-sized grid (a multiple of 8)
+    long items = (long)a.R * nx;
+#ifdef DSV41_SCORE_GRID
+    long wgs = DSV41_SCORE_GRID;
+#else
+    long wgs = (long)kScoreLoopPerCu * score_cus();
+#endif
+    if (wgs > items) wgs = items;
+    wgs = (wgs + kXcds - 1) / kXcds * kXcds;
+    index_score_items_kernel<<<dim3((unsigned)wgs), 256, 0, st>>>(a);
+    DSV41_CHECK_LAUNCH();
+    return 0;
+  }
   const dim3 grid((nx + kXcds - 1) / kXcds * kXcds * a.R);
   if (a.hist) {
     if (a.kfmt == 1) index_score_kernel<1, true><<<grid, 256, 0, st>>>(a, nx);
