@@ -1433,10 +1433,11 @@ constexpr int kFuseMaxSplits = 32;  // splits a decode launch merges itself
 #ifndef DSV41_DEC_WG
 #define DSV41_DEC_WG 192
 #endif
-constexpr int kDecWG = DSV41_DEC_WG;  // decode-kernel workgroups the split plan aims at
+constexpr int kDecWG = DSV41_DEC_WG;
+  // decode-kernel workgroups the split plan aims at
 
 // Split plan.  Decode kernel: <= 192 workgroups over (rows x 16-head groups x splits), >= 2 tiles of 64 keys per
-// split.  64-head kernel: >= 512 workgroups when rows are few, >= 2 tiles of 32 keys per split.
+// split.  64-head kernel: splits up to one workgroup per CU when rows are few, >= 2 tiles of 32 keys per split.
 void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
   const bool dec = use_decode_kernel(R, H);
   const int tile = dec ? 64 : 32;
@@ -1456,7 +1457,9 @@ void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
     return;
   } else {
     const long wgs = (long)R * ((H + 63) / 64);
-    const long target = wgs >= 256 ? 1 : (512 + wgs - 1) / wgs;
+    // one workgroup per CU (the kernel holds a CU alone): splits up to one round of the grid, no second round
+    const long cus = (long)cus_per_xcd() * kXcds > 0 ? (long)cus_per_xcd() * kXcds : 256;
+    const long target = wgs >= cus ? 1 : cus / wgs;
     per = (int)((tiles + target - 1) / target);
     if (per < 2 && target > 1) per = 2;
   }
