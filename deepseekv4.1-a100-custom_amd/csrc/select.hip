@@ -39,6 +39,7 @@ struct SelArgs {
   int* out;          // [R, k]
   long out_rstride;
   int offset;
+  int* rowbin;       // [R]: the row's threshold bin, written by select_chunks for emit_kernel
 };
 
 DSV41_DEV int row_c(const SelArgs& a, int r) {
@@ -133,6 +134,7 @@ __global__ void __launch_bounds__(256) select_chunks_kernel(const SelArgs a) {
   }
   find_threshold_bin(a.hist + (long)r * kBins, a.k, tmp, &s_bin, &s_above);
   const int B = s_bin;
+  if (ch == 0 && tid == 0 && a.rowbin) a.rowbin[r] = B;
   uint32_t key[4];
   int n_above = 0, n_cand = 0;
 #pragma unroll
@@ -334,6 +336,275 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
   for (int i = tot + tid; i < k; i += kFinThreads) orow[i] = -1;
 #pragma unroll 1
   for (int i = tid; i < kBins; i += kFinThreads) gh[i] = 0;
+}
+
+// Per-chunk emission (replaces finalize for rows of few chunk groups): grid (chunks, rows) as select_chunks.  Every
+// workgroup of a row resolves the row's exact threshold itself -- the chunk counts, the candidates' keys (bin B, in
+// index order) and two 10-bit radix passes over them in LDS -- then counts per chunk the candidates above / equal to
+// the threshold key, and from the prefix over earlier chunks of (above B + taken candidates) writes its own chunk's
+// taken positions in index order (it re-reads its 1024 scores).  Ties at the threshold go to the lowest positions.
+// The work is proportional to the candidates (a few percent of the row) per workgroup, and the row's workgroups run
+// in parallel where finalize ran one workgroup per row.  Workgroup 0 of the row clears its histogram (this kernel
+// reads the threshold bin select_chunks stored, not the histogram).
+constexpr int kEmitCap = 8192;  // candidate keys staged in LDS (more: read from the workspace)
+#ifndef DSV41_EMIT
+#define DSV41_EMIT 1
+#endif
+constexpr bool kEmit = DSV41_EMIT;
+#ifndef DSV41_EMIT_MAX_GRID
+#define DSV41_EMIT_MAX_GRID 2048
+#endif
+constexpr long kEmitMaxGrid = DSV41_EMIT_MAX_GRID;  // emit grids up to this many workgroups (each redoes the radix)
+__global__ void __launch_bounds__(256) emit_kernel(const SelArgs a) {
+  __shared__ uint32_t ck[kEmitCap];
+  __shared__ uint16_t owner[kEmitCap];  // chunk of staged candidate j
+  __shared__ int pa[1025], pc[1025];  // exclusive prefixes of above / candidates over the row's chunks
+  __shared__ int cout[1024], ceq[1024];  // per chunk: output offset, equal candidates in earlier chunks
+  __shared__ int hist[1024];
+  __shared__ int tmp[16];
+  __shared__ int s_digit, s_rem;
+  DSV41_TS(0);
+  const int ch = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+  const int c = row_c(a, r), k = a.k;
+  int* orow = a.out + (long)r * a.out_rstride;
+  int* gh = a.hist + (long)r * kBins;
+  if (c <= k) {  // every valid position, then -1
+    if (ch == 0) {
+#pragma unroll 1
+      for (int i = tid; i < k; i += 256) orow[i] = i < c ? i + a.offset : -1;
+#pragma unroll 1
+      for (int i = tid; i < kBins; i += 256) gh[i] = 0;
+    }
+    return;
+  }
+  const int nch = (c + kChunk - 1) / kChunk;
+  if (ch >= nch) return;
+  // chunk scores (4 consecutive positions per thread), loaded first
+  const int p0 = ch * kChunk + 4 * tid;
+  const float* srow = a.score + (long)r * a.ld;
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = srow[p0 + e < c ? p0 + e : 0];
+  const int B = a.rowbin[r];
+  DSV41_TS(1);
+  // ---- chunk counts -> prefixes (thread t: chunks 4t .. 4t+3)
+  int na[4], nc[4], la = 0, lc = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int q = 4 * tid + u;
+    na[u] = nc[u] = 0;
+    if (q < nch) {
+      const int2 cv = *(const int2*)(a.counts + ((long)r * a.nchunks + q) * 2);
+      na[u] = cv.x;
+      nc[u] = cv.y;
+    }
+    la += na[u];
+    lc += nc[u];
+  }
+  int tot_a, tot_c;
+  int ea = block_scan<256>(la, tmp, &tot_a);
+  int ec = block_scan<256>(lc, tmp, &tot_c);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int q = 4 * tid + u;
+    if (q <= nch) {
+      pa[q] = ea;
+      pc[q] = ec;
+    }
+    ea += na[u];
+    ec += nc[u];
+  }
+  if (tid == 0) {  // (nch == 1024: the loop above stops at chunk 1023)
+    pa[nch] = tot_a;
+    pc[nch] = tot_c;
+  }
+  if (ch == 0) {
+#pragma unroll 1
+    for (int i = tid; i < kBins; i += 256) gh[i] = 0;
+  }
+  __syncthreads();
+  DSV41_TS(2);
+  const int need = k - tot_a;  // candidates to take (<= 0: the above entries alone reach k)
+  const bool staged = tot_c <= kEmitCap;
+  const long reg = (long)r * a.rs;
+  auto chunk_of = [&](int j) {  // last chunk q with pc[q] <= j
+    int lo = 0, hi = nch - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pc[mid] <= j) lo = mid;
+      else hi = mid - 1;
+    }
+    return lo;
+  };
+  auto key_of = [&](int j) -> uint32_t {  // (staged: ck)
+    if (staged) return ck[j];
+    const int q = chunk_of(j);
+    return a.cand_key[reg + (long)q * kChunk + (j - pc[q])];
+  };
+  uint32_t T = 0xffffffffu;  // threshold key (candidates above it are taken, `remaining` equal ones)
+  int remaining = 0;
+  if (need > 0) {
+    if (staged) {
+      // owner[j] = chunk of candidate j (thread t fills its chunks' ranges), then every key load is independent
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int q = 4 * tid + u;
+        if (q < nch)
+#pragma unroll 1
+          for (int j = pc[q]; j < pc[q + 1]; ++j) owner[j] = (uint16_t)q;
+      }
+      __syncthreads();
+#pragma unroll 1
+      for (int j0 = 0; j0 < tot_c; j0 += 8 * 256) {
+        uint32_t kv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int j = j0 + u * 256 + tid;
+          const int q = j < tot_c ? owner[j] : 0;
+          kv[u] = j < tot_c ? a.cand_key[reg + (long)q * kChunk + (j - pc[q])] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int j = j0 + u * 256 + tid;
+          if (j < tot_c) ck[j] = kv[u];
+        }
+      }
+    }
+    // radix select of the need-th largest candidate on the low 20 key bits (the bin fixes the top 12)
+    uint32_t prefix = 0u, pmask = 0u;
+    remaining = need;
+#pragma unroll 1
+    for (int pass = 0; pass < 2; ++pass) {
+      const int shift = pass == 0 ? 10 : 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) hist[4 * tid + u] = 0;
+      __syncthreads();
+#pragma unroll 1
+      for (int j = tid; j < tot_c; j += 256) {
+        const uint32_t d = key_of(j) & 0xfffffu;
+        if ((d & pmask) == prefix) atomicAdd(&hist[(d >> shift) & 1023], 1);
+      }
+      __syncthreads();
+      // thread t owns bins 1023 - 4t .. 1020 - 4t (high to low)
+      int hb[4], local = 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        hb[u] = hist[1023 - 4 * tid - u];
+        local += hb[u];
+      }
+      int total;
+      int greater = block_scan<256>(local, tmp, &total);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (greater < remaining && remaining <= greater + hb[u]) {
+          s_digit = 1023 - 4 * tid - u;
+          s_rem = remaining - greater;
+        }
+        greater += hb[u];
+      }
+      __syncthreads();
+      prefix |= (uint32_t)s_digit << shift;
+      pmask |= 1023u << shift;
+      remaining = s_rem;
+      __syncthreads();
+    }
+    T = ((uint32_t)B << 20) | prefix;
+  }
+  DSV41_TS(4);
+  // ---- per chunk: candidates above / equal to T (thread t: chunks 4t .. 4t+3)
+  {
+    int g4[4], e4[4];
+    if (staged) {  // one thread per candidate, LDS counters per chunk
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        cout[4 * tid + u] = 0;
+        ceq[4 * tid + u] = 0;
+      }
+      __syncthreads();
+      if (need > 0) {
+#pragma unroll 1
+        for (int j = tid; j < tot_c; j += 256) {
+          const uint32_t key = ck[j];
+          if (key > T) atomicAdd(&cout[owner[j]], 1);
+          else if (key == T) atomicAdd(&ceq[owner[j]], 1);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        g4[u] = cout[4 * tid + u];
+        e4[u] = ceq[4 * tid + u];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int q = 4 * tid + u;
+        g4[u] = e4[u] = 0;
+        if (q < nch && need > 0) {
+#pragma unroll 1
+          for (int j = pc[q]; j < pc[q + 1]; ++j) {
+            const uint32_t key = key_of(j);
+            g4[u] += key > T;
+            e4[u] += key == T;
+          }
+        }
+      }
+    }
+    int le = e4[0] + e4[1] + e4[2] + e4[3], tot_e;
+    int eb = block_scan<256>(le, tmp, &tot_e);  // equal candidates in earlier chunks
+    int taken[4], lt = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      int t = remaining - eb;
+      t = t < 0 ? 0 : (t > e4[u] ? e4[u] : t);
+      taken[u] = na[u] + g4[u] + t;
+      ceq[4 * tid + u] = eb;
+      eb += e4[u];
+      lt += taken[u];
+    }
+    int tot_t;
+    int ob = block_scan<256>(lt, tmp, &tot_t);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      cout[4 * tid + u] = ob;
+      ob += taken[u];
+    }
+  }
+  __syncthreads();
+  DSV41_TS(5);
+  const int out0 = cout[ch], eq0 = ceq[ch];
+  // ---- this chunk's taken positions in index order
+  int nt = 0, ne = 0;
+  bool is_eq[4], take[4];
+  uint32_t key[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const bool in = p0 + e < c;
+    key[e] = score_key(v[e]);
+    const int b = (int)(key[e] >> 20);
+    is_eq[e] = in && need > 0 && b == B && key[e] == T;
+    take[e] = in && (b > B || (need > 0 && b == B && key[e] > T));
+    ne += is_eq[e];
+  }
+  int tot_e2;
+  int er = eq0 + block_scan<256>(ne, tmp, &tot_e2);  // rank of this thread's first equal candidate
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (is_eq[e]) {
+      take[e] = er < remaining;
+      ++er;
+    }
+    nt += take[e];
+  }
+  int tot_t2;
+  int o = out0 + block_scan<256>(nt, tmp, &tot_t2);
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (take[e]) {
+      if (o < k) orow[o] = p0 + e + a.offset;
+      ++o;
+    }
+  DSV41_TS(6);
 }
 
 // ------------------------------------------------------------------------------------------------ one launch
@@ -567,11 +838,11 @@ __global__ void __launch_bounds__(256) select_group_kernel(const GroupArgs g) {
 
 // Workspace: histograms [R, kBins] | chunk counts [R, nch, 2] | above, candidate positions, candidate keys [R, rs]
 // each (rs = n rounded up to 32, so rows never share a cache line; the one-launch path uses the first two as 64-bit
-// candidate slots [R, rs]) | arrival counters [R] (64-bit) | timeout flag.
+// candidate slots [R, rs]) | threshold bins [R] (padded to 8 bytes) | arrival counters [R] (64-bit) | timeout flag.
 long row_stride(int n) { return ((long)n + 31) / 32 * 32; }
 long select_base_bytes(int R, int n) {
   const long nch = (n + kChunk - 1) / kChunk;
-  return ((long)R * kBins + (long)R * nch * 2 + 3L * R * row_stride(n)) * 4;
+  return ((long)R * kBins + (long)R * nch * 2 + 3L * R * row_stride(n) + (R + 1L) / 2 * 2) * 4;  // (+ row bins)
 }
 
 }  // namespace
@@ -624,9 +895,14 @@ int dsv41_select_topk(const float* score, long ld, int R, int n, int k, const lo
     DSV41_CHECK_LAUNCH();
     return 0;
   }
+  a.rowbin = (int*)(a.cand_key + (long)R * a.rs);
   select_chunks_kernel<<<dim3(nch, R), 256, 0, st>>>(a);
   DSV41_CHECK_LAUNCH();
-  finalize_kernel<<<R, kFinThreads, 0, st>>>(a);
+  if ((long)R * nch <= kEmitMaxGrid && kEmit) {  // few rows: every chunk's workgroup emits its own positions
+    emit_kernel<<<dim3(nch, R), 256, 0, st>>>(a);
+  } else {
+    finalize_kernel<<<R, kFinThreads, 0, st>>>(a);
+  }
   DSV41_CHECK_LAUNCH();
   return 0;
 }
