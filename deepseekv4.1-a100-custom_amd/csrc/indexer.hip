@@ -304,14 +304,17 @@ __global__ void __launch_bounds__(256) index_score_items_kernel(const ScoreArgs 
 }
 
 // Prefill score kernel (many query rows of one sequence; e4m3 keys + prepared e4m3 queries): a workgroup owns 8
-// consecutive query rows (2 per wave) and a range of key positions, streamed through LDS in 256-key chunks
-// (direct-to-LDS loads, double buffered) and shared by the 4 waves.  Per 16-key column tile a wave runs
-// 2 rows x 4 head tiles 16x16x128 fp8 MFMAs on one B fragment.  Key tiles past a row's causal limit are skipped.
-constexpr int kPQ = 8;       // query rows per workgroup
+// consecutive query rows (one per wave, 8 waves) and a range of key positions, streamed through LDS in 256-key chunks
+// (direct-to-LDS loads, double buffered) and shared by the 8 waves.  Per step a wave runs its row's 4 head tiles of
+// 16x16x128 fp8 MFMAs on two 16-key B fragments, then the two epilogues (ReLU, weighted head sum).  One row per wave
+// keeps a wave under 128 VGPRs: four waves per SIMD hide the MFMA and LDS latencies of each other's steps (two rows
+// per wave held 228 VGPRs, two waves per SIMD).  Key tiles past a row's causal limit are skipped.
+constexpr int kPQ = 8;        // query rows per workgroup
+constexpr int kPThreads = 512;
 constexpr int kPChunk = 256;  // keys per LDS chunk (32 KB)
 
 template <int NHT>  // 16-head tiles: ceil(HI / 16)
-__global__ void __launch_bounds__(256) index_score_prefill_kernel(const ScoreArgs a, int key_split) {
+__global__ void __launch_bounds__(kPThreads, 2) index_score_prefill_kernel(const ScoreArgs a, int key_split) {
   __shared__ __align__(16) uint8_t kbuf[2][kPChunk * 128];
   __shared__ float sbuf[2][kPChunk];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -319,7 +322,7 @@ __global__ void __launch_bounds__(256) index_score_prefill_kernel(const ScoreArg
   const int r0 = blockIdx.y * kPQ;
   const int slot = r0 / a.rows_per_slot;  // all rows of a block belong to one sequence (host-checked)
   // causal limits of the block's rows (increasing with the row)
-  long cl_lo = row_cl(a, r0), cl_hi = row_cl(a, min(r0 + kPQ, a.R) - 1);
+  long cl_hi = row_cl(a, min(r0 + kPQ, a.R) - 1);
   if (cl_hi > a.n_pos) cl_hi = a.n_pos;
   const int span = (a.n_pos + key_split - 1) / key_split;
   const int kb0 = blockIdx.x * span;
@@ -328,50 +331,48 @@ __global__ void __launch_bounds__(256) index_score_prefill_kernel(const ScoreArg
   const uint8_t* kbase = (const uint8_t*)a.keys + (long)slot * a.k_sstride;
   const float* sbase = a.kscale + (long)slot * a.ks_sstride;
   const int nchunks = (kb1 - kb0 + kPChunk - 1) / kPChunk;
-  auto issue = [&](int ci) {  // 256 keys x 128 B = 2048 chunks of 16 B: 8 per thread; + 256 scales
+  auto issue = [&](int ci) {  // 256 keys x 128 B = 2048 chunks of 16 B: 4 per thread; + 256 scales
     const int c0 = kb0 + ci * kPChunk;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 4; ++u) {
       // LDS unit q holds key q / 8, 16-byte part (q % 8) ^ (key % 8) (XOR swizzle against bank conflicts)
-      const int q = u * 256 + threadIdx.x;
+      const int q = u * kPThreads + threadIdx.x;
       const int kl = q >> 3;
       int key = c0 + kl;
       key = key < kb1 ? key : kb1 - 1;
       __builtin_amdgcn_global_load_lds((const void*)(kbase + (long)key * 128 + ((q & 7) ^ (kl & 7)) * 16),
-                                       (void*)(kbuf[ci & 1] + (u * 256 + wave * 64) * 16), 16, 0, 0);
+                                       (void*)(kbuf[ci & 1] + (u * kPThreads + wave * 64) * 16), 16, 0, 0);
     }
-    int key = c0 + threadIdx.x;
-    key = key < kb1 ? key : kb1 - 1;
-    __builtin_amdgcn_global_load_lds((const void*)(sbase + key), (void*)(sbuf[ci & 1] + wave * 64), 4, 0, 0);
+    if (wave < 4) {
+      int key = c0 + threadIdx.x;
+      key = key < kb1 ? key : kb1 - 1;
+      __builtin_amdgcn_global_load_lds((const void*)(sbase + key), (void*)(sbuf[ci & 1] + wave * 64), 4, 0, 0);
+    }
   };
   issue(0);
-  // query fragments of this wave's 2 rows and their head weights
-  i32x8_t qa[2][kHT];
-  float wr[2][kHT][4];
+  // query fragments of this wave's row and its head weights
+  i32x8_t qa[kHT];
+  float wr[kHT][4];
   constexpr int nht = NHT;
-#pragma unroll
-  for (int qq = 0; qq < 2; ++qq) {
-    const int r = min(r0 + wave * 2 + qq, a.R - 1);
+  const int row = r0 + wave;
+  {
+    const int r = min(row, a.R - 1);
 #pragma unroll
     for (int ht = 0; ht < kHT; ++ht) {
       const int h = ht * 16 + l16;
       const bool hv = ht < nht && h < a.HI;
       const uint4* qrow = (const uint4*)((const uint8_t*)a.q + (long)r * a.q_rstride + (long)(hv ? h : 0) * 128 + g * 32);
       const uint4 u0 = qrow[0], u1 = qrow[1];
-      qa[qq][ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+      qa[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
       const float wv = hv ? a.w[(long)r * a.w_rstride + h] : 0.0f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) wr[qq][ht][i] = __shfl(wv, 4 * g + i, 64);
+      for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wv, 4 * g + i, 64);
     }
   }
-  int rows[2];
-  long clr[2];
-#pragma unroll
-  for (int qq = 0; qq < 2; ++qq) {
-    rows[qq] = r0 + wave * 2 + qq;
-    clr[qq] = rows[qq] < a.R ? row_cl(a, rows[qq]) : 0;
-    if (clr[qq] > a.n_pos) clr[qq] = a.n_pos;
-  }
+  long clr = row < a.R ? row_cl(a, row) : 0;
+  if (clr > a.n_pos) clr = a.n_pos;
+  const long wave_lim = clr < kb1 ? clr : kb1;
+  float* orow = a.out + (long)(row < a.R ? row : 0) * a.out_rstride;
   for (int ci = 0; ci < nchunks; ++ci) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -379,14 +380,13 @@ __global__ void __launch_bounds__(256) index_score_prefill_kernel(const ScoreArg
     const int c0 = kb0 + ci * kPChunk;
     const uint8_t* kb = kbuf[ci & 1];
     const float* sb = sbuf[ci & 1];
-    const long wave_lim = clr[1] > clr[0] ? clr[1] : clr[0];
-    // two 16-key tiles per step: all 2 x 2 x NHT MFMAs first, then the epilogues (the first tile's VALU work covers
+    // two 16-key tiles per step: all 2 x NHT MFMAs first, then the epilogues (the first tile's VALU work covers
     // the second tile's MFMA latency)
 #pragma unroll 1
     for (int kt = 0; kt < kPChunk / 16; kt += 2) {
       const int t0 = c0 + kt * 16;
-      if (t0 >= kb1 || t0 >= wave_lim) break;  // wave-uniform
-      f32x4_t acc[2][2][kHT];  // [tile][row][head tile]
+      if (t0 >= wave_lim) break;  // wave-uniform
+      f32x4_t acc[2][kHT];  // [tile][head tile]
       float ksc[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -397,31 +397,24 @@ __global__ void __launch_bounds__(256) index_score_prefill_kernel(const ScoreArg
                                       (int)k1.w};
         ksc[u] = sb[kl];
 #pragma unroll
-        for (int qq = 0; qq < 2; ++qq)
-#pragma unroll
-          for (int ht = 0; ht < nht; ++ht)
-            acc[u][qq][ht] = mfma_fp8_16x16x128(qa[qq][ht], bfrag, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
+        for (int ht = 0; ht < nht; ++ht)
+          acc[u][ht] = mfma_fp8_16x16x128(qa[ht], bfrag, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
       }
       // every MFMA of the step is issued before the epilogues start (the empty statements pin the results here)
       if constexpr (NHT == 4)
-        __asm__ volatile("" : "+v"(acc[0][0][0]), "+v"(acc[0][0][1]), "+v"(acc[0][0][2]), "+v"(acc[0][0][3]),
-                         "+v"(acc[0][1][0]), "+v"(acc[0][1][1]), "+v"(acc[0][1][2]), "+v"(acc[0][1][3]),
-                         "+v"(acc[1][0][0]), "+v"(acc[1][0][1]), "+v"(acc[1][0][2]), "+v"(acc[1][0][3]),
-                         "+v"(acc[1][1][0]), "+v"(acc[1][1][1]), "+v"(acc[1][1][2]), "+v"(acc[1][1][3]));
+        __asm__ volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[0][2]), "+v"(acc[0][3]), "+v"(acc[1][0]),
+                         "+v"(acc[1][1]), "+v"(acc[1][2]), "+v"(acc[1][3]));
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int t = t0 + u * 16 + l16;
+        float sum = 0.0f;
 #pragma unroll
-        for (int qq = 0; qq < 2; ++qq) {
-          float sum = 0.0f;
+        for (int ht = 0; ht < nht; ++ht)
 #pragma unroll
-          for (int ht = 0; ht < nht; ++ht)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sum += wr[qq][ht][i] * relu(acc[u][qq][ht][i]);
-          sum = row_sum4(sum);
-          if (g == 0 && rows[qq] < a.R && t < clr[qq] && t < kb1)
-            a.out[(long)rows[qq] * a.out_rstride + t] = is_cand(a, rows[qq], t) ? sum * ksc[u] : -__builtin_inff();
-        }
+          for (int i = 0; i < 4; ++i) sum += wr[ht][i] * relu(acc[u][ht][i]);
+        sum = row_sum4(sum);
+        if (g == 0 && row < a.R && t < wave_lim)
+          orow[t] = is_cand(a, row, t) ? sum * ksc[u] : -__builtin_inff();
       }
     }
   }
@@ -716,10 +709,10 @@ int launch_score(ScoreArgs& a, hipStream_t st) {
     int split = (512 + qblocks - 1) / qblocks;
     split = split < 1 ? 1 : (split > 16 ? 16 : split);
     switch ((a.HI + 15) / 16) {
-      case 1: index_score_prefill_kernel<1><<<dim3(split, qblocks), 256, 0, st>>>(a, split); break;
-      case 2: index_score_prefill_kernel<2><<<dim3(split, qblocks), 256, 0, st>>>(a, split); break;
-      case 3: index_score_prefill_kernel<3><<<dim3(split, qblocks), 256, 0, st>>>(a, split); break;
-      default: index_score_prefill_kernel<4><<<dim3(split, qblocks), 256, 0, st>>>(a, split); break;
+      case 1: index_score_prefill_kernel<1><<<dim3(split, qblocks), kPThreads, 0, st>>>(a, split); break;
+      case 2: index_score_prefill_kernel<2><<<dim3(split, qblocks), kPThreads, 0, st>>>(a, split); break;
+      case 3: index_score_prefill_kernel<3><<<dim3(split, qblocks), kPThreads, 0, st>>>(a, split); break;
+      default: index_score_prefill_kernel<4><<<dim3(split, qblocks), kPThreads, 0, st>>>(a, split); break;
     }
     DSV41_CHECK_LAUNCH();
     return 0;
