@@ -965,6 +965,7 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   __shared__ uint2 pex[2][4][2][64];  // [tile parity][head block][key block][lane]
   __shared__ float xmax[2][2][4][64];  // [tile parity][key half][lane group][head]: partial maxima; at the end sums
   __shared__ __align__(16) float salpha[2][64];  // [tile parity][head]: rescale factor (1 when the reference stays)
+  __shared__ __align__(16) int srescale[2][4];    // [tile parity][head block]: some factor differs from 1
   __shared__ float hfac[64];
 
   const int hg64 = blockIdx.y;
@@ -1110,6 +1111,10 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
         l_run[b] *= alpha;
         m_ref[b] = m_new;
         if (kb == 0 && g == 0) salpha[tp & 1][hl] = alpha;
+        if (kb == 0) {  // one word per head block: did any of its heads move its reference (the PV waves' test)
+          const unsigned long long moved = __ballot(alpha != 1.0f);
+          if (lane == 0) srescale[tp & 1][2 * hb + b] = moved != 0;
+        }
         float p[4], psum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -1224,14 +1229,14 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
         const uint2 v1 = lds_read_tr16(p + 16 * DQK);
         return make_uint4(v0.x, v0.y, v1.x, v1.y);
       };
-      // the LDS reads of the iteration first (rescale factors of heads 16b + 4g .. + 3, P fragments), before the
-      // gathers (which clobber memory)
+      // the LDS reads of the iteration first (the head blocks' rescale words, P fragments), before the gathers
+      // (which clobber memory)
       uint4 pa[4];
-      float4 al[4];
+      int4 resc = make_int4(0, 0, 0, 0);
       if (mm) {
+        resc = *(const int4*)srescale[tp & 1];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          al[b] = *(const float4*)&salpha[tp & 1][16 * b + 4 * g];
           // 16x16x32 MFMA over the tile's 32 keys in the k order (4g + i, then 16 + 4g + i): the A operand of
           // head block b is its two 16-key probability fragments side by side, the B operand two transposed V reads
           const uint2 p0 = pex[tp & 1][b][0][lane], p1 = pex[tp & 1][b][1][lane];
@@ -1239,17 +1244,18 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
         }
       }
       __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
-      if (mm) {  // rescale by the factors of tile t - 1 (rarely needed: skipped unless some factor differs from 1)
+      if (mm && (resc.x | resc.y | resc.z | resc.w)) {  // rescale by the factors of tile t - 2 (rarely needed)
+        const int rb[4] = {resc.x, resc.y, resc.z, resc.w};
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const bool any = al[b].x != 1.0f || al[b].y != 1.0f || al[b].z != 1.0f || al[b].w != 1.0f;
-          if (__ballot(any)) {
+          if (rb[b]) {
+            const float4 al = *(const float4*)&salpha[tp & 1][16 * b + 4 * g];
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) {
-              o[b][ct][0] *= al[b].x;
-              o[b][ct][1] *= al[b].y;
-              o[b][ct][2] *= al[b].z;
-              o[b][ct][3] *= al[b].w;
+              o[b][ct][0] *= al.x;
+              o[b][ct][1] *= al.y;
+              o[b][ct][2] *= al.z;
+              o[b][ct][3] *= al.w;
             }
           }
         }
