@@ -961,7 +961,8 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   static_assert(64 * DV * 4 <= NBUF * TILE_ELEMS * 2, "output staging fits the tile buffers");
   constexpr float kRescale = 8.0f;
   __shared__ __align__(16) uint16_t ktile[NBUF * TILE_ELEMS];
-  __shared__ const uint16_t* rptr[NBUF][TILE];
+  __shared__ const uint16_t* rptr[NBUF][TILE];  // row of each key (the zero row when invalid: no test per gather)
+  __shared__ uint32_t rvalid[NBUF];            // bit j: key j of the tile is valid
   __shared__ uint2 pex[2][4][2][64];  // [tile parity][head block][key block][lane]
   __shared__ float xmax[2][2][4][64];  // [tile parity][key half][lane group][head]: partial maxima; at the end sums
   __shared__ __align__(16) float salpha[2][64];  // [tile parity][head]: rescale factor (1 when the reference stays)
@@ -1020,7 +1021,9 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
           p = ix < a.n1 ? base1 + (long)ix * DQK : base2 + (long)(ix - a.n1) * DQK;
         }
       }
-      rptr[ti % NBUF][lane & 31] = p;
+      rptr[ti % NBUF][lane & 31] = p ? p : g_zero_row;
+      const uint32_t bits = (uint32_t)(__ballot(p != nullptr) >> (32 * (ti & 1)));
+      if ((lane & 31) == 0) rvalid[ti % NBUF] = bits;
     }
   };
 
@@ -1084,10 +1087,10 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
       // base addresses and immediate offsets
       const uint16_t* kre = buf + jr * DQK + ((g ^ (jr & 3)) + (jr & 4)) * 8;
       const uint16_t* kro = kre - (jr & 4) * 16;
-      const uint16_t* const* rp = rptr[t % NBUF];
+      const uint32_t vbits = rvalid[t % NBUF] >> (16 * kb + 4 * g);
       bool ok[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ok[i] = rp[16 * kb + 4 * g + i] != nullptr;
+      for (int i = 0; i < 4; ++i) ok[i] = (vbits >> i) & 1u;
       uint4 kf[KS];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kf[ks] = *(const uint4*)((ks & 1 ? kro : kre) + ks * 32);
@@ -1172,8 +1175,7 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
       for (int rd = 0; rd < kLd; ++rd) {
         const int cc = rd * 256 + cq * 64 + lane;
         const int j = cc / U, cs = cc - j * U;
-        const uint16_t* p = rp[j];
-        src[rd] = p ? p + (cs ^ (j & 7)) * 8 : g_zero_row;
+        src[rd] = rp[j] + (cs ^ (j & 7)) * 8;  // (invalid keys: the zero row, read whole)
       }
     };
     auto dma = [&](int ti, int rd) {  // direct-to-LDS 16-byte load (inline assembly: no compiler waits around it)
