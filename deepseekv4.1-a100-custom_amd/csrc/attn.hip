@@ -1178,8 +1178,10 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
         src[rd] = rp[j] + (cs ^ (j & 7)) * 8;  // (invalid keys: the zero row, read whole)
       }
     };
+    // LDS byte address of this wave's first chunk in buffer 0 (wave-uniform, computed once)
+    const uint32_t wlds = lds_addr_of(ktile) + (uint32_t)(cq * 64 * 16);
     auto dma = [&](int ti, int rd) {  // direct-to-LDS 16-byte load (inline assembly: no compiler waits around it)
-      lds_dma16(src[rd], ktile + (ti % NBUF) * TILE_ELEMS + (rd * 256 + cq * 64) * 8);
+      lds_dma16_at(src[rd], wlds + (uint32_t)(((ti % NBUF) * TILE_ELEMS + rd * 256 * 8) * 2));
     };
     // O of heads 16b + 4g + i, columns cq*DV/4 + 16 ct + l16
     f32x4_t o[4][CT];

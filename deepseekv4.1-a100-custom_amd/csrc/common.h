@@ -179,6 +179,17 @@ __device__ long long g_dsv41_px[1024][32];
 // accesses across it.
 DSV41_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// As lds_dma16, with the destination given as a wave-uniform LDS byte address (no generic-to-LDS conversion per
+// load: the caller computes the workgroup's LDS base once).
+DSV41_DEV void lds_dma16_at(const void* src, uint32_t lds_addr) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr);  // (an SGPR operand: uniform values may sit in VGPRs)
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+}
+// LDS byte address of a __shared__ object.
+DSV41_DEV uint32_t lds_addr_of(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)p);
+}
+
 // 16-byte direct-to-LDS load: lane i writes lds_dst + 16 i (lds_dst is wave-uniform).  Issued as inline assembly
 // so the compiler does not treat later LDS reads as dependent on it (it would wait for every outstanding load
 // before them); callers wait for these loads with explicit vmcnt counts.  Compiler-tracked loads are unaffected:
