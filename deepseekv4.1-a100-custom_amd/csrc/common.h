@@ -194,9 +194,10 @@ DSV41_DEV uint32_t lds_addr_of(const void* p) {
 // so the compiler does not treat later LDS reads as dependent on it (it would wait for every outstanding load
 // before them); callers wait for these loads with explicit vmcnt counts.  Compiler-tracked loads are unaffected:
 // loads complete in order, so the compiler's own waits only become stricter.
+// The LDS address is the low 32 bits of the flat address of an LDS object (the LDS aperture sits in the high
+// half), taken without the address-space conversion's null test.
 DSV41_DEV void lds_dma16(const void* src, void* lds_dst) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds_dst);
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_dst);
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
 }
 
