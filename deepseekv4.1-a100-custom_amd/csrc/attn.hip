@@ -1032,8 +1032,14 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
     resolve(0, p0);
     resolve(1, p0);
     resolve(2, p1);
+    resolve(3, p1);  // (every slot holds valid pointers: the gathers past the row read through stale slots)
   }
   (&xmax[1][0][0][0])[tid] = -1e30f;  // (512 entries: the maxima "of tile -1")
+  // zero probabilities and rescale words "of tiles -2 and -1": the PV waves' first two iterations multiply zeros
+  // instead of branching around their MFMAs
+#pragma unroll
+  for (int u = 0; u < 4; ++u) ((uint32_t*)&pex[0][0][0][0])[u * 512 + tid] = 0u;
+  if (tid < 8) (&srescale[0][0])[tid] = 0;
   float* stg = (float*)ktile;  // output staging [64 heads][DV] once the tiles are done
 #define PF_TS(k, thr) \
   if (t >= 30 && t < 34) DSV41_TST(16 * (t - 30) + (k), thr)
@@ -1202,7 +1208,9 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
     }
     const int vj = 4 * g + (l16 >> 2);  // key rows vj (first half) and vj + 16 (second half); (vj + 16) & 7 = vj & 7
     const int vsw = vj & 7;
-    uint4 vb[CT];  // V fragments of tile t - 2, read in iteration t - 1
+    uint4 vb[CT];  // V fragments of tile t - 2, read in iteration t - 1 (zero before the first)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) vb[ct] = make_uint4(0, 0, 0, 0);
     // element offsets in a V row of column tiles ct = c4 and c4 + 4: chunk (cq DV/32 + 2 ct + h01) ^ vsw with
     // h01 = (l16 & 3) >> 1; the swizzle only permutes the low three chunk bits, so tile c4 + 4 lies 8 chunks (64
     // elements) after tile c4
@@ -1223,9 +1231,10 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
       // PV of tile t - 2 (P written in iteration t - 1, V read into registers in iteration t - 1), interleaved with
       // the gathers of tile t + 2 into buffer (t + 2) % NBUF (tile t - 2's: every read of it ended before B0; its
       // pointers were resolved in iteration t - 1); then the V fragments of tile t - 1
+      // (near the end the gathers of tiles past the row land in buffers no wave reads again, from row pointers
+      // left by earlier tiles: no branch per load; E1 waits for them before the buffers take the output)
       const int tp = t - 2;
-      const bool mm = t >= 2, gather = t + 2 < ntiles;
-      if (gather) sources(t + 2);
+      sources(t + 2);
       const uint16_t* vrow = ktile + ((t + NBUF - 1) % NBUF) * TILE_ELEMS + vj * DQK + ((l16 & 1) << 2);
       auto vread = [&](int ct) {  // column tile ct: chunk 2 ct + h01 (+ the wave's quarter), swizzled
         const uint16_t* p = vrow + voff[ct & 3] + (ct >> 2) * 64;
@@ -1236,8 +1245,8 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
       // the LDS reads of the iteration first (the head blocks' rescale words, P fragments), before the gathers
       // (which clobber memory)
       uint4 pa[4];
-      int4 resc = make_int4(0, 0, 0, 0);
-      if (mm) {
+      int4 resc;
+      {
         resc = *(const int4*)srescale[tp & 1];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
@@ -1248,7 +1257,7 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
         }
       }
       __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
-      if (mm && (resc.x | resc.y | resc.z | resc.w)) {  // rescale by the factors of tile t - 2 (rarely needed)
+      if (resc.x | resc.y | resc.z | resc.w) {  // rescale by the factors of tile t - 2 (rarely needed)
         const int rb[4] = {resc.x, resc.y, resc.z, resc.w};
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
@@ -1266,14 +1275,10 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
       }
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        if (gather) {
 #pragma unroll
-          for (int rd = ct * kLd / CT; rd < (ct + 1) * kLd / CT; ++rd) dma(t + 2, rd);
-        }
-        if (mm) {
+        for (int rd = ct * kLd / CT; rd < (ct + 1) * kLd / CT; ++rd) dma(t + 2, rd);
 #pragma unroll
-          for (int b = 0; b < 4; ++b) o[b][ct] = mfma_bf16_16x16x32(pa[b], vb[ct], o[b][ct]);
-        }
+        for (int b = 0; b < 4; ++b) o[b][ct] = mfma_bf16_16x16x32(pa[b], vb[ct], o[b][ct]);
       }
       __builtin_amdgcn_sched_barrier(0);  // (after the MFMAs: the fragments are overwritten)
       if (t >= 1 && t <= ntiles) {
