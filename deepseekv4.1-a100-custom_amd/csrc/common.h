@@ -185,6 +185,11 @@ DSV41_DEV void lds_dma16_at(const void* src, uint32_t lds_addr) {
   const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr);  // (an SGPR operand: uniform values may sit in VGPRs)
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
 }
+// As lds_dma16_at, 4 bytes per lane (lane i writes lds_addr + 4 i).
+DSV41_DEV void lds_dma4_at(const void* src, uint32_t lds_addr) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+}
 // LDS byte address of a __shared__ object.
 DSV41_DEV uint32_t lds_addr_of(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)p);

@@ -167,10 +167,14 @@ __global__ void __launch_bounds__(256) index_score_items_kernel(const ScoreArgs 
   __shared__ int pre[kLoopMaxRows + 1];  // items of XCD x in rows < r
   __shared__ int rlim[kLoopMaxRows];     // valid count of row r (clamped to n_pos)
   __shared__ long rslot[kLoopMaxRows];
+  __shared__ __align__(16) uint8_t qlds[2][64 * 128];  // the next rows' queries (direct-to-LDS), alternating
+  __shared__ float wlds[2][64];                        // and their head weights
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
 #pragma unroll 1
   for (int i = threadIdx.x; i < kHistBins; i += 256) lhist[i] = 0;
+#pragma unroll 1
+  for (int i = threadIdx.x; i < 2 * 64 * 128 / 16; i += 256) ((uint4*)qlds)[i] = make_uint4(0, 0, 0, 0);
   if (wave == 0) {
     int cnt = 0;
     if (lane < a.R) {
@@ -202,46 +206,87 @@ __global__ void __launch_bounds__(256) index_score_items_kernel(const ScoreArgs 
     it.slot = rslot[it.r];
     return it;
   };
-  // two item buffers, selected by a compile-time index (constant subscripts keep everything in VGPRs)
+  // Byte order of the 128-byte rows in the MFMA operands: lane group g holds bytes [16g, 16g+16) and
+  // [64+16g, 64+16g+16) of its key / query row (the same permutation of the dot product's terms on both sides),
+  // so one 16-byte load instruction reads one 64-byte half row per key: half the cache accesses of 32-byte
+  // groups at stride 32.
+  // Two key buffers, selected by a compile-time index (constant subscripts keep everything in VGPRs); the query
+  // fragments and weights of the current row stay in VGPRs for the row's run of items.
   uint4 k0[2][NT], k1[2][NT];
-  float ksc[2][NT], wl[2][kHT];
-  i32x8_t qa8[2][kHT];
+  float ksc[2][NT];
+  float hmask[kHT][4];  // 1 for the heads (ht*16 + 4g + i) below HI, else 0
+#pragma unroll
+  for (int ht = 0; ht < kHT; ++ht)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hmask[ht][i] = (ht < nht && ht * 16 + 4 * g + i < a.HI) ? 1.0f : 0.0f;
+  i32x8_t qa8[kHT];
+  float wr[kHT][4];
   auto load = [&](auto bufc, const Item& it) {
     constexpr int U = decltype(bufc)::value;  // (positions past the row's count read its last valid key)
-    const uint8_t* kbase = (const uint8_t*)a.keys + it.slot * a.k_sstride + g * 32;
+    const uint8_t* kbase = (const uint8_t*)a.keys + it.slot * a.k_sstride + g * 16;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       int t = it.kt0 + nt * 16 + l16;
       t = t < it.lim ? t : it.lim - 1;
       const uint8_t* krow = kbase + (long)t * 128;
       k0[U][nt] = *(const uint4*)krow;
-      k1[U][nt] = *(const uint4*)(krow + 16);
+      k1[U][nt] = *(const uint4*)(krow + 64);
       ksc[U][nt] = a.kscale[it.slot * a.ks_sstride + t];
     }
+  };
+  auto load_q = [&](int r) {  // query fragments and masked, shuffled head weights of row r
+    float wl[kHT];
 #pragma unroll
     for (int ht = 0; ht < kHT; ++ht) {
       const int h = ht * 16 + l16;
-      const bool hv = ht < nht && h < a.HI;
-      const int hc = hv ? h : 0;
-      const uint4* qrow = (const uint4*)((const uint8_t*)a.q + (long)it.r * a.q_rstride + (long)hc * 128 + g * 32);
-      const uint4 u0 = qrow[0], u1 = qrow[1];
-      qa8[U][ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
-      wl[U][ht] = a.w[(long)it.r * a.w_rstride + hc];
-      if (!hv) wl[U][ht] = 0.0f;
+      const int hc = (ht < nht && h < a.HI) ? h : 0;
+      const uint8_t* qrow = (const uint8_t*)a.q + (long)r * a.q_rstride + (long)hc * 128 + g * 16;
+      const uint4 u0 = *(const uint4*)qrow, u1 = *(const uint4*)(qrow + 64);
+      qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+      wl[ht] = a.w[(long)r * a.w_rstride + hc];
     }
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[ht], 4 * g + i, 64) * hmask[ht][i];
+  };
+  // the query of row r into qlds[p] / wlds[p] (direct-to-LDS; heads past HI are not read and stay zero), waited
+  // for by the next flush (vmcnt(0) before its barrier)
+  auto dma_q = [&](int r, int p) {
+    const uint32_t qb = lds_addr_of(&qlds[p][0]);
+    const uint8_t* qrow = (const uint8_t*)a.q + (long)r * a.q_rstride;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int c = k * 256 + wave * 64 + lane;  // 16-byte chunk: head c / 8
+      if (c < a.HI * 8) lds_dma16_at(qrow + c * 16, qb + (uint32_t)(k * 256 + wave * 64) * 16);
+    }
+    if (wave == 0) {
+      const float* wsrc = a.w + (long)r * a.w_rstride + (lane < a.HI ? lane : a.HI - 1);
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr_of(&wlds[p][0]));
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(wsrc), "s"(m0) : "memory", "m0");
+    }
+  };
+  auto q_from_lds = [&](int p) {  // (after a barrier that follows the loads' completion)
+    float wl[kHT];
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht) {
+      const uint8_t* qrow = &qlds[p][(ht * 16 + l16) * 128 + g * 16];
+      const uint4 u0 = *(const uint4*)qrow, u1 = *(const uint4*)(qrow + 64);
+      qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+      wl[ht] = wlds[p][ht * 16 + l16];
+    }
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[ht], 4 * g + i, 64) * hmask[ht][i];
   };
   auto process = [&](auto bufc, const Item& it) {
     constexpr int U = decltype(bufc)::value;
     uint4 qa16[kHT][4];  // (unused: e4m3 keys)
-    float wr[kHT][4];
-#pragma unroll
-    for (int ht = 0; ht < kHT; ++ht)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[U][ht], 4 * g + i, 64);
     float* orow = a.out + (long)it.r * a.out_rstride;
     float sum[NT];  // (all tiles' MFMAs first: constant indices, nothing dynamic left for scratch)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) sum[nt] = score_tile<1>(qa8[U], qa16, wr, nht, k0[U][nt], k1[U][nt], nullptr);
+    for (int nt = 0; nt < NT; ++nt) sum[nt] = score_tile<1>(qa8, qa16, wr, nht, k0[U][nt], k1[U][nt], nullptr);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int t = it.kt0 + nt * 16 + l16;
@@ -253,6 +298,7 @@ __global__ void __launch_bounds__(256) index_score_items_kernel(const ScoreArgs 
     }
   };
   auto flush = [&](int r) {  // the LDS histogram into row r's (bins in pairs: one 64-bit add), cleared
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0): a pending query load has landed
     __syncthreads();
     int* gh = a.hist + (long)r * kHistBins;
     if (((uintptr_t)gh & 7) == 0) {
@@ -280,27 +326,47 @@ __global__ void __launch_bounds__(256) index_score_items_kernel(const ScoreArgs 
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
   // workgroup m takes the contiguous items [j0, j1) of its XCD (mostly one row: the histogram is added to the
-  // row's once per row run, not per item); two items in flight: the loads of the next item are issued
-  // (unconditionally; past the last item they repeat it) before the current one is scored, so the compiler's load
-  // counts stay exact
+  // row's once per row run, and the query is loaded once per row run); two items in flight: the keys of the next
+  // item are loaded (unconditionally; past the last item they repeat it) while the current one is scored
   const int j0 = (int)((long)m * total / M), j1 = (int)((long)(m + 1) * total / M);
   if (j0 >= j1) return;
   Item ia = locate(j0);
   load(B0{}, ia);
+  load_q(ia.r);
+  int qp = 0;  // qlds buffer of the next row change
+  DSV41_PX(0);
 #pragma unroll 1
   for (int j = j0; j < j1; j += 2) {
+    const int pi = (j - j0) / 2;
+    if (pi < 7) DSV41_PX(1 + 4 * pi);
     const Item ib = locate(j + 1 < j1 ? j + 1 : j);
     load(B1{}, ib);
+    const bool swb = j + 1 < j1 && ib.r != ia.r;
+    if (swb) dma_q(ib.r, qp);
     process(B0{}, ia);
-    if (j + 1 >= j1 || ib.r != ia.r) flush(ia.r);
+    if (pi < 7) DSV41_PX(2 + 4 * pi);
+    if (j + 1 >= j1 || swb) flush(ia.r);
+    if (swb) {
+      q_from_lds(qp);
+      qp ^= 1;
+    }
     const Item ia2 = locate(j + 2 < j1 ? j + 2 : j);
     load(B0{}, ia2);
+    const bool swa = j + 2 < j1 && ia2.r != ib.r;
+    if (swa) dma_q(ia2.r, qp);
+    if (pi < 7) DSV41_PX(3 + 4 * pi);
     if (j + 1 < j1) {
       process(B1{}, ib);
-      if (j + 2 >= j1 || ia2.r != ib.r) flush(ib.r);
+      if (pi < 7) DSV41_PX(4 + 4 * pi);
+      if (j + 2 >= j1 || swa) flush(ib.r);
+      if (swa) {
+        q_from_lds(qp);
+        qp ^= 1;
+      }
     }
     ia = ia2;
   }
+  DSV41_PX(31);
 }
 
 // Prefill score kernel (many query rows of one sequence; e4m3 keys + prepared e4m3 queries): a workgroup owns 8
@@ -331,6 +397,9 @@ __global__ void __launch_bounds__(kPThreads, 2) index_score_prefill_kernel(const
   const uint8_t* kbase = (const uint8_t*)a.keys + (long)slot * a.k_sstride;
   const float* sbase = a.kscale + (long)slot * a.ks_sstride;
   const int nchunks = (kb1 - kb0 + kPChunk - 1) / kPChunk;
+  // (direct-to-LDS loads as inline assembly: the compiler does not wait for them before every LDS read; the
+  // chunk loop waits for them explicitly)
+  const uint32_t kb_lds = lds_addr_of(&kbuf[0][0]), sb_lds = lds_addr_of(&sbuf[0][0]);
   auto issue = [&](int ci) {  // 256 keys x 128 B = 2048 chunks of 16 B: 4 per thread; + 256 scales
     const int c0 = kb0 + ci * kPChunk;
 #pragma unroll
@@ -340,13 +409,13 @@ __global__ void __launch_bounds__(kPThreads, 2) index_score_prefill_kernel(const
       const int kl = q >> 3;
       int key = c0 + kl;
       key = key < kb1 ? key : kb1 - 1;
-      __builtin_amdgcn_global_load_lds((const void*)(kbase + (long)key * 128 + ((q & 7) ^ (kl & 7)) * 16),
-                                       (void*)(kbuf[ci & 1] + (u * kPThreads + wave * 64) * 16), 16, 0, 0);
+      lds_dma16_at(kbase + (long)key * 128 + ((q & 7) ^ (kl & 7)) * 16,
+                   kb_lds + (uint32_t)((ci & 1) * kPChunk * 128 + (u * kPThreads + wave * 64) * 16));
     }
     if (wave < 4) {
       int key = c0 + threadIdx.x;
       key = key < kb1 ? key : kb1 - 1;
-      __builtin_amdgcn_global_load_lds((const void*)(sbase + key), (void*)(sbuf[ci & 1] + wave * 64), 4, 0, 0);
+      lds_dma4_at(sbase + key, sb_lds + (uint32_t)((ci & 1) * kPChunk + wave * 64) * 4);
     }
   };
   issue(0);
@@ -407,17 +476,270 @@ __global__ void __launch_bounds__(kPThreads, 2) index_score_prefill_kernel(const
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int t = t0 + u * 16 + l16;
-        float sum = 0.0f;
+        float part[kHT] = {0.0f, 0.0f, 0.0f, 0.0f};  // one chain per head tile
 #pragma unroll
         for (int ht = 0; ht < nht; ++ht)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) sum += wr[ht][i] * relu(acc[u][ht][i]);
+          for (int i = 0; i < 4; ++i) part[ht] += wr[ht][i] * relu(acc[u][ht][i]);
+        float sum = (part[0] + part[1]) + (part[2] + part[3]);
         sum = row_sum4(sum);
         if (g == 0 && row < a.R && t < wave_lim)
           orow[t] = is_cand(a, row, t) ? sum * ksc[u] : -__builtin_inff();
       }
     }
   }
+}
+
+// Decode rows with e4m3 keys and a histogram, grouped by sequence (a sequence's draft rows are consecutive rows with
+// the same slot): a group is a run of up to 8 consecutive rows of one slot, and its key chunks (256 keys, the
+// group's longest valid count) are streamed through LDS once for all its rows (direct-to-LDS loads, double
+// buffered) while wave w scores row w of the group against them with its query fragments in VGPRs (the prefill
+// kernel's layout, one workgroup of 8 waves per CU).  Work items are the (group, chunk) pairs, numbered per XCD
+// (chunk c on XCD c mod 8) and taken in contiguous runs.  Each row's histogram is counted in LDS as 16-bit bins
+// (two per word; a run adds at most 255 chunks of 256 keys to a bin before it is flushed) and added to the row's
+// device histogram when the run leaves the group.  Rows of other layouts form groups of one row (correct, slower).
+constexpr int kGRows = 6;                          // rows per group
+constexpr int kGSplit = 2;                         // waves per row (each scores a 1/kGSplit slice of the chunk)
+constexpr int kGThreads = 64 * kGRows * kGSplit;   // 12 waves: three per SIMD
+constexpr int kGFlushItems = 255;  // chunks counted into the 16-bit bins between flushes
+
+__global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const ScoreArgs a) {
+  __shared__ __align__(16) uint8_t kbuf[2][kPChunk * 128];
+  __shared__ float sbuf[2][kPChunk];
+  __shared__ uint32_t gh[kGRows][kHistBins / 2];
+  __shared__ int gstart[kLoopMaxRows + 1];  // group g: rows [gstart[g], gstart[g + 1])
+  __shared__ int gpre[kLoopMaxRows + 1];    // items of this XCD in groups < g
+  __shared__ int glim[kLoopMaxRows];        // longest valid count of group g (clamped to n_pos)
+  __shared__ long gslot[kLoopMaxRows];
+  __shared__ int rlim[kLoopMaxRows];
+  __shared__ int ngroups;
+  const int x = blockIdx.x % kXcds, m = blockIdx.x / kXcds, M = gridDim.x / kXcds;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  DSV41_PX(0);
+#pragma unroll 1
+  for (int i = threadIdx.x; i < kGRows * kHistBins / 2; i += kGThreads) (&gh[0][0])[i] = 0;
+  if (wave == 0) {
+    // groups: runs of equal slots, split every 8 rows
+    const bool in = lane < a.R;
+    long s = 0;
+    int cl = 0;
+    if (in) {
+      s = a.seq ? a.seq[lane] : (long)(lane / a.rows_per_slot);
+      long c = row_cl(a, lane);
+      cl = (int)(c > a.n_pos ? a.n_pos : c);
+      rlim[lane] = cl;
+    }
+    const long sp = __shfl_up(s, 1, 64);
+    const bool head = in && (lane == 0 || sp != s);
+    const unsigned long long below = (2ull << lane) - 1;  // lanes <= this one
+    const unsigned long long hm = __ballot(head) & below;
+    const int run0 = 63 - __builtin_clzll(hm | 1ull);
+    const bool head2 = in && ((lane - run0) % kGRows == 0);
+    const unsigned long long h2 = __ballot(head2);
+    const int gi = __popcll(h2 & below) - 1;
+    const int G = __popcll(h2);
+    // the group's longest count: a max over its rows (at most 8 consecutive lanes)
+    int gl = cl;
+#pragma unroll
+    for (int d = 1; d < kGRows; d <<= 1) {
+      const int o = __shfl_down(gl, d, 64);
+      const int og = __shfl_down(gi, d, 64);
+      if (lane + d < a.R && og == gi) gl = gl > o ? gl : o;
+    }
+    if (head2) {
+      gstart[gi] = lane;
+      glim[gi] = gl;
+      gslot[gi] = s;
+    }
+    if (lane == 0) {
+      gstart[G] = a.R;
+      ngroups = G;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int G = ngroups;
+    int cnt = 0;
+    if (lane < G) {
+      const int nx = (glim[lane] + kPChunk - 1) / kPChunk;
+      cnt = nx > x ? (nx - x + kXcds - 1) / kXcds : 0;
+    }
+    const int inc = wave_incl_scan(cnt);
+    if (lane < G) gpre[lane + 1] = inc;
+    if (lane == 0) gpre[0] = 0;
+  }
+  __syncthreads();
+  const int G = ngroups;
+  const int total = gpre[G];
+  DSV41_PX(1);
+  const int j0 = (int)((long)m * total / M), j1 = (int)((long)(m + 1) * total / M);
+  if (j0 >= j1) return;
+  struct Item {
+    int grp, c0;
+  };
+  auto locate = [&](int j) {  // (workgroup-uniform)
+    const bool le = lane < G && gpre[lane] <= j;
+    Item it;
+    it.grp = __popcll(__ballot(le)) - 1;
+    it.c0 = (x + kXcds * (j - gpre[it.grp])) * kPChunk;
+    return it;
+  };
+  // (direct-to-LDS loads as inline assembly: the compiler does not wait for them before every LDS read; the
+  // loop waits for them explicitly)
+  const uint32_t kb_lds = lds_addr_of(&kbuf[0][0]), sb_lds = lds_addr_of(&sbuf[0][0]);
+  auto issue = [&](const Item& it, int buf) {  // 256 keys x 128 B: 4 16-byte units per thread; + 256 scales
+    const long slot = gslot[it.grp];
+    const int lim = glim[it.grp];
+    const uint8_t* kbase = (const uint8_t*)a.keys + slot * a.k_sstride;
+#pragma unroll
+    for (int u = 0; u < (kPChunk * 8 + kGThreads - 1) / kGThreads; ++u) {
+      // LDS unit q holds key q / 8, 16-byte part (q % 8) ^ (key % 8) (XOR swizzle against bank conflicts)
+      const int q = u * kGThreads + threadIdx.x;
+      if (u * kGThreads + wave * 64 >= kPChunk * 8) break;  // (wave-uniform)
+      const int kl = q >> 3;
+      int key = it.c0 + kl;
+      key = key < lim ? key : lim - 1;
+      lds_dma16_at(kbase + (long)key * 128 + ((q & 7) ^ (kl & 7)) * 16,
+                   kb_lds + (uint32_t)(buf * kPChunk * 128 + (u * kGThreads + wave * 64) * 16));
+    }
+    if (wave < 4) {
+      int key = it.c0 + threadIdx.x;
+      key = key < lim ? key : lim - 1;
+      lds_dma4_at(a.kscale + slot * a.ks_sstride + key, sb_lds + (uint32_t)(buf * kPChunk + wave * 64) * 4);
+    }
+  };
+  i32x8_t qa[kHT];
+  float wr[kHT][4];
+  auto load_q = [&](int r) {
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht) {
+      const int h = ht * 16 + l16;
+      const bool hv = h < a.HI;
+      const uint4* qrow = (const uint4*)((const uint8_t*)a.q + (long)r * a.q_rstride + (long)(hv ? h : 0) * 128 + g * 32);
+      const uint4 u0 = qrow[0], u1 = qrow[1];
+      qa[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+      const float wv = hv ? a.w[(long)r * a.w_rstride + h] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wv, 4 * g + i, 64);
+    }
+  };
+  auto flush = [&](int grp) {  // the group's LDS histograms into its rows' (16-bit bin pairs -> one 64-bit add)
+    __syncthreads();
+    const int rs = gstart[grp], nr = gstart[grp + 1] - rs;
+#pragma unroll 1
+    for (int w = 0; w < nr; ++w) {
+      int* dh = a.hist + (long)(rs + w) * kHistBins;
+      const bool al = ((uintptr_t)dh & 7) == 0;
+#pragma unroll 1
+      for (int i = threadIdx.x; i < kHistBins / 2; i += kGThreads) {
+        const uint32_t v = gh[w][i];
+        if (v) {
+          const uint32_t lo = v & 0xffffu, hi = v >> 16;
+          if (al) {
+            atomicAdd((unsigned long long*)(dh + 2 * i), ((unsigned long long)hi << 32) | lo);
+          } else {
+            if (lo) atomicAdd(dh + 2 * i, (int)lo);
+            if (hi) atomicAdd(dh + 2 * i + 1, (int)hi);
+          }
+          gh[w][i] = 0;
+        }
+      }
+    }
+    __syncthreads();
+  };
+  Item cur = locate(j0);
+  issue(cur, 0);
+  DSV41_PX(2);
+  int grp = -1, since = 0, row = 0, lim_r = 0;
+  const int wrow = wave % kGRows, wpart = wave / kGRows;  // this wave's row of the group and slice of the chunk
+  constexpr int kPairs = kPChunk / 32 / kGSplit;          // 32-key tile pairs per slice
+#pragma unroll 1
+  for (int j = j0; j < j1; ++j) {
+    const bool newg = cur.grp != grp;
+    const int oldg = grp;
+    if (newg) {  // the query of this wave's row of the new group (loaded before the wait below)
+      grp = cur.grp;
+      const int rs = gstart[grp], nr = gstart[grp + 1] - rs;
+      row = wrow < nr ? rs + wrow : -1;
+      lim_r = row >= 0 ? rlim[row] : 0;
+      load_q(row >= 0 ? row : rs);
+    }
+    if (j - j0 < 8) DSV41_PX(3 + 3 * (j - j0));
+    __builtin_amdgcn_s_waitcnt(0);  // this item's keys and the query have landed (and the last flush's adds)
+    __syncthreads();                // ... for every wave; every wave is done with the other buffer and the counts
+    if (j - j0 < 8) DSV41_PX(4 + 3 * (j - j0));
+    Item nxt = cur;
+    if (j + 1 < j1) {
+      nxt = locate(j + 1);
+      issue(nxt, (j + 1 - j0) & 1);
+    }
+    if ((newg && oldg >= 0) || since == kGFlushItems) {  // (after the next item's loads: its wait covers the adds)
+      flush(newg ? oldg : grp);
+      since = 0;
+    }
+    ++since;
+    const int buf = (j - j0) & 1;
+    const uint8_t* kb = kbuf[buf];
+    const float* sb = sbuf[buf];
+    const int c0 = cur.c0;
+    const int wlim = lim_r < c0 + kPChunk ? lim_r : c0 + kPChunk;
+    float* orow = a.out + (long)(row >= 0 ? row : 0) * a.out_rstride;
+    // 16-key tiles in pairs; the next pair's fragments are read from LDS before this pair's epilogue (whose LDS
+    // adds then do not hold up those reads)
+    i32x8_t bfr[2][2];
+    float bsc[2][2];
+    auto frag = [&](int kt, i32x8_t& b, float& sc) {
+      const int kl = kt * 16 + l16;
+      const uint4 k0 = *(const uint4*)(kb + kl * 128 + (((2 * g) ^ (kl & 7)) << 4));
+      const uint4 k1 = *(const uint4*)(kb + kl * 128 + (((2 * g + 1) ^ (kl & 7)) << 4));
+      b = i32x8_t{(int)k0.x, (int)k0.y, (int)k0.z, (int)k0.w, (int)k1.x, (int)k1.y, (int)k1.z, (int)k1.w};
+      sc = sb[kl];
+    };
+    const int p0 = wpart * kPairs;
+    frag(2 * p0, bfr[0][0], bsc[0][0]);
+    frag(2 * p0 + 1, bfr[0][1], bsc[0][1]);
+#pragma unroll
+    for (int pp = 0; pp < kPairs; ++pp) {
+      const int cs = pp & 1, p = p0 + pp;
+      const int t0 = c0 + p * 32;
+      if (t0 >= wlim) break;  // wave-uniform
+      f32x4_t acc[2][kHT];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int ht = 0; ht < kHT; ++ht)
+          acc[u][ht] = mfma_fp8_16x16x128(qa[ht], bfr[cs][u], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
+      if (pp + 1 < kPairs) {
+        frag(2 * p + 2, bfr[cs ^ 1][0], bsc[cs ^ 1][0]);
+        frag(2 * p + 3, bfr[cs ^ 1][1], bsc[cs ^ 1][1]);
+      }
+      __asm__ volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[0][2]), "+v"(acc[0][3]), "+v"(acc[1][0]),
+                       "+v"(acc[1][1]), "+v"(acc[1][2]), "+v"(acc[1][3]));
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = t0 + u * 16 + l16;
+        float part[kHT];
+#pragma unroll
+        for (int ht = 0; ht < kHT; ++ht) {
+          part[ht] = wr[ht][0] * relu(acc[u][ht][0]);
+#pragma unroll
+          for (int i = 1; i < 4; ++i) part[ht] += wr[ht][i] * relu(acc[u][ht][i]);
+        }
+        const float sum = row_sum4((part[0] + part[1]) + (part[2] + part[3]));
+        if (g == 0 && t < wlim) {
+          const float v = is_cand(a, row, t) ? sum * bsc[cs][u] : -__builtin_inff();
+          orow[t] = v;
+          const uint32_t bin = score_key(v) >> 20;
+          atomicAdd(&gh[wrow][bin >> 1], 1u << ((bin & 1) * 16));
+        }
+      }
+    }
+    if (j - j0 < 8) DSV41_PX(5 + 3 * (j - j0));
+    cur = nxt;
+  }
+  flush(grp);
+  DSV41_PX(31);
 }
 
 // ------------------------------------------------------------------------------------------------ top-k
@@ -683,6 +1005,10 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
 #define DSV41_SCORE_LOOP 1
 #endif
 constexpr bool kScoreLoop = DSV41_SCORE_LOOP;
+#ifndef DSV41_SCORE_GROUP
+#define DSV41_SCORE_GROUP 1
+#endif
+constexpr bool kScoreGroup = DSV41_SCORE_GROUP;
 #ifndef DSV41_SCORE_PER_CU
 #define DSV41_SCORE_PER_CU 2
 #endif
@@ -731,6 +1057,11 @@ int launch_score(ScoreArgs& a, hipStream_t st) {
   const int nx = (a.n_pos + kKeysPerWG - 1) / kKeysPerWG;
   if (a.hist && a.kfmt == 1 && !a.write_masked && a.R > 4 && a.R <= kLoopMaxRows && kScoreLoop) {
     // many rows: the valid (row, chunk) items spread over a machine-sized grid (a multiple of 8)
+    if (kScoreGroup) {
+      index_score_group_kernel<<<dim3((unsigned)((score_cus() + kXcds - 1) / kXcds * kXcds)), kGThreads, 0, st>>>(a);
+      DSV41_CHECK_LAUNCH();
+      return 0;
+    }
     long items = (long)a.R * nx;
 #ifdef DSV41_SCORE_GRID
     long wgs = DSV41_SCORE_GRID;
@@ -817,6 +1148,7 @@ long cand_nbp(int n, int bs) { return ((n + bs - 1) / bs + 3) / 4 * 4; }
 extern "C" {
 
 #ifdef DSV41_TIMING
+int dsv41_read_px_idx(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_px), sizeof(g_dsv41_px)); }
 int dsv41_read_ts_idx(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ts), sizeof(g_dsv41_ts)); }
 int dsv41_read_ph_idx(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_ph), sizeof(g_dsv41_ph)); }
 int dsv41_read_wg_idx(long long* host) { return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dsv41_wg), sizeof(g_dsv41_wg)); }

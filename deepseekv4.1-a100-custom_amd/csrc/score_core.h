@@ -62,11 +62,15 @@ DSV41_DEV float score_tile(const i32x8_t (&qa8)[kHT], const uint4 (&qa16)[kHT][4
       for (int ks = 0; ks < 4; ++ks) acc[ht] = mfma_bf16_16x16x32(qa16[ht][ks], kb16[ks], acc[ht]);
   }
   (void)nht;  // head tiles past the head count hold a valid query row with weight 0: no branches around the MFMAs
-  float sum = 0.0f;
+  float part[kHT];  // one chain per head tile (four short dependent chains instead of one of 16)
 #pragma unroll
-  for (int ht = 0; ht < kHT; ++ht)
+  for (int ht = 0; ht < kHT; ++ht) {
+    part[ht] = wr[ht][0] * relu(acc[ht][0]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sum += wr[ht][i] * relu(acc[ht][i]);
+    for (int i = 1; i < 4; ++i) part[ht] += wr[ht][i] * relu(acc[ht][i]);
+  }
+  static_assert(kHT == 4, "head tiles");
+  float sum = (part[0] + part[1]) + (part[2] + part[3]);
   sum = row_sum4(sum);
   return sum;
 }

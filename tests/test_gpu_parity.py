@@ -467,6 +467,47 @@ def test_decode_selector_end_to_end(cls):
         assert err <= 1e-2, (b, err)
 
 
+@pytest.mark.parametrize("layout", ["drafts", "interleaved"])
+def test_decode_selector_draft_rows(layout):
+    """More than four decode rows through the score kernel then the selection (n_pos > 65536): a sequence's draft
+    rows are consecutive rows of one slot (runs longer than 8 rows, a slot that reappears later, ragged counts down
+    to a few positions), or the slots interleave row by row.  Top-k == oracle top-k of the kernel's own scores
+    (bit-exact; the selection reads the kernel's histogram), scores within 1e-2 of the oracle, twice in a row
+    (the histogram is left zeroed for the next call)."""
+    from dsv41_amd.fused3 import DecodeSelector
+    from dsv41_amd.workloads import encode_e4m3_rows, fp4_round
+    g = torch.Generator(device=DEV).manual_seed(23)
+    if layout == "drafts":
+        seq_l = [0] * 6 + [1] * 6 + [2] * 3 + [3] * 11 + [4] * 2 + [0] * 2
+        base = {0: 70000, 1: 30000, 2: 513, 3: 66000, 4: 5}
+        cls = []
+        for i, s in enumerate(seq_l):
+            j = sum(1 for t in seq_l[:i] if t == s)  # draft j of its sequence: one more valid position each
+            cls.append(min(base[s] + j, 70000))
+    else:
+        seq_l = [0, 1, 2, 3] * 3
+        cls = [70000, 40000, 9000, 300, 69999, 40001, 9001, 301, 69998, 40002, 9002, 302]
+    R, H, n, k = len(seq_l), 64, 70001, 2048
+    keys = fp4_round(torch.randn(5, n, 128, generator=g, device=DEV) * 0.1)
+    keys[:, :, [5, 60]] *= 6
+    k8, ks = encode_e4m3_rows(keys)
+    q = fp4_round(torch.randn(R, 1, H, 128, generator=g, device=DEV))
+    w = (torch.randn(R, H, generator=g, device=DEV) * 0.01).to(torch.bfloat16)
+    sel = DecodeSelector(R, n, k, DEV, keep_scores=True)
+    assert not sel.one_launch
+    want = O.index_score(q.float().cpu().numpy(), k8.float().cpu().numpy(), w.float().cpu().numpy(), seq_l, cls,
+                         k_scale=ks.cpu().numpy())
+    for rep in range(2):
+        print(f"[draft rows {layout}] R {R} call {rep}", flush=True)
+        idx = sel(q, k8, w, i64(seq_l), i64(cls), k_scale=ks)
+        torch.cuda.synchronize()
+        sc = sel.score.cpu().numpy()
+        np.testing.assert_array_equal(idx.cpu().numpy()[:, 0], O.topk_indices(sc, k, cls), err_msg=f"call {rep}")
+        for b, c in enumerate(cls):
+            err = np.abs(sc[b, :c] - want[b, :c]).max() / np.abs(want[b, :c]).max()
+            assert err <= 1e-2, (b, err)
+
+
 @pytest.mark.parametrize("n,cl", [(262145, 262144), (200001, 150000)])
 def test_decode_selector_long_row(n, cl):
     """One long row (C4 shape: up to 512 chunks of 512 positions) through the one-launch indexer (forced: by default
