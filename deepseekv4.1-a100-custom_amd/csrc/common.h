@@ -94,6 +94,13 @@ DSV41_DEV float row_sum4(float x) {
   const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
+// row_sum4 of two values at once: x0's sum in lanes 0-31, x1's in lanes 32-63 (one swap of each kind for both).
+DSV41_DEV float row_sum4_pair(float x0, float x1) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0), __float_as_uint(x1), false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);  // lanes l < 32: x0[l] + x0[l+32]; else x1
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 DSV41_DEV float row_max4(float x) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));

@@ -456,7 +456,7 @@ __global__ void __launch_bounds__(kPThreads, 2) index_score_prefill_kernel(const
       const int t0 = c0 + kt * 16;
       if (t0 >= wave_lim) break;  // wave-uniform
       f32x4_t acc[2][kHT];  // [tile][head tile]
-      float ksc[2];
+      const float ksc = sb[(kt + (lane >> 5)) * 16 + l16];  // scale of the key this lane writes
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int kl = (kt + u) * 16 + l16;
@@ -464,7 +464,6 @@ __global__ void __launch_bounds__(kPThreads, 2) index_score_prefill_kernel(const
         const uint4 k1 = *(const uint4*)(kb + kl * 128 + (((2 * g + 1) ^ (kl & 7)) << 4));
         const i32x8_t bfrag = i32x8_t{(int)k0.x, (int)k0.y, (int)k0.z, (int)k0.w, (int)k1.x, (int)k1.y, (int)k1.z,
                                       (int)k1.w};
-        ksc[u] = sb[kl];
 #pragma unroll
         for (int ht = 0; ht < nht; ++ht)
           acc[u][ht] = mfma_fp8_16x16x128(qa[ht], bfrag, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
@@ -473,19 +472,22 @@ __global__ void __launch_bounds__(kPThreads, 2) index_score_prefill_kernel(const
       if constexpr (NHT == 4)
         __asm__ volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[0][2]), "+v"(acc[0][3]), "+v"(acc[1][0]),
                          "+v"(acc[1][1]), "+v"(acc[1][2]), "+v"(acc[1][3]));
+      float xs[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int t = t0 + u * 16 + l16;
         float part[kHT] = {0.0f, 0.0f, 0.0f, 0.0f};  // one chain per head tile
 #pragma unroll
         for (int ht = 0; ht < nht; ++ht)
 #pragma unroll
           for (int i = 0; i < 4; ++i) part[ht] += wr[ht][i] * relu(acc[u][ht][i]);
-        float sum = (part[0] + part[1]) + (part[2] + part[3]);
-        sum = row_sum4(sum);
-        if (g == 0 && row < a.R && t < wave_lim)
-          orow[t] = is_cand(a, row, t) ? sum * ksc[u] : -__builtin_inff();
+        xs[u] = (part[0] + part[1]) + (part[2] + part[3]);
       }
+      // both tiles' head sums in one reduction: tile (lane >> 5) in each half; lanes 0-15 and 32-47 write
+      const float sum = row_sum4_pair(xs[0], xs[1]);
+      const int uu = lane >> 5;
+      const int t = t0 + uu * 16 + l16;
+      if ((g & 1) == 0 && row < a.R && t < wave_lim)
+        orow[t] = is_cand(a, row, t) ? sum * ksc : -__builtin_inff();
     }
   }
 }
@@ -688,17 +690,17 @@ __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const S
     // 16-key tiles in pairs; the next pair's fragments are read from LDS before this pair's epilogue (whose LDS
     // adds then do not hold up those reads)
     i32x8_t bfr[2][2];
-    float bsc[2][2];
-    auto frag = [&](int kt, i32x8_t& b, float& sc) {
+    float bsc[2];  // scale of the key this lane records: tile 2p + (lane >> 5), key l16
+    auto frag = [&](int kt, i32x8_t& b) {
       const int kl = kt * 16 + l16;
       const uint4 k0 = *(const uint4*)(kb + kl * 128 + (((2 * g) ^ (kl & 7)) << 4));
       const uint4 k1 = *(const uint4*)(kb + kl * 128 + (((2 * g + 1) ^ (kl & 7)) << 4));
       b = i32x8_t{(int)k0.x, (int)k0.y, (int)k0.z, (int)k0.w, (int)k1.x, (int)k1.y, (int)k1.z, (int)k1.w};
-      sc = sb[kl];
     };
     const int p0 = wpart * kPairs;
-    frag(2 * p0, bfr[0][0], bsc[0][0]);
-    frag(2 * p0 + 1, bfr[0][1], bsc[0][1]);
+    frag(2 * p0, bfr[0][0]);
+    frag(2 * p0 + 1, bfr[0][1]);
+    bsc[0] = sb[(2 * p0 + (lane >> 5)) * 16 + l16];
 #pragma unroll
     for (int pp = 0; pp < kPairs; ++pp) {
       const int cs = pp & 1, p = p0 + pp;
@@ -711,14 +713,15 @@ __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const S
         for (int ht = 0; ht < kHT; ++ht)
           acc[u][ht] = mfma_fp8_16x16x128(qa[ht], bfr[cs][u], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
       if (pp + 1 < kPairs) {
-        frag(2 * p + 2, bfr[cs ^ 1][0], bsc[cs ^ 1][0]);
-        frag(2 * p + 3, bfr[cs ^ 1][1], bsc[cs ^ 1][1]);
+        frag(2 * p + 2, bfr[cs ^ 1][0]);
+        frag(2 * p + 3, bfr[cs ^ 1][1]);
+        bsc[cs ^ 1] = sb[(2 * p + 2 + (lane >> 5)) * 16 + l16];
       }
       __asm__ volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[0][2]), "+v"(acc[0][3]), "+v"(acc[1][0]),
                        "+v"(acc[1][1]), "+v"(acc[1][2]), "+v"(acc[1][3]));
+      float xs[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int t = t0 + u * 16 + l16;
         float part[kHT];
 #pragma unroll
         for (int ht = 0; ht < kHT; ++ht) {
@@ -726,13 +729,17 @@ __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const S
 #pragma unroll
           for (int i = 1; i < 4; ++i) part[ht] += wr[ht][i] * relu(acc[u][ht][i]);
         }
-        const float sum = row_sum4((part[0] + part[1]) + (part[2] + part[3]));
-        if (g == 0 && t < wlim) {
-          const float v = is_cand(a, row, t) ? sum * bsc[cs][u] : -__builtin_inff();
-          orow[t] = v;
-          const uint32_t bin = score_key(v) >> 20;
-          atomicAdd(&gh[wrow][bin >> 1], 1u << ((bin & 1) * 16));
-        }
+        xs[u] = (part[0] + part[1]) + (part[2] + part[3]);
+      }
+      // both tiles' head sums in one reduction: tile (lane >> 5) in each half; lanes 0-15 and 32-47 record
+      const float sum = row_sum4_pair(xs[0], xs[1]);
+      const int uu = lane >> 5;
+      const int t = t0 + uu * 16 + l16;
+      if ((g & 1) == 0 && t < wlim) {
+        const float v = is_cand(a, row, t) ? sum * bsc[cs] : -__builtin_inff();
+        orow[t] = v;
+        const uint32_t bin = score_key(v) >> 20;
+        atomicAdd(&gh[wrow][bin >> 1], 1u << ((bin & 1) * 16));
       }
     }
     if (j - j0 < 8) DSV41_PX(5 + 3 * (j - j0));
