@@ -18,6 +18,9 @@
 
 namespace {
 
+#ifdef ABL_PRIVHIST
+__device__ __align__(16) int g_abl_hist[256 * kHistBins];
+#endif
 template <int KFMT, bool HIST, int WV = 4>
 __global__ void __launch_bounds__(64 * WV) index_score_kernel(const ScoreArgs a, int nx) {
   // 1-D grid: block b runs on XCD b % 8 (round-robin dispatch); key chunk x belongs to XCD x % 8 and its R rows
@@ -133,7 +136,11 @@ __global__ void __launch_bounds__(64 * WV) index_score_kernel(const ScoreArgs a,
   if (by == 0) DSV41_PH(3);
   if (HIST) {
     __syncthreads();
+#ifdef ABL_PRIVHIST
+    int* gh = g_abl_hist + (long)(blockIdx.x % ABL_PRIVHIST) * kHistBins;
+#else
     int* gh = a.hist + (long)r * kHistBins;
+#endif
     if (((uintptr_t)gh & 7) == 0) {
 #pragma unroll 1
       for (int i = threadIdx.x; i < kHistBins / 2; i += 64 * WV) {  // bins in pairs: one 64-bit add (no carry
@@ -152,222 +159,7 @@ __global__ void __launch_bounds__(64 * WV) index_score_kernel(const ScoreArgs a,
   DSV41_WG_TS(1);
 }
 
-// Decode rows with e4m3 keys and a histogram, many rows of different lengths (ragged slots, draft rows): the
-// work items are the (row, 256-key chunk) pairs below each row's valid count, numbered per XCD: chunk c of every
-// row belongs to XCD c mod 8 (so the draft rows of one sequence read a chunk's keys through one L2), and workgroup
-// m of an XCD takes that XCD's items m, m + M, ... (M workgroups per XCD).  The grid is sized for the machine, not
-// for the longest row (a one-chunk-per-workgroup grid spends most of its time dispatching workgroups with nothing
-// to score), and the keys and query of a workgroup's next item are loaded while the current one is scored.  Per
-// item: one 256-key chunk against the row's query, the scores, and the LDS histogram added to the row's (the flush
-// clears it for the next item).
-constexpr int kLoopMaxRows = 64;
-__global__ void __launch_bounds__(256) index_score_items_kernel(const ScoreArgs a) {
-  const int x = blockIdx.x % kXcds, m = blockIdx.x / kXcds, M = gridDim.x / kXcds;
-  __shared__ int lhist[kHistBins];
-  __shared__ int pre[kLoopMaxRows + 1];  // items of XCD x in rows < r
-  __shared__ int rlim[kLoopMaxRows];     // valid count of row r (clamped to n_pos)
-  __shared__ long rslot[kLoopMaxRows];
-  __shared__ __align__(16) uint8_t qlds[2][64 * 128];  // the next rows' queries (direct-to-LDS), alternating
-  __shared__ float wlds[2][64];                        // and their head weights
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int l16 = lane & 15, g = lane >> 4;
-#pragma unroll 1
-  for (int i = threadIdx.x; i < kHistBins; i += 256) lhist[i] = 0;
-#pragma unroll 1
-  for (int i = threadIdx.x; i < 2 * 64 * 128 / 16; i += 256) ((uint4*)qlds)[i] = make_uint4(0, 0, 0, 0);
-  if (wave == 0) {
-    int cnt = 0;
-    if (lane < a.R) {
-      long cl = row_cl(a, lane);
-      if (cl > a.n_pos) cl = a.n_pos;
-      const int nx = (int)((cl + kKeysPerWG - 1) / kKeysPerWG);
-      cnt = nx > x ? (nx - x + kXcds - 1) / kXcds : 0;
-      rlim[lane] = (int)cl;
-      rslot[lane] = a.seq ? a.seq[lane] : (long)(lane / a.rows_per_slot);
-    }
-    const int inc = wave_incl_scan(cnt);
-    if (lane < a.R) pre[lane + 1] = inc;
-    if (lane == 0) pre[0] = 0;
-  }
-  __syncthreads();
-  const int total = pre[a.R];
-  const int nht = (a.HI + 15) / 16;
-  constexpr int NT = 4;
-  struct Item {
-    int r, kt0, lim;
-    long slot;
-  };
-  auto locate = [&](int j) {  // item j of this XCD (wave-uniform)
-    const bool le = lane < a.R && pre[lane] <= j;
-    Item it;
-    it.r = __popcll(__ballot(le)) - 1;
-    it.kt0 = (x + kXcds * (j - pre[it.r])) * kKeysPerWG + wave * kKeysPerWave;
-    it.lim = rlim[it.r];
-    it.slot = rslot[it.r];
-    return it;
-  };
-  // Byte order of the 128-byte rows in the MFMA operands: lane group g holds bytes [16g, 16g+16) and
-  // [64+16g, 64+16g+16) of its key / query row (the same permutation of the dot product's terms on both sides),
-  // so one 16-byte load instruction reads one 64-byte half row per key: half the cache accesses of 32-byte
-  // groups at stride 32.
-  // Two key buffers, selected by a compile-time index (constant subscripts keep everything in VGPRs); the query
-  // fragments and weights of the current row stay in VGPRs for the row's run of items.
-  uint4 k0[2][NT], k1[2][NT];
-  float ksc[2][NT];
-  float hmask[kHT][4];  // 1 for the heads (ht*16 + 4g + i) below HI, else 0
-#pragma unroll
-  for (int ht = 0; ht < kHT; ++ht)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hmask[ht][i] = (ht < nht && ht * 16 + 4 * g + i < a.HI) ? 1.0f : 0.0f;
-  i32x8_t qa8[kHT];
-  float wr[kHT][4];
-  auto load = [&](auto bufc, const Item& it) {
-    constexpr int U = decltype(bufc)::value;  // (positions past the row's count read its last valid key)
-    const uint8_t* kbase = (const uint8_t*)a.keys + it.slot * a.k_sstride + g * 16;
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      int t = it.kt0 + nt * 16 + l16;
-      t = t < it.lim ? t : it.lim - 1;
-      const uint8_t* krow = kbase + (long)t * 128;
-      k0[U][nt] = *(const uint4*)krow;
-      k1[U][nt] = *(const uint4*)(krow + 64);
-      ksc[U][nt] = a.kscale[it.slot * a.ks_sstride + t];
-    }
-  };
-  auto load_q = [&](int r) {  // query fragments and masked, shuffled head weights of row r
-    float wl[kHT];
-#pragma unroll
-    for (int ht = 0; ht < kHT; ++ht) {
-      const int h = ht * 16 + l16;
-      const int hc = (ht < nht && h < a.HI) ? h : 0;
-      const uint8_t* qrow = (const uint8_t*)a.q + (long)r * a.q_rstride + (long)hc * 128 + g * 16;
-      const uint4 u0 = *(const uint4*)qrow, u1 = *(const uint4*)(qrow + 64);
-      qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
-      wl[ht] = a.w[(long)r * a.w_rstride + hc];
-    }
-#pragma unroll
-    for (int ht = 0; ht < kHT; ++ht)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[ht], 4 * g + i, 64) * hmask[ht][i];
-  };
-  // the query of row r into qlds[p] / wlds[p] (direct-to-LDS; heads past HI are not read and stay zero), waited
-  // for by the next flush (vmcnt(0) before its barrier)
-  auto dma_q = [&](int r, int p) {
-    const uint32_t qb = lds_addr_of(&qlds[p][0]);
-    const uint8_t* qrow = (const uint8_t*)a.q + (long)r * a.q_rstride;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int c = k * 256 + wave * 64 + lane;  // 16-byte chunk: head c / 8
-      if (c < a.HI * 8) lds_dma16_at(qrow + c * 16, qb + (uint32_t)(k * 256 + wave * 64) * 16);
-    }
-    if (wave == 0) {
-      const float* wsrc = a.w + (long)r * a.w_rstride + (lane < a.HI ? lane : a.HI - 1);
-      const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr_of(&wlds[p][0]));
-      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(wsrc), "s"(m0) : "memory", "m0");
-    }
-  };
-  auto q_from_lds = [&](int p) {  // (after a barrier that follows the loads' completion)
-    float wl[kHT];
-#pragma unroll
-    for (int ht = 0; ht < kHT; ++ht) {
-      const uint8_t* qrow = &qlds[p][(ht * 16 + l16) * 128 + g * 16];
-      const uint4 u0 = *(const uint4*)qrow, u1 = *(const uint4*)(qrow + 64);
-      qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
-      wl[ht] = wlds[p][ht * 16 + l16];
-    }
-#pragma unroll
-    for (int ht = 0; ht < kHT; ++ht)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[ht], 4 * g + i, 64) * hmask[ht][i];
-  };
-  auto process = [&](auto bufc, const Item& it) {
-    constexpr int U = decltype(bufc)::value;
-    uint4 qa16[kHT][4];  // (unused: e4m3 keys)
-    float* orow = a.out + (long)it.r * a.out_rstride;
-    float sum[NT];  // (all tiles' MFMAs first: constant indices, nothing dynamic left for scratch)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) sum[nt] = score_tile<1>(qa8, qa16, wr, nht, k0[U][nt], k1[U][nt], nullptr);
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int t = it.kt0 + nt * 16 + l16;
-      if (g == 0 && t < it.lim) {
-        const float v = is_cand(a, it.r, t) ? sum[nt] * ksc[U][nt] : -__builtin_inff();
-        orow[t] = v;
-        atomicAdd(&lhist[score_key(v) >> 20], 1);
-      }
-    }
-  };
-  auto flush = [&](int r) {  // the LDS histogram into row r's (bins in pairs: one 64-bit add), cleared
-    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xf << 8));  // vmcnt(0): a pending query load has landed
-    __syncthreads();
-    int* gh = a.hist + (long)r * kHistBins;
-    if (((uintptr_t)gh & 7) == 0) {
-#pragma unroll 1
-      for (int i = threadIdx.x; i < kHistBins / 2; i += 256) {
-        const uint32_t lo = (uint32_t)lhist[2 * i], hi = (uint32_t)lhist[2 * i + 1];
-        if (lo | hi) {
-          atomicAdd((unsigned long long*)(gh + 2 * i), ((unsigned long long)hi << 32) | lo);
-          lhist[2 * i] = 0;
-          lhist[2 * i + 1] = 0;
-        }
-      }
-    } else {
-#pragma unroll 1
-      for (int i = threadIdx.x; i < kHistBins; i += 256) {
-        const int v = lhist[i];
-        if (v) {
-          atomicAdd(&gh[i], v);
-          lhist[i] = 0;
-        }
-      }
-    }
-    __syncthreads();
-  };
-  using B0 = std::integral_constant<int, 0>;
-  using B1 = std::integral_constant<int, 1>;
-  // workgroup m takes the contiguous items [j0, j1) of its XCD (mostly one row: the histogram is added to the
-  // row's once per row run, and the query is loaded once per row run); two items in flight: the keys of the next
-  // item are loaded (unconditionally; past the last item they repeat it) while the current one is scored
-  const int j0 = (int)((long)m * total / M), j1 = (int)((long)(m + 1) * total / M);
-  if (j0 >= j1) return;
-  Item ia = locate(j0);
-  load(B0{}, ia);
-  load_q(ia.r);
-  int qp = 0;  // qlds buffer of the next row change
-  DSV41_PX(0);
-#pragma unroll 1
-  for (int j = j0; j < j1; j += 2) {
-    const int pi = (j - j0) / 2;
-    if (pi < 7) DSV41_PX(1 + 4 * pi);
-    const Item ib = locate(j + 1 < j1 ? j + 1 : j);
-    load(B1{}, ib);
-    const bool swb = j + 1 < j1 && ib.r != ia.r;
-    if (swb) dma_q(ib.r, qp);
-    process(B0{}, ia);
-    if (pi < 7) DSV41_PX(2 + 4 * pi);
-    if (j + 1 >= j1 || swb) flush(ia.r);
-    if (swb) {
-      q_from_lds(qp);
-      qp ^= 1;
-    }
-    const Item ia2 = locate(j + 2 < j1 ? j + 2 : j);
-    load(B0{}, ia2);
-    const bool swa = j + 2 < j1 && ia2.r != ib.r;
-    if (swa) dma_q(ia2.r, qp);
-    if (pi < 7) DSV41_PX(3 + 4 * pi);
-    if (j + 1 < j1) {
-      process(B1{}, ib);
-      if (pi < 7) DSV41_PX(4 + 4 * pi);
-      if (j + 2 >= j1 || swa) flush(ib.r);
-      if (swa) {
-        q_from_lds(qp);
-        qp ^= 1;
-      }
-    }
-    ia = ia2;
-  }
-  DSV41_PX(31);
-}
+constexpr int kLoopMaxRows = 64;  // rows of the grouped decode score kernel's tables
 
 // Prefill score kernel (many query rows of one sequence; e4m3 keys + prepared e4m3 queries): a workgroup owns 8
 // consecutive query rows (one per wave, 8 waves) and a range of key positions, streamed through LDS in 256-key chunks
@@ -493,13 +285,15 @@ __global__ void __launch_bounds__(kPThreads, 2) index_score_prefill_kernel(const
 }
 
 // Decode rows with e4m3 keys and a histogram, grouped by sequence (a sequence's draft rows are consecutive rows with
-// the same slot): a group is a run of up to 8 consecutive rows of one slot, and its key chunks (256 keys, the
+// the same slot): a group is a run of up to 6 consecutive rows of one slot, and its key chunks (256 keys, the
 // group's longest valid count) are streamed through LDS once for all its rows (direct-to-LDS loads, double
-// buffered) while wave w scores row w of the group against them with its query fragments in VGPRs (the prefill
-// kernel's layout, one workgroup of 8 waves per CU).  Work items are the (group, chunk) pairs, numbered per XCD
-// (chunk c on XCD c mod 8) and taken in contiguous runs.  Each row's histogram is counted in LDS as 16-bit bins
-// (two per word; a run adds at most 255 chunks of 256 keys to a bin before it is flushed) and added to the row's
-// device histogram when the run leaves the group.  Rows of other layouts form groups of one row (correct, slower).
+// buffered).  Two waves per row score its two 128-key halves of the chunk with the row's query fragments in VGPRs
+// (12 waves, three per SIMD, one workgroup per CU; the next 32-key pair's fragments are read before the current
+// pair's epilogue).  Work items are the (group, chunk) pairs, numbered per XCD (chunk c on XCD c mod 8) and taken
+// in contiguous runs.  Each row's histogram is counted in LDS as 16-bit bins (two per word; a run adds at most 255
+// chunks of 256 keys to a bin before it is flushed) and added to the row's device histogram when the run leaves
+// the group, after the next item's loads are issued (their wait covers the adds).  Rows of other layouts form
+// groups of one row (correct, slower).
 constexpr int kGRows = 6;                          // rows per group
 constexpr int kGSplit = 2;                         // waves per row (each scores a 1/kGSplit slice of the chunk)
 constexpr int kGThreads = 64 * kGRows * kGSplit;   // 12 waves: three per SIMD
@@ -518,7 +312,6 @@ __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const S
   const int x = blockIdx.x % kXcds, m = blockIdx.x / kXcds, M = gridDim.x / kXcds;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
-  DSV41_PX(0);
 #pragma unroll 1
   for (int i = threadIdx.x; i < kGRows * kHistBins / 2; i += kGThreads) (&gh[0][0])[i] = 0;
   if (wave == 0) {
@@ -574,7 +367,6 @@ __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const S
   __syncthreads();
   const int G = ngroups;
   const int total = gpre[G];
-  DSV41_PX(1);
   const int j0 = (int)((long)m * total / M), j1 = (int)((long)(m + 1) * total / M);
   if (j0 >= j1) return;
   struct Item {
@@ -652,7 +444,6 @@ __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const S
   };
   Item cur = locate(j0);
   issue(cur, 0);
-  DSV41_PX(2);
   int grp = -1, since = 0, row = 0, lim_r = 0;
   const int wrow = wave % kGRows, wpart = wave / kGRows;  // this wave's row of the group and slice of the chunk
   constexpr int kPairs = kPChunk / 32 / kGSplit;          // 32-key tile pairs per slice
@@ -667,10 +458,8 @@ __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const S
       lim_r = row >= 0 ? rlim[row] : 0;
       load_q(row >= 0 ? row : rs);
     }
-    if (j - j0 < 8) DSV41_PX(3 + 3 * (j - j0));
     __builtin_amdgcn_s_waitcnt(0);  // this item's keys and the query have landed (and the last flush's adds)
     __syncthreads();                // ... for every wave; every wave is done with the other buffer and the counts
-    if (j - j0 < 8) DSV41_PX(4 + 3 * (j - j0));
     Item nxt = cur;
     if (j + 1 < j1) {
       nxt = locate(j + 1);
@@ -742,11 +531,9 @@ __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const S
         atomicAdd(&gh[wrow][bin >> 1], 1u << ((bin & 1) * 16));
       }
     }
-    if (j - j0 < 8) DSV41_PX(5 + 3 * (j - j0));
     cur = nxt;
   }
   flush(grp);
-  DSV41_PX(31);
 }
 
 // ------------------------------------------------------------------------------------------------ top-k
@@ -1008,19 +795,6 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
   }
 }
 
-#ifndef DSV41_SCORE_LOOP
-#define DSV41_SCORE_LOOP 1
-#endif
-constexpr bool kScoreLoop = DSV41_SCORE_LOOP;
-#ifndef DSV41_SCORE_GROUP
-#define DSV41_SCORE_GROUP 1
-#endif
-constexpr bool kScoreGroup = DSV41_SCORE_GROUP;
-#ifndef DSV41_SCORE_PER_CU
-#define DSV41_SCORE_PER_CU 2
-#endif
-constexpr int kScoreLoopPerCu = DSV41_SCORE_PER_CU;  // workgroups per CU of the looped decode score grid
-
 // Compute units of the current device (queried once per device; 256 when the query fails).
 int score_cus() {
   static int cached[64] = {0};
@@ -1062,22 +836,9 @@ int launch_score(ScoreArgs& a, hipStream_t st) {
     return 0;
   }
   const int nx = (a.n_pos + kKeysPerWG - 1) / kKeysPerWG;
-  if (a.hist && a.kfmt == 1 && !a.write_masked && a.R > 4 && a.R <= kLoopMaxRows && kScoreLoop) {
-    // many rows: the valid (row, chunk) items spread over a machine-sized grid (a multiple of 8)
-    if (kScoreGroup) {
-      index_score_group_kernel<<<dim3((unsigned)((score_cus() + kXcds - 1) / kXcds * kXcds)), kGThreads, 0, st>>>(a);
-      DSV41_CHECK_LAUNCH();
-      return 0;
-    }
-    long items = (long)a.R * nx;
-#ifdef DSV41_SCORE_GRID
-    long wgs = DSV41_SCORE_GRID;
-#else
-    long wgs = (long)kScoreLoopPerCu * score_cus();
-#endif
-    if (wgs > items) wgs = items;
-    wgs = (wgs + kXcds - 1) / kXcds * kXcds;
-    index_score_items_kernel<<<dim3((unsigned)wgs), 256, 0, st>>>(a);
+  if (a.hist && a.kfmt == 1 && !a.write_masked && a.R > 4 && a.R <= kLoopMaxRows) {
+    // many rows (draft rows of a few sequences): (group, chunk) items over one workgroup per CU
+    index_score_group_kernel<<<dim3((unsigned)((score_cus() + kXcds - 1) / kXcds * kXcds)), kGThreads, 0, st>>>(a);
     DSV41_CHECK_LAUNCH();
     return 0;
   }
