@@ -640,7 +640,9 @@ def test_topk_many_rows_bit_exact():
     r = rng(16)
     R, n, k = 600, 16896, 2048
     sc = r.standard_normal((R, n)).astype(np.float32)
-    sc[::7] = np.round(sc[::7] * 3) / 3  # tie-heavy rows
+    sc[::7] = np.round(sc[::7] * 3) / 3  # tie-heavy rows (the threshold's first-digit bin overflows the list)
+    sc[3::11] = np.round(sc[3::11] * 64) / 64  # ties inside a listed bin
+    sc[5::13, 100] = 1e30  # one outlier: the first digit spans the range, its threshold bin holds most positions
     start, ratio = 65536 - 4 * 600 + 4 * 16896 - 65536, 4  # rows see (start + i + 1) // 4 positions
     cls = [(start + i + 1) // ratio for i in range(R)]
     out = torch.empty(R, k, dtype=torch.int32, device=DEV)
