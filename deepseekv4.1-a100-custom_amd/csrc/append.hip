@@ -223,8 +223,7 @@ __global__ void __launch_bounds__(256) index_keys_encode_kernel(const uint16_t* 
   const uint32_t w = *(const uint32_t*)(kbf + r * 128 + 2 * lane);
   const float v0 = __uint_as_float(w << 16), v1 = __uint_as_float(w & 0xffff0000u);
   float a = fmaxf(fabsf(v0), fabsf(v1));
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) a = fmaxf(a, wave_shfl_xor(a, m));
+  a = group_max(a, 64);
   int ex = ceil_log2_f(__fdiv_rn(fmaxf(a, 1e-30f), 448.0f));
   ex = ex < -126 ? -126 : ex;
   const float inv = pow2i(-ex);

@@ -164,7 +164,7 @@ __global__ void __launch_bounds__(256) attn_split_kernel(const AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v = round_bf16(o[ct][i] * inv[i]);
-        const float partner = wave_shfl_xor(v, 1);
+        const float partner = dpp_mov<0xB1>(v);  // lane ^ 1
         if (a.rd > 0 && c >= DV - a.rd) {
           const int jj = (c - (DV - a.rd)) >> 1;
           const float cs = a.cos_t[pr * (a.rd / 2) + jj];
@@ -249,13 +249,11 @@ DSV41_DEV void merge_splits(const AttnArgs& a, int r, int h0, long pr, float (*w
     // pm/pl lines can hold entries of other units: agent-scope loads do not use the CU cache
     const float m = ok ? __hip_atomic_load(a.pm + pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -1e30f;
     const float l = ok ? __hip_atomic_load(a.pl + pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
-    float M = m;
-#pragma unroll
-    for (int d = 1; d < 32; d <<= 1) M = fmaxf(M, __shfl_xor(M, d, 64));
+    const float M = group_max(m, 32);  // over the head's 32 split lanes (DPP moves and a row swap)
     const float w = ok ? l * exp2f((m - M) * kLog2e) : 0.0f;
-    float den = w;
-#pragma unroll
-    for (int d = 1; d < 32; d <<= 1) den += __shfl_xor(den, d, 64);
+    const float w16 = row16_sum(w);
+    const auto hs = __builtin_amdgcn_permlane16_swap(__float_as_uint(w16), __float_as_uint(w16), false, false);
+    float den = __uint_as_float(hs[0]) + __uint_as_float(hs[1]);  // the 32-lane sum
     den += exp2f((a.sink[h < H ? h : H - 1] - M) * kLog2e);
     wts[hh][sp] = w / den;
   }

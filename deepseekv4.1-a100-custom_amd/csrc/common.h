@@ -108,6 +108,38 @@ DSV41_DEV float row_max4(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// Reductions within 16-lane rows by DPP lane moves (VALU, no LDS round trip): quad xor 1 and 2, then the
+// half-row mirror (the other quad of each 8-lane half) and the row mirror (the other half); every lane of the
+// group receives the result.
+template <int CTRL>
+DSV41_DEV float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+DSV41_DEV float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);         // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);         // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);        // row_half_mirror
+  return v + dpp_mov<0x140>(v);  // row_mirror
+}
+// Whole-wave sum, the result in every lane.
+DSV41_DEV float wave_sum(float v) { return row_sum4(row16_sum(v)); }
+// Maximum over aligned groups of `group` consecutive lanes (a power of two <= 64), the result in every lane.
+DSV41_DEV float group_max(float v, int group) {
+  if (group >= 2) v = fmaxf(v, dpp_mov<0xB1>(v));
+  if (group >= 4) v = fmaxf(v, dpp_mov<0x4E>(v));
+  if (group >= 8) v = fmaxf(v, dpp_mov<0x141>(v));
+  if (group >= 16) v = fmaxf(v, dpp_mov<0x140>(v));
+  if (group >= 32) {
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  }
+  if (group >= 64) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  }
+  return v;
+}
+
 template <typename T>
 DSV41_DEV T wave_shfl_xor(T v, int m) {
   return __shfl_xor(v, m, 64);
@@ -196,6 +228,12 @@ DSV41_DEV void lds_dma16_at(const void* src, uint32_t lds_addr) {
 DSV41_DEV void lds_dma4_at(const void* src, uint32_t lds_addr) {
   const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr);
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+}
+// The LDS-address-space view of a generic pointer to a __shared__ object (its low 32 bits): accesses through it
+// are LDS instructions (counted by lgkmcnt alone), not flat ones.
+template <class T>
+DSV41_DEV __attribute__((address_space(3))) T* lds_ptr(T* p) {
+  return (__attribute__((address_space(3))) T*)(uint32_t)(uintptr_t)p;
 }
 // LDS byte address of a __shared__ object.
 DSV41_DEV uint32_t lds_addr_of(const void* p) {

@@ -143,9 +143,9 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   // by the chunk holding its position, its operands and the raw index queries loaded ahead of the keys
   const IsAppend& ap = g.app;
   long ppos = 0, knew_row = -1;
-  int opmask = 0;
+  bool key_wave = false;  // (FUSED) this wave scores the new key's position and computes the key itself
   Qprep512 qp;
-  RowRegs<kIsThreads> rg;
+  RowRegs<64, 128> rk;  // the new key's operands (one wave: two elements per lane)
   auto make_op = [&](int which) {
     RowOp o{};
     o.cos_t = ap.cos_t;
@@ -194,10 +194,12 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
       row_op<kIsThreads>(make_op(which), redf);
       return;
     }
-    // the chunk holding the new key's position computes it (and scores it from the computed values)
+    // the wave whose keys hold the new key's position computes it (and scores it from the computed values); the
+    // other waves of the chunk do not wait for it
     if (closes) knew_row = (ppos + 1) / ap.ratio - 1;
-    opmask = closes && ch == (int)(knew_row / kIsChunk) ? 4 : 0;
-    if (opmask) row_load<kIsThreads>(make_op(__builtin_ctz(opmask)), rg);
+    key_wave = closes && knew_row >= ch * kIsChunk + wave * kIsKeysPerWave &&
+               knew_row < ch * kIsChunk + (wave + 1) * kIsKeysPerWave;
+    if (key_wave) row_load<64>(make_op(2), rk);
     qprep512_load(ap.q_idx + (long)r * a.HI * 128, ap.w_idx + (long)r * a.HI, a.HI, qp);
   } else {
     // the row's queries (64 heads x 128 e4m3 = 512 chunks of 16 bytes) go to LDS once, one direct load per thread
@@ -211,11 +213,8 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
       wl[ht] = hv ? a.w[(long)r * a.w_rstride + h] : 0.0f;
     }
   }
-#ifdef DSV41_TIMING
-  __builtin_amdgcn_s_waitcnt(0);
   DSV41_TS(49);
   DSV41_PX(1);
-#endif
 #pragma unroll 1
   for (int i = t; i < kHistBins; i += kIsThreads) lhist[i] = 0;
   constexpr int NT = kIsKeysPerWave / 16;  // column tiles of 16 keys per wave, all loads issued up front
@@ -231,41 +230,30 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     k1[nt] = pv ? *(const uint4*)(krow + 16) : make_uint4(0, 0, 0, 0);
     ksc[nt] = pv ? a.kscale[slot * a.ks_sstride + p] : 0.0f;
   }
+  if constexpr (FUSED) {
+    // the new key, computed by its wave while the chunk's keys are in flight (its operands were loaded first);
+    // knew / ksnew are this wave's alone
+    if (key_wave) {
 #ifdef DSV41_TIMING
+      if (lane == 0 && blockIdx.x < 1024) g_dsv41_px[blockIdx.x][7] = wall_clock64();
+#endif
+      row_compute<64>(make_op(2), rk, nullptr);
+#ifdef DSV41_TIMING
+      if (lane == 0 && blockIdx.x < 1024) g_dsv41_px[blockIdx.x][8] = wall_clock64();
+#endif
+    }
+  }
   DSV41_TS(50);
   DSV41_PX(2);
-  __builtin_amdgcn_s_waitcnt(0);
-  DSV41_TS(51);
-  DSV41_PX(3);
-#endif
   if constexpr (FUSED) {
-    if (opmask) {  // (the operands were loaded ahead of the keys)
-      const int first = __builtin_ctz(opmask);
-      row_compute<kIsThreads, true>(make_op(first), rg, redf);  // (LDS-only barriers: the keys stay in flight)
-#pragma unroll 1
-      for (int which = first + 1; which < 3; ++which)
-        if (opmask >> which & 1) row_op<kIsThreads>(make_op(which), redf);
-    }
     DSV41_PX(4);
     qprep512_store(qp, a.HI, qs, wfl);
-    lds_barrier();  // queries, weights and the new key staged
+    lds_barrier();  // queries and weights staged
     DSV41_PX(5);
 #pragma unroll
     for (int ht = 0; ht < kHT; ++ht) {
       const int h = ht * 16 + l16;
       wl[ht] = ht < nht && h < a.HI ? wfl[h] : 0.0f;
-    }
-    // the new key's position is scored with the key computed here (its row in the table was read before it was
-    // written)
-    if (knew_row >= pw && knew_row < pw + kIsKeysPerWave && (opmask & 4)) {
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        if (pw + nt * 16 + l16 == knew_row) {
-          k0[nt] = *(const uint4*)(knew + g4 * 32);
-          k1[nt] = *(const uint4*)(knew + g4 * 32 + 16);
-          ksc[nt] = ksnew;
-        }
-      }
     }
   }
   float wr[kHT][4];  // weights of the heads this lane's accumulators hold: ht*16 + 4g + i
@@ -280,6 +268,22 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     const int hc = ht < nht && h < a.HI ? h : 0;
     const uint4 u0 = *(const uint4*)(qs + hc * 128 + g4 * 32), u1 = *(const uint4*)(qs + hc * 128 + g4 * 32 + 16);
     qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+  }
+  if constexpr (FUSED) {
+    // (after the barrier: the chunk's other waves score without waiting for it)
+    if (key_wave) {
+      // the new key's position scored with the key computed above (its row in the table was read before it was
+      // written)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // (its LDS copy; the table stores need not land)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        if (pw + nt * 16 + l16 == knew_row) {
+          k0[nt] = *(const uint4*)(knew + g4 * 32);
+          k1[nt] = *(const uint4*)(knew + g4 * 32 + 16);
+          ksc[nt] = ksnew;
+        }
+      }
+    }
   }
   DSV41_TS(52);
   const bool sel = c > k;  // (otherwise every valid position is taken)
@@ -297,6 +301,9 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   }
   DSV41_TS(53);
   DSV41_PX(6);
+#ifdef DSV41_TIMING
+  if (FUSED && key_wave && lane == 0 && blockIdx.x < 1024) g_dsv41_px[blockIdx.x][9] = wall_clock64();
+#endif
   __syncthreads();
   DSV41_PH(1);
   DSV41_TS(54);

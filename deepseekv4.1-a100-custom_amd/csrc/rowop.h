@@ -19,8 +19,11 @@ DSV41_DEV float fq_scale(float amax, int mode) {
 }
 
 DSV41_DEV float fq_value(float x, float s, int mode) {
-  if (mode == 0) return round_e4m3(fminf(fmaxf(__fdiv_rn(x, s), -448.0f), 448.0f)) * s;
-  return round_e2m1(fminf(fmaxf(__fdiv_rn(x, s), -6.0f), 6.0f)) * s;
+  // modes 0 and 1: s is a power of two in [2^-126, 2^126], so x / s is x times the exact reciprocal (both are the
+  // correctly rounded x * 2^-e); mode 2 divides
+  const float xs = mode == 2 ? __fdiv_rn(x, s) : x * __int_as_float(0x7f000000 - __float_as_int(s));
+  if (mode == 0) return round_e4m3(fminf(fmaxf(xs, -448.0f), 448.0f)) * s;
+  return round_e2m1(fminf(fmaxf(xs, -6.0f), 6.0f)) * s;
 }
 
 // Workgroup barrier; LB: an LDS-only barrier (does not wait for the block's outstanding global loads, e.g. loads
@@ -33,11 +36,12 @@ DSV41_DEV void row_barrier() {
     __syncthreads();
 }
 
-// Block-wide sum / max of one float per thread (NT threads); red holds >= NT / 64 floats.
+// Block-wide sum / max of one float per thread (NT threads); red holds >= NT / 64 floats.  NT = 64: one wave's
+// (no barrier; red unused), callable by a single wave of a larger block.
 template <int NT, bool LB = false>
 DSV41_DEV float block_sum(float v, float* red) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += wave_shfl_xor(v, m);
+  v = wave_sum(v);
+  if constexpr (NT == 64) return v;
   row_barrier<LB>();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   row_barrier<LB>();
@@ -49,8 +53,8 @@ DSV41_DEV float block_sum(float v, float* red) {
 
 template <int NT, bool LB = false>
 DSV41_DEV float block_max(float v, float* red) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, wave_shfl_xor(v, m));
+  v = group_max(v, 64);
+  if constexpr (NT == 64) return v;
   row_barrier<LB>();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   row_barrier<LB>();
@@ -78,19 +82,21 @@ struct RowOp {
   float* ks_lds;
 };
 
-// The operands of one row operation, loaded ahead of its arithmetic (row_load, then row_compute).
-template <int NT>
+// The operands of one row operation, loaded ahead of its arithmetic (row_load, then row_compute), for rows of up to
+// MAXD elements.  The NT threads doing a row operation are a whole block, or (NT = 64) one wave of a larger block;
+// element e lives in thread e % NT of the group.
+template <int NT, int MAXD = kRowMaxD>
 struct RowRegs {
-  static constexpr int IT = kRowMaxD / NT;
+  static constexpr int IT = MAXD / NT;
   float v[IT], w[IT], cs[IT], sn[IT];
 };
 
-template <int NT>
-DSV41_DEV void row_load(const RowOp& o, RowRegs<NT>& g) {
-  const int t = threadIdx.x;
+template <int NT, int MAXD = kRowMaxD>
+DSV41_DEV void row_load(const RowOp& o, RowRegs<NT, MAXD>& g) {
+  const int t = threadIdx.x & (NT - 1);
   const int p = o.pos < 0 ? 0 : (int)o.pos;
 #pragma unroll
-  for (int u = 0; u < RowRegs<NT>::IT; ++u) {
+  for (int u = 0; u < RowRegs<NT, MAXD>::IT; ++u) {
     const int e = t + u * NT;
     const int ec = e < o.D ? e : 0;
     g.v[u] = bf2f(o.x[ec]);
@@ -103,11 +109,11 @@ DSV41_DEV void row_load(const RowOp& o, RowRegs<NT>& g) {
   }
 }
 
-// Every thread of the block must call it.  LB: LDS-only barriers inside.
-template <int NT, bool LB = false>
-DSV41_DEV void row_compute(const RowOp& o, RowRegs<NT>& g, float* red) {
-  constexpr int IT = RowRegs<NT>::IT;
-  const int t = threadIdx.x;
+// Every thread of the group (the block, or the one wave when NT = 64) must call it.  LB: LDS-only barriers inside.
+template <int NT, bool LB = false, int MAXD = kRowMaxD>
+DSV41_DEV void row_compute(const RowOp& o, RowRegs<NT, MAXD>& g, float* red) {
+  constexpr int IT = RowRegs<NT, MAXD>::IT;
+  const int t = threadIdx.x & (NT - 1);
   float* v = g.v;
   if (o.norm_w) {
     float ss = 0.0f;
@@ -122,15 +128,13 @@ DSV41_DEV void row_compute(const RowOp& o, RowRegs<NT>& g, float* red) {
   for (int u = 0; u < IT; ++u) {
     if (u * NT >= o.D) break;
     if (o.rd > 0) {
-      const float partner = wave_shfl_xor(v[u], 1);
+      const float partner = dpp_mov<0xB1>(v[u]);  // lane ^ 1
       const int e = t + u * NT;
       if (e >= o.D - o.rd && e < o.D)
         v[u] = (e & 1) ? round_bf16(partner * g.sn[u] + v[u] * g.cs[u]) : round_bf16(v[u] * g.cs[u] - partner * g.sn[u]);
     }
     if (o.qmode >= 0) {
-      float a = fabsf(v[u]);
-#pragma unroll 1
-      for (int m = 1; m < o.group; m <<= 1) a = fmaxf(a, wave_shfl_xor(a, m));
+      const float a = group_max(fabsf(v[u]), o.group);
       v[u] = fq_value(v[u], fq_scale(a, o.qmode), o.qmode);
     }
     const int e = t + u * NT;
@@ -153,12 +157,12 @@ DSV41_DEV void row_compute(const RowOp& o, RowRegs<NT>& g, float* red) {
       if (e < o.D) {
         const uint8_t b = (uint8_t)e4m3_bits(round_e4m3(fminf(fmaxf(round_bf16(v[u]) * pow2i(-ex), -448.0f), 448.0f)));
         o.k8[e] = b;
-        if (o.k8_lds) o.k8_lds[e] = b;
+        if (o.k8_lds) lds_ptr(o.k8_lds)[e] = b;
       }
     }
     if (t == 0) {
       *o.ks = pow2i(ex);
-      if (o.ks_lds) *o.ks_lds = pow2i(ex);
+      if (o.ks_lds) *lds_ptr(o.ks_lds) = pow2i(ex);
     }
   }
 }
@@ -195,8 +199,7 @@ DSV41_DEV void qprep_op(const uint16_t* q, const uint16_t* w_bf16, const float* 
   }
 #pragma unroll
   for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(x[e]));
-  amax = fmaxf(amax, wave_shfl_xor(amax, 1));
-  amax = fmaxf(amax, wave_shfl_xor(amax, 2));
+  amax = group_max(amax, 4);
   int ex = ceil_log2_f(fmaxf(amax, 1e-30f) * (1.0f / 448.0f));
   ex = ex < -126 ? -126 : ex;
   const float inv = pow2i(-ex);
@@ -248,9 +251,7 @@ DSV41_DEV void qprep512_store(const Qprep512& g, int HI, uint8_t* q8, float* wf)
   }
 #pragma unroll
   for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(x[e]));
-  amax = fmaxf(amax, wave_shfl_xor(amax, 1));
-  amax = fmaxf(amax, wave_shfl_xor(amax, 2));
-  amax = fmaxf(amax, wave_shfl_xor(amax, 4));
+  amax = group_max(amax, 8);
   int ex = ceil_log2_f(fmaxf(amax, 1e-30f) * (1.0f / 448.0f));
   ex = ex < -126 ? -126 : ex;
   const float inv = pow2i(-ex);
