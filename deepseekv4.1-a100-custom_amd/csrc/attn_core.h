@@ -81,11 +81,10 @@ DSV41_DEV __amdgpu_buffer_rsrc_t pacc_rsrc(const float* pacc) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)pacc, 0, 0x7fffffff, 0x00020000);
 }
 
-template <int DV>
-DSV41_DEV void merge_slice(const AttnArgs& a, int r, int h0, long pr, int sp) {
+template <int DV, int MS>  // MS: splits per batch of loads (one batch for up to MS splits: one round trip)
+DSV41_DEV void merge_slice_ms(const AttnArgs& a, int r, int h0, long pr, int sp) {
   constexpr int CG = DV / 8, E = 16 * CG;
   static_assert(E / 2 <= 512, "a slice fits the workgroup (nsplit >= 2)");
-  constexpr int MS = 16;  // splits per batch of loads
   const int ns = a.nsplit, H = a.H;
   const int e = (int)((long)sp * E / ns) + (int)threadIdx.x;
   if (e >= (int)((long)(sp + 1) * E / ns)) return;
@@ -145,6 +144,14 @@ DSV41_DEV void merge_slice(const AttnArgs& a, int r, int h0, long pr, int sp) {
     pk[q / 2] = pack_bf16x2(re, im);
   }
   *(uint4*)(a.out + (long)r * a.out_rstride + (long)h * DV + c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+}
+
+template <int DV>
+DSV41_DEV void merge_slice(const AttnArgs& a, int r, int h0, long pr, int sp) {
+  if (a.nsplit <= 16)
+    merge_slice_ms<DV, 16>(a, r, h0, pr, sp);
+  else
+    merge_slice_ms<DV, 32>(a, r, h0, pr, sp);
 }
 
 }  // namespace
