@@ -568,9 +568,11 @@ def main():
     cfg = r["cfg"]
     kb, ku = r["kern_bytes"], r["kern_us"]
     R = cfg.slots * cfg.rows_per_slot
-    sel_name = ("index_select_kernel<128, true> (cache appends + scores + top-k, one launch)" if r["fused"] else
+    sel_name = ("index_select_kernel<128, true> (cache appends + scores + top-k, one launch)"
+                if r["fused"] and r["one_launch"] else
                 "index_select_kernel (scores + top-k, one launch)" if r["one_launch"] else
-                "index_score_kernel + select kernels (scores with histogram, then the top-k; multi-launch)")
+                ("decode_appends_kernel + " if r["fused"] else "") +
+                "score kernel with histogram + select kernels (multi-launch)")
     att_name = ("attn_decode_kernel<576, 512> (splits merged in-kernel)" if R < 16 else
                 "attn_prefill_ws_kernel<576, 512> + attn_decode_combine_kernel (key splits)")
     kernel_names = {"indexer": sel_name, "sattn": att_name,
