@@ -18,9 +18,6 @@
 
 namespace {
 
-#ifdef ABL_PRIVHIST
-__device__ __align__(16) int g_abl_hist[256 * kHistBins];
-#endif
 template <int KFMT, bool HIST, int WV = 4>
 __global__ void __launch_bounds__(64 * WV) index_score_kernel(const ScoreArgs a, int nx) {
   // 1-D grid: block b runs on XCD b % 8 (round-robin dispatch); key chunk x belongs to XCD x % 8 and its R rows
@@ -136,11 +133,7 @@ __global__ void __launch_bounds__(64 * WV) index_score_kernel(const ScoreArgs a,
   if (by == 0) DSV41_PH(3);
   if (HIST) {
     __syncthreads();
-#ifdef ABL_PRIVHIST
-    int* gh = g_abl_hist + (long)(blockIdx.x % ABL_PRIVHIST) * kHistBins;
-#else
     int* gh = a.hist + (long)r * kHistBins;
-#endif
     if (((uintptr_t)gh & 7) == 0) {
 #pragma unroll 1
       for (int i = threadIdx.x; i < kHistBins / 2; i += 64 * WV) {  // bins in pairs: one 64-bit add (no carry
