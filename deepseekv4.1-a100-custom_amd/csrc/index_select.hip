@@ -79,6 +79,49 @@ struct IsAppend {
   const uint16_t* w_idx;
 };
 
+// Row operation `which` of row r's appends (0: the SWA ring row, 1: the compressed row, 2: the index key, with an
+// LDS copy of its e4m3 bytes and scale in knew / ksnew when given); position ppos, sequence slot.  Compressed /
+// index-key rows go to compress_len - 1 when the step closes a group, else to the table's spare last row.
+DSV41_DEV RowOp is_app_op(const IsAppend& ap, int r, long slot, long ppos, int which, uint8_t* knew, float* ksnew) {
+  RowOp o{};
+  o.cos_t = ap.cos_t;
+  o.sin_t = ap.sin_t;
+  o.rd = ap.rd;
+  o.eps = ap.eps;
+  const bool closes = ((ppos + 1) % ap.ratio) == 0;
+  if (which == 0) {
+    o.x = ap.kv_raw + (long)r * ap.Dw;
+    o.D = ap.Dw;
+    o.norm_w = ap.kv_norm;
+    o.pos = ppos < 0 ? 0 : ppos;
+    o.qmode = 0;
+    o.group = 32;
+    o.out = ap.ring + slot * ap.ring_sstride + (o.pos % ap.W) * (long)ap.Dw;
+  } else if (which == 1) {
+    const long row = closes ? (ppos + 1) / ap.ratio - 1 : ap.cap - 1;
+    o.x = ap.latent + (long)r * ap.Dw;
+    o.D = ap.Dw;
+    o.pos = ppos + 1 - ap.ratio;
+    o.qmode = 2;
+    o.group = 16;
+    o.out = ap.ckv + slot * ap.ckv_sstride + row * (long)ap.Dw;
+  } else {
+    const long row = closes ? (ppos + 1) / ap.ratio - 1 : ap.kcap - 1;
+    o.x = ap.k_raw + (long)r * 128;
+    o.D = 128;
+    o.norm_w = ap.k_norm;
+    o.pos = ppos + 1 - ap.ratio;
+    o.qmode = 1;
+    o.group = 32;
+    o.out = ap.kbf ? ap.kbf + slot * ap.kbf_sstride + row * 128L : nullptr;
+    o.k8 = ap.k8 + slot * ap.k8_sstride + row * 128L;
+    o.ks = ap.ks + slot * ap.ks_sstride + row;
+    o.k8_lds = knew;
+    o.ks_lds = ksnew;
+  }
+  return o;
+}
+
 struct IsArgs {
   ScoreArgs s;                // prepared e4m3 queries, folded weights, e4m3 keys + scales, seq, cl, n_pos; out or null
   int k, offset;
@@ -146,52 +189,19 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   bool key_wave = false;  // (FUSED) this wave scores the new key's position and computes the key itself
   Qprep512 qp;
   RowRegs<64, 128> rk;  // the new key's operands (one wave: two elements per lane)
-  auto make_op = [&](int which) {
-    RowOp o{};
-    o.cos_t = ap.cos_t;
-    o.sin_t = ap.sin_t;
-    o.rd = ap.rd;
-    o.eps = ap.eps;
-    const bool closes = ((ppos + 1) % ap.ratio) == 0;
-    if (which == 0) {
-      o.x = ap.kv_raw + (long)r * ap.Dw;
-      o.D = ap.Dw;
-      o.norm_w = ap.kv_norm;
-      o.pos = ppos < 0 ? 0 : ppos;
-      o.qmode = 0;
-      o.group = 32;
-      o.out = ap.ring + slot * ap.ring_sstride + (o.pos % ap.W) * (long)ap.Dw;
-    } else if (which == 1) {
-      const long row = closes ? (ppos + 1) / ap.ratio - 1 : ap.cap - 1;
-      o.x = ap.latent + (long)r * ap.Dw;
-      o.D = ap.Dw;
-      o.pos = ppos + 1 - ap.ratio;
-      o.qmode = 2;
-      o.group = 16;
-      o.out = ap.ckv + slot * ap.ckv_sstride + row * (long)ap.Dw;
-    } else {
-      const long row = closes ? (ppos + 1) / ap.ratio - 1 : ap.kcap - 1;
-      o.x = ap.k_raw + (long)r * 128;
-      o.D = 128;
-      o.norm_w = ap.k_norm;
-      o.pos = ppos + 1 - ap.ratio;
-      o.qmode = 1;
-      o.group = 32;
-      o.out = ap.kbf ? ap.kbf + slot * ap.kbf_sstride + row * 128L : nullptr;
-      o.k8 = ap.k8 + slot * ap.k8_sstride + row * 128L;
-      o.ks = ap.ks + slot * ap.ks_sstride + row;
-      o.k8_lds = knew;
-      o.ks_lds = &ksnew;
-    }
-    return o;
-  };
+  auto make_op = [&](int which) { return is_app_op(ap, r, slot, ppos, which, knew, &ksnew); };
   if constexpr (FUSED) {
     ppos = ap.pos[r];
     const bool closes = ((ppos + 1) % ap.ratio) == 0;
     if (extra) {  // the ring row, the compressed row, or (no group closes) the index key's spare row; then done
       const int which = bx % 3;
       if ((which == 1 && !(ap.latent && ap.ckv)) || (which == 2 && closes)) return;
-      row_op<kIsThreads>(make_op(which), redf);
+      if (which == 0)  // (constant operation indices: the row operation's fields stay in registers)
+        row_op<kIsThreads>(make_op(0), redf);
+      else if (which == 1)
+        row_op<kIsThreads>(make_op(1), redf);
+      else
+        row_op<kIsThreads>(make_op(2), redf);
       return;
     }
     // the wave whose keys hold the new key's position computes it (and scores it from the computed values); the
@@ -553,6 +563,157 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
 
 int is_slots(int n_pos) { return (n_pos + kIsChunk - 1) / kIsChunk; }
 
+
+// ------------------------------------------------------------------------------------------------ appends + scores
+// The decode step's appends and the indexer scores with the row histogram in one launch, for rows longer than the
+// one-launch selection takes (the selection follows as its own launches, dsv41_select_topk).  Score grid: chunks of
+// 1024 positions, 16 waves x 64 keys (the layout of the long-row score kernel: chunk x of row r runs on XCD x mod 8),
+// the row's e4m3 queries prepared in every workgroup (the first 512 threads, into LDS) while its keys are in flight.
+// After the score grid, 3 append-only workgroups per row: the ring row, the compressed row and the index key; for a
+// row whose step closes a group the last one also scores the new key (position cl - 1: the same MFMA tile as the
+// chunks', one valid column) and adds it to the row's histogram, and the chunk holding that position skips it (its
+// table row is read before it is written).  The launch boundary orders all of it before the selection.
+constexpr int kDsWaves = 16;
+constexpr int kDsThreads = 64 * kDsWaves;
+constexpr int kDsChunk = kDsWaves * kKeysPerWave;
+
+struct DsArgs {
+  ScoreArgs s;  // e4m3 keys (ap.k8 / ap.ks), seq, cl, n_pos, out, hist, cand; q / w unused (prepared here)
+  IsAppend app;
+  int nx;       // score chunks per row
+};
+
+__global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d) {
+  const ScoreArgs& a = d.s;
+  const IsAppend& ap = d.app;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int main_wgs = (d.nx + kXcds - 1) / kXcds * kXcds * a.R;
+  __shared__ int lhist[kHistBins];
+  __shared__ __align__(16) uint8_t qs[64 * 128];
+  __shared__ float wfl[64];
+  __shared__ __align__(16) uint8_t knew[128];
+  __shared__ float ksnew, redf[kDsWaves];
+  const int nht = (a.HI + 15) / 16;
+  auto stage_queries = [&](int r, Qprep512& qp, bool load) {  // (threads < 512: head t / 8)
+    if (t >= 512) return;
+    if (load)
+      qprep512_load(ap.q_idx + (long)r * a.HI * 128, ap.w_idx + (long)r * a.HI, a.HI, qp);
+    else
+      qprep512_store(qp, a.HI, qs, wfl);
+  };
+  auto read_queries = [&](i32x8_t (&qa8)[kHT], float (&wr)[kHT][4]) {
+    float wl[kHT];
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht) {
+      const int h = ht * 16 + l16;
+      const int hc = ht < nht && h < a.HI ? h : 0;
+      const uint4 u0 = *(const uint4*)(qs + hc * 128 + g * 32), u1 = *(const uint4*)(qs + hc * 128 + g * 32 + 16);
+      qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+      wl[ht] = ht < nht && h < a.HI ? wfl[h] : 0.0f;
+    }
+#pragma unroll
+    for (int ht = 0; ht < kHT; ++ht)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[ht], 4 * g + i, 64);
+  };
+  uint4 qa16[kHT][4];  // (unused: e4m3 keys)
+  if ((int)blockIdx.x >= main_wgs) {  // ---- append-only workgroups: (row, which) = (e / 3, e % 3)
+    const int e = (int)blockIdx.x - main_wgs, r = e / 3, which = e % 3;
+    const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
+    const long ppos = ap.pos[r];
+    const bool closes = ((ppos + 1) % ap.ratio) == 0;
+    if (which == 1 && !(ap.latent && ap.ckv)) return;
+    if (which == 0) {  // (constant operation indices: the row operation's fields stay in registers)
+      row_op<kDsThreads>(is_app_op(ap, r, slot, ppos, 0, nullptr, nullptr), redf);
+      return;
+    }
+    if (which == 1) {
+      row_op<kDsThreads>(is_app_op(ap, r, slot, ppos, 1, nullptr, nullptr), redf);
+      return;
+    }
+    if (!closes) {
+      row_op<kDsThreads>(is_app_op(ap, r, slot, ppos, 2, nullptr, nullptr), redf);
+      return;
+    }
+    Qprep512 qp;
+    stage_queries(r, qp, true);
+    row_op<kDsThreads>(is_app_op(ap, r, slot, ppos, 2, knew, &ksnew), redf);  // the key, table and LDS copy
+    stage_queries(r, qp, false);
+    __syncthreads();
+    if (wave == 0) {
+      i32x8_t qa8[kHT];
+      float wr[kHT][4];
+      read_queries(qa8, wr);
+      // column 0 of the tile holds the key (lanes with l16 = 0: bytes 32 g .. +32), the others zero
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      const uint4 k0 = l16 == 0 ? *(const uint4*)(knew + g * 32) : z;
+      const uint4 k1 = l16 == 0 ? *(const uint4*)(knew + g * 32 + 16) : z;
+      const float sum = score_tile<1>(qa8, qa16, wr, nht, k0, k1, nullptr);
+      long cl = row_cl(a, r);
+      if (cl > a.n_pos) cl = a.n_pos;
+      const long knew_row = (ppos + 1) / ap.ratio - 1;
+      if (lane == 0 && knew_row >= 0 && knew_row < cl) {
+        const float v = is_cand(a, r, knew_row) ? sum * ksnew : -__builtin_inff();
+        a.out[(long)r * a.out_rstride + knew_row] = v;
+        atomicAdd(a.hist + (long)r * kHistBins + (score_key(v) >> 20), 1);
+      }
+    }
+    return;
+  }
+  // ---- score grid (block b on XCD b % 8; chunk x of every row on XCD x % 8)
+  const int bxcd = blockIdx.x % kXcds, bj = blockIdx.x / kXcds;
+  const int r = bj % a.R, bx = (bj / a.R) * kXcds + bxcd;
+  if (bx >= d.nx) return;
+  long cl = row_cl(a, r);
+  if (cl > a.n_pos) cl = a.n_pos;
+  if ((long)bx * kDsChunk >= cl) return;
+  const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
+  const long ppos = ap.pos[r];
+  const long knew_row = ((ppos + 1) % ap.ratio) == 0 ? (ppos + 1) / ap.ratio - 1 : -1;  // (-1: no new key)
+  Qprep512 qp;
+  stage_queries(r, qp, true);
+#pragma unroll 1
+  for (int i = t; i < kHistBins; i += kDsThreads) lhist[i] = 0;
+  const int lim = (int)cl;
+  const int kt0 = bx * kDsChunk + wave * kKeysPerWave;
+  constexpr int NT = 4;
+  uint4 k0[NT], k1[NT];
+  float ksc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int p = kt0 + nt * 16 + l16;
+    const bool pv = p < lim;
+    const uint8_t* krow = (const uint8_t*)a.keys + slot * a.k_sstride + (long)p * 128 + g * 32;
+    k0[nt] = pv ? *(const uint4*)krow : make_uint4(0, 0, 0, 0);
+    k1[nt] = pv ? *(const uint4*)(krow + 16) : make_uint4(0, 0, 0, 0);
+    ksc[nt] = pv ? a.kscale[slot * a.ks_sstride + p] : 0.0f;
+  }
+  stage_queries(r, qp, false);
+  __syncthreads();  // queries staged, histogram cleared
+  i32x8_t qa8[kHT];
+  float wr[kHT][4];
+  read_queries(qa8, wr);
+  float* orow = a.out + (long)r * a.out_rstride;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int p = kt0 + nt * 16 + l16;
+    const float sum = score_tile<1>(qa8, qa16, wr, nht, k0[nt], k1[nt], nullptr);
+    if (g == 0 && p < lim && p != knew_row) {  // (the new key's position is its append workgroup's)
+      const float v = is_cand(a, r, p) ? sum * ksc[nt] : -__builtin_inff();
+      orow[p] = v;
+      atomicAdd(&lhist[score_key(v) >> 20], 1);
+    }
+  }
+  __syncthreads();
+  int* gh = a.hist + (long)r * kHistBins;
+#pragma unroll 1
+  for (int i = t; i < kHistBins / 2; i += kDsThreads) {  // bins in pairs: one 64-bit add (no carry out of a bin)
+    const uint32_t lo = (uint32_t)lhist[2 * i], hi = (uint32_t)lhist[2 * i + 1];
+    if (lo | hi) atomicAdd((unsigned long long*)(gh + 2 * i), ((unsigned long long)hi << 32) | lo);
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -667,6 +828,49 @@ int dsv41_decode_select(const void* kv_raw, const void* kv_norm, void* ring, lon
                    (const uint16_t*)k_norm, (uint16_t*)kbf, kbf_sstride, (uint8_t*)k8, k8_sstride, ks, ks_sstride,
                    kcap, pos, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx};
   return select_launch<true>(g, (hipStream_t)stream);
+}
+
+
+int dsv41_decode_score(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
+                       const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
+                       const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
+                       long ks_sstride, int kcap, const long* pos, const long* seq, int R, int ratio,
+                       const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
+                       const void* w_idx, int HI, const long* cl, int n_pos, float* score, long score_rstride,
+                       int* hist, const void* cand, long cand_rstride, void* stream) {
+  if (R <= 0 || n_pos <= 0) return 0;
+  if (!row_ok(Dw, 32) || ratio <= 0 || rd < 0 || rd % 2 != 0 || rd > Dw || rd > 128 || W <= 0 || !kv_raw ||
+      !kv_norm || !ring || !k_raw || !k_norm || !k8 || !ks || !pos || !seq || !q_idx || !w_idx || kcap <= 0 ||
+      (latent && (!ckv || cap <= 0)) || (rd > 0 && (!cos_t || !sin_t)) || !cl || !score || !hist || HI <= 0 ||
+      HI > 64 || n_pos > kcap || ((uintptr_t)hist & 7) != 0)
+    return (int)hipErrorInvalidValue;
+  DsArgs d{};
+  ScoreArgs& a = d.s;
+  a.HI = HI;
+  a.R = R;
+  a.kfmt = 1;
+  a.keys = k8;
+  a.k_sstride = k8_sstride;
+  a.kscale = ks;
+  a.ks_sstride = ks_sstride;
+  a.seq = seq;
+  a.rows_per_slot = 1;
+  a.cl = cl;
+  a.n_pos = n_pos;
+  a.out = score;
+  a.out_rstride = score_rstride;
+  a.hist = hist;
+  a.cand = (const uint8_t*)cand;
+  a.cand_rstride = cand_rstride;
+  d.app = IsAppend{(const uint16_t*)kv_raw, (const uint16_t*)kv_norm, (uint16_t*)ring, ring_sstride, W, Dw,
+                   (const uint16_t*)latent, (uint16_t*)ckv, ckv_sstride, cap, (const uint16_t*)k_raw,
+                   (const uint16_t*)k_norm, (uint16_t*)kbf, kbf_sstride, (uint8_t*)k8, k8_sstride, ks, ks_sstride,
+                   kcap, pos, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx};
+  d.nx = (n_pos + kDsChunk - 1) / kDsChunk;
+  const int grid = (d.nx + kXcds - 1) / kXcds * kXcds * R + 3 * R;
+  decode_score_kernel<<<grid, kDsThreads, 0, (hipStream_t)stream>>>(d);
+  DSV41_CHECK_LAUNCH();
+  return 0;
 }
 
 }  // extern "C"

@@ -47,6 +47,8 @@ SIGNATURES = {
     "dsv41_norm_quant": [_P, _P, _F, _P, _L, _I, _P],
     "dsv41_decode_select": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _I,
                             _I, _P, _P, _I, _F, _P, _P, _I, _P, _I, _I, _I, _P, _L, _P, _L, _P, _L, _P, _L, _P],
+    "dsv41_decode_score": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _I,
+                           _I, _P, _P, _I, _F, _P, _P, _I, _P, _I, _P, _L, _P, _P, _L, _P],
     "dsv41_decode_step_workspace_bytes": [_I, _I, _I, _I],
     "dsv41_decode_step_fits": [_I, _I, _I, _I, _I, _I, _I],
     "dsv41_decode_step": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _I, _I,

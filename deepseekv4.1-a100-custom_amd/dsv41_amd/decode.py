@@ -48,15 +48,16 @@ class DecodeLayer:
         self._prepared = (q8, wf) if q_idx is not None else None
 
     def appends_select(self, kv_raw, kv_norm, latent, k_raw, k_norm, pos, seq, q_idx, w_idx, cl=None, cand=None):
-        """appends() followed by select() in one launch (dsv41_decode_select) when the selection fits one launch and
-        the keys are e4m3; the rows' sequences must be distinct (one row per slot).  Falls back to the two calls
-        otherwise.  Returns the top-k indices [B, 1, k]."""
+        """appends() followed by select(), the appends inside the indexer's first launch (dsv41_decode_select when
+        the selection fits one launch, else dsv41_decode_score and the top-k launches) when the keys are e4m3; the
+        rows' sequences must be distinct (one row per slot).  Falls back to the two calls otherwise.  Returns the
+        top-k indices [B, 1, k]."""
         from ._lib import as_i64
         dev = q_idx.device
         if cl is None:
             cl = torch.div(pos + 1, self.ratio, rounding_mode="floor")
         sel = self.selector(q_idx.shape[0], dev)
-        if not sel.one_launch or self.k8 is None or k_raw is None:
+        if self.k8 is None or k_raw is None:
             self.appends(kv_raw, kv_norm, latent, k_raw, k_norm, pos, seq, q_idx, w_idx)
             return self.select(q_idx, w_idx, pos, seq, cl)
         app = dict(kv_raw=kv_raw, kv_norm=kv_norm, ring=self.ring, latent=latent, ckv=self.ckv, k_raw=k_raw,

@@ -205,6 +205,22 @@ int dsv41_decode_select(const void* kv_raw, const void* kv_norm, void* ring, lon
                         long ws_bytes, float* score_out, long score_rstride, int* out, long out_rstride,
                         const void* cand, long cand_rstride, void* stream);
 
+/* The decode step's cache appends and the indexer scores with their histogram in one launch, for rows longer than
+ * dsv41_decode_select's one launch takes (the multi-launch decode indexer, dsv41/decode.py:106-174 with :284-294):
+ * the operations of dsv41_decode_appends (ring row, compressed row, index-key row; the e4m3 query preparation in
+ * the launch) followed by dsv41_index_score over the e4m3 key table k8 / ks with the row histogram hist [R, 4096]
+ * (zero on entry; dsv41_select_topk leaves it zero), scores into score [R, n_pos] for positions < cl[r]; the new key
+ * of a row whose step closes a group is scored from the values this launch computes.  Same results as
+ * dsv41_decode_appends followed by dsv41_index_score (e4m3 keys, with the histogram).  Rows must belong to distinct
+ * sequences (a row's new key is not visible to other rows of the launch); index-key width 128, HI <= 64. */
+int dsv41_decode_score(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
+                       const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
+                       const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
+                       long ks_sstride, int kcap, const long* pos, const long* seq, int R, int ratio,
+                       const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
+                       const void* w_idx, int HI, const long* cl, int n_pos, float* score, long score_rstride,
+                       int* hist, const void* cand, long cand_rstride, void* stream);
+
 /* Workspace of dsv41_candidate_blocks (block maxima and the selected blocks of every row). */
 long dsv41_candidate_blocks_workspace_bytes(int R, int n, int topk_blocks, int block_size);
 
