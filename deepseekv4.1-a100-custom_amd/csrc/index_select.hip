@@ -132,6 +132,7 @@ struct IsArgs {
   unsigned long long* cnt;    // [R, nslots]: epoch << 32 | candidates << 16 | above
   unsigned long long* cand;   // [R, nslots * kIsChunk]
   int* err;
+  unsigned long long* pub;    // (FUSED) [R]: epoch << 32 | the score of the row's new key (its append workgroup's)
   IsAppend app;               // FUSED instances only
 };
 
@@ -181,35 +182,73 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   i32x8_t qa8[kHT];
   uint4 qa16[kHT][4];  // (bf16 queries: unused here)
   float wl[kHT];
-  // FUSED: the ring row, the compressed row and a spare-row index key are written by 3 append-only workgroups per
-  // row after the row grid (they take no part in the row barriers); the new index key of a row whose group closes
-  // by the chunk holding its position, its operands and the raw index queries loaded ahead of the keys
+  // FUSED: the ring row, the compressed row and the index key are written by 3 append-only workgroups per row after
+  // the row grid; a row whose group closes gets its new key at position cl - 1: its append workgroup also scores it
+  // (the same MFMA tile as the chunks', so the same bits), adds it to the row histogram and publishes the score with
+  // this launch's epoch; the chunk holding the position skips it (its table row is read before it is written) and
+  // takes the published score with the histogram (the row barrier covers the entry)
   const IsAppend& ap = g.app;
   long ppos = 0, knew_row = -1;
-  bool key_wave = false;  // (FUSED) this wave scores the new key's position and computes the key itself
+  bool holder = false;  // (FUSED) this chunk holds the new key's position
   Qprep512 qp;
-  RowRegs<64, 128> rk;  // the new key's operands (one wave: two elements per lane)
   auto make_op = [&](int which) { return is_app_op(ap, r, slot, ppos, which, knew, &ksnew); };
   if constexpr (FUSED) {
     ppos = ap.pos[r];
     const bool closes = ((ppos + 1) % ap.ratio) == 0;
-    if (extra) {  // the ring row, the compressed row, or (no group closes) the index key's spare row; then done
+    if (closes) knew_row = (ppos + 1) / ap.ratio - 1;
+    if (extra) {  // the ring row, the compressed row or the index-key row; then done
       const int which = bx % 3;
-      if ((which == 1 && !(ap.latent && ap.ckv)) || (which == 2 && closes)) return;
-      if (which == 0)  // (constant operation indices: the row operation's fields stay in registers)
+      if (which == 1 && !(ap.latent && ap.ckv)) return;
+      if (which == 0) {  // (constant operation indices: the row operation's fields stay in registers)
         row_op<kIsThreads>(make_op(0), redf);
-      else if (which == 1)
+        return;
+      }
+      if (which == 1) {
         row_op<kIsThreads>(make_op(1), redf);
-      else
+        return;
+      }
+      if (!closes) {
         row_op<kIsThreads>(make_op(2), redf);
+        return;
+      }
+      qprep512_load(ap.q_idx + (long)r * a.HI * 128, ap.w_idx + (long)r * a.HI, a.HI, qp);
+      row_op<kIsThreads>(make_op(2), redf);  // the key row, into the table and knew / ksnew
+      qprep512_store(qp, a.HI, qs, wfl);
+      __syncthreads();
+      if (wave == 0) {
+        // column 0 of the tile holds the key (lanes with l16 = 0: bytes 32 g4 .. +32), the others zero
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        const uint4 k0n = l16 == 0 ? *(const uint4*)(knew + g4 * 32) : z;
+        const uint4 k1n = l16 == 0 ? *(const uint4*)(knew + g4 * 32 + 16) : z;
+        float wr[kHT][4];
+#pragma unroll
+        for (int ht = 0; ht < kHT; ++ht) {
+          const int h = ht * 16 + l16;
+          const int hc = ht < nht && h < a.HI ? h : 0;
+          const uint4 u0 = *(const uint4*)(qs + hc * 128 + g4 * 32), u1 = *(const uint4*)(qs + hc * 128 + g4 * 32 + 16);
+          qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+          wl[ht] = ht < nht && h < a.HI ? wfl[h] : 0.0f;
+        }
+#pragma unroll
+        for (int ht = 0; ht < kHT; ++ht)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[ht], 4 * g4 + i, 64);
+        const float sum = score_tile<1>(qa8, qa16, wr, nht, k0n, k1n, nullptr);
+        if (lane == 0 && knew_row < c) {
+          const float v = is_cand(a, r, knew_row) ? sum * ksnew : -__builtin_inff();
+          if (a.out && knew_row < a.n_pos) a.out[(long)r * a.out_rstride + knew_row] = v;
+          if (c > k) {  // (otherwise nobody reads the histogram)
+            DSV41_PH(1);
+            __hip_atomic_fetch_add(g.hist + (long)r * kHistBins + (score_key(v) >> 20), 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(g.pub + r, (unsigned long long)epoch << 32 | __float_as_uint(v), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
       return;
     }
-    // the wave whose keys hold the new key's position computes it (and scores it from the computed values); the
-    // other waves of the chunk do not wait for it
-    if (closes) knew_row = (ppos + 1) / ap.ratio - 1;
-    key_wave = closes && knew_row >= ch * kIsChunk + wave * kIsKeysPerWave &&
-               knew_row < ch * kIsChunk + (wave + 1) * kIsKeysPerWave;
-    if (key_wave) row_load<64>(make_op(2), rk);
+    holder = closes && knew_row >= 0 && knew_row < c && ch == (int)(knew_row / kIsChunk);
     qprep512_load(ap.q_idx + (long)r * a.HI * 128, ap.w_idx + (long)r * a.HI, a.HI, qp);
   } else {
     // the row's queries (64 heads x 128 e4m3 = 512 chunks of 16 bytes) go to LDS once, one direct load per thread
@@ -240,19 +279,6 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     k1[nt] = pv ? *(const uint4*)(krow + 16) : make_uint4(0, 0, 0, 0);
     ksc[nt] = pv ? a.kscale[slot * a.ks_sstride + p] : 0.0f;
   }
-  if constexpr (FUSED) {
-    // the new key, computed by its wave while the chunk's keys are in flight (its operands were loaded first);
-    // knew / ksnew are this wave's alone
-    if (key_wave) {
-#ifdef DSV41_TIMING
-      if (lane == 0 && blockIdx.x < 1024) g_dsv41_px[blockIdx.x][7] = wall_clock64();
-#endif
-      row_compute<64>(make_op(2), rk, nullptr);
-#ifdef DSV41_TIMING
-      if (lane == 0 && blockIdx.x < 1024) g_dsv41_px[blockIdx.x][8] = wall_clock64();
-#endif
-    }
-  }
   DSV41_TS(50);
   DSV41_PX(2);
   if constexpr (FUSED) {
@@ -279,22 +305,6 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     const uint4 u0 = *(const uint4*)(qs + hc * 128 + g4 * 32), u1 = *(const uint4*)(qs + hc * 128 + g4 * 32 + 16);
     qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
   }
-  if constexpr (FUSED) {
-    // (after the barrier: the chunk's other waves score without waiting for it)
-    if (key_wave) {
-      // the new key's position scored with the key computed above (its row in the table was read before it was
-      // written)
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // (its LDS copy; the table stores need not land)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        if (pw + nt * 16 + l16 == knew_row) {
-          k0[nt] = *(const uint4*)(knew + g4 * 32);
-          k1[nt] = *(const uint4*)(knew + g4 * 32 + 16);
-          ksc[nt] = ksnew;
-        }
-      }
-    }
-  }
   DSV41_TS(52);
   const bool sel = c > k;  // (otherwise every valid position is taken)
   float* orow = a.out ? a.out + (long)r * a.out_rstride : nullptr;
@@ -305,15 +315,15 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     if (g4 == 0) {
       const float v = p < c ? (is_cand(a, r, p) ? sum * ksc[nt] : -__builtin_inff()) : 0.0f;
       sc[p - ch * kIsChunk] = v;
-      if (p < c && sel) atomicAdd(&lhist[score_key(v) >> 20], 1);
-      if (orow && p < a.n_pos) orow[p] = p < c ? v : -__builtin_inff();
+      // (FUSED: the new key's position is its append workgroup's: scored, counted and written there)
+      if (!(FUSED && holder && p == knew_row)) {
+        if (p < c && sel) atomicAdd(&lhist[score_key(v) >> 20], 1);
+        if (orow && p < a.n_pos) orow[p] = p < c ? v : -__builtin_inff();
+      }
     }
   }
   DSV41_TS(53);
   DSV41_PX(6);
-#ifdef DSV41_TIMING
-  if (FUSED && key_wave && lane == 0 && blockIdx.x < 1024) g_dsv41_px[blockIdx.x][9] = wall_clock64();
-#endif
   __syncthreads();
   DSV41_PH(1);
   DSV41_TS(54);
@@ -345,6 +355,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     constexpr int BP = kHistBins / kIsThreads;  // bins per thread: 4095 - BP*t (h[0]) down to 4096 - BP*(t+1)
     int h[BP];
     int local, total, above, spins = 0;
+    unsigned long long pubv = 0ull;  // (FUSED holder) the new key's published score, read with the histogram
 #pragma unroll 1
     while (true) {
 #pragma unroll
@@ -354,6 +365,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
         h[BP - 1 - 2 * u] = (int)(v & 0xffffffffu);
         h[BP - 2 - 2 * u] = (int)(v >> 32);
       }
+      if (FUSED && holder && t == 0) pubv = __hip_atomic_load(g.pub + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       local = 0;
 #pragma unroll
       for (int i = 0; i < BP; ++i) local += h[i];
@@ -369,6 +381,19 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
 #ifdef DSV41_TIMING
     if (t == 0 && blockIdx.x < 1024) g_is_spins[blockIdx.x][0] = spins;
 #endif
+    if (FUSED && holder && t == 0) {
+      // the score is published right after its histogram entry: wait for this launch's epoch on it
+#pragma unroll 1
+      for (int sp2 = 0; (uint32_t)(pubv >> 32) != epoch; ++sp2) {
+        if (sp2 >= kIsSpinLimit) {
+          __hip_atomic_store(g.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        pubv = __hip_atomic_load(g.pub + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      sc[knew_row - ch * kIsChunk] = __uint_as_float((uint32_t)pubv);
+    }
     if (above < k && k <= above + local) {
 #pragma unroll 1
       for (int i = 0; i < BP; ++i) {
@@ -774,7 +799,8 @@ int select_setup(IsArgs& g, const void* q8, long q_rstride, const float* wf, lon
   g.hist = (int*)w;
   g.cnt = (unsigned long long*)(w + (long)R * kHistBins * 4);
   g.cand = g.cnt + (long)R * ns;
-  g.err = (int*)(g.cand + (long)R * ns * kIsChunk + (long)R * ns);  // (after a spare [R, nslots] u64 region)
+  g.pub = g.cand + (long)R * ns * kIsChunk;                       // [R] u64 (in a spare [R, nslots] u64 region)
+  g.err = (int*)(g.cand + (long)R * ns * kIsChunk + (long)R * ns);
   return 0;
 }
 
