@@ -1323,6 +1323,58 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const AttnArgs
   const int H = a.H, ns = a.nsplit;
   if (h >= H) return;
   const long base = ((long)r * H + h) * ns;
+  const long pr = (a.mode == 1 && a.pos) ? (a.pos[r] < 0 ? 0 : a.pos[r]) : 0;
+  const uint16_t* pb = (const uint16_t*)a.pacc;
+  auto finish = [&](int c, const float (&num)[8], float den) {
+    const float inv = 1.0f / den;
+    uint32_t pk[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float re = round_bf16(num[e] * inv), im = round_bf16(num[e + 1] * inv);
+      const int cc = c + e;
+      if (a.rd > 0 && cc >= DV - a.rd) {
+        const int jj = (cc - (DV - a.rd)) >> 1;
+        const float cs = a.cos_t[pr * (a.rd / 2) + jj];
+        const float sn = -a.sin_t[pr * (a.rd / 2) + jj];
+        const float yr = re * cs - im * sn, yi = re * sn + im * cs;
+        re = yr;
+        im = yi;
+      }
+      pk[e / 2] = pack_bf16x2(re, im);
+    }
+    *(uint4*)(a.out + (long)r * a.out_rstride + (long)h * DV + c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  };
+  if (ns <= B && DV == 512) {
+    // one round trip: the splits' maxima, sums and partial rows are loaded together (none depends on another)
+    const int c = (threadIdx.x & 63) * 8;
+    uint4 v[B];
+    float m[B], l[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int s = u < ns ? u : ns - 1;
+      v[u] = *(const uint4*)(pb + (base + s) * DV + c);
+      m[u] = u < ns ? a.pm[base + s] : -1e30f;
+      l[u] = a.pl[base + s];
+    }
+    float mx = -1e30f;
+#pragma unroll
+    for (int u = 0; u < B; ++u) mx = fmaxf(mx, m[u]);
+    float num[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float den = exp2f((a.sink[h] - mx) * kLog2e);
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const float wg = u < ns ? l[u] * exp2f((m[u] - mx) * kLog2e) : 0.0f;
+      den += wg;
+      const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        num[2 * e] += wg * __uint_as_float(vv[e] << 16);
+        num[2 * e + 1] += wg * __uint_as_float(vv[e] & 0xffff0000u);
+      }
+    }
+    finish(c, num, den);
+    return;
+  }
   float mx = -1e30f;
   for (int s0 = 0; s0 < ns; s0 += MAXS) {
     float mv[MAXS];
@@ -1331,8 +1383,6 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const AttnArgs
 #pragma unroll
     for (int s = 0; s < MAXS; ++s) mx = fmaxf(mx, mv[s]);
   }
-  const long pr = (a.mode == 1 && a.pos) ? (a.pos[r] < 0 ? 0 : a.pos[r]) : 0;
-  const uint16_t* pb = (const uint16_t*)a.pacc;
   const float sink_term = exp2f((a.sink[h] - mx) * kLog2e);
   for (int c = (threadIdx.x & 63) * 8; c < DV; c += 512) {
     float num[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -1357,23 +1407,7 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const AttnArgs
         }
       }
     }
-    const float inv = 1.0f / den;
-    uint32_t pk[4];
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      float re = round_bf16(num[e] * inv), im = round_bf16(num[e + 1] * inv);
-      const int cc = c + e;
-      if (a.rd > 0 && cc >= DV - a.rd) {
-        const int jj = (cc - (DV - a.rd)) >> 1;
-        const float cs = a.cos_t[pr * (a.rd / 2) + jj];
-        const float sn = -a.sin_t[pr * (a.rd / 2) + jj];
-        const float yr = re * cs - im * sn, yi = re * sn + im * cs;
-        re = yr;
-        im = yi;
-      }
-      pk[e / 2] = pack_bf16x2(re, im);
-    }
-    *(uint4*)(a.out + (long)r * a.out_rstride + (long)h * DV + c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    finish(c, num, den);
   }
 }
 
