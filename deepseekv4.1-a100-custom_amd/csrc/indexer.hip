@@ -547,31 +547,7 @@ struct TopkArgs {
 // Block-wide exclusive scan of one int per thread (NT threads = NT/64 waves).  Returns the prefix; *total = sum.
 template <int NT>
 DSV41_DEV int block_excl_scan(int v, int* tmp, int* total) {
-  constexpr int NW = NT / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
-  }
-  if (lane == 63) tmp[wave] = x;
-  __syncthreads();
-  if (wave == 0) {
-    int w = lane < NW ? tmp[lane] : 0;
-#pragma unroll
-    for (int d = 1; d < NW; d <<= 1) {
-      const int y = __shfl_up(w, d, 64);
-      if (lane >= d) w += y;
-    }
-    if (lane < NW) tmp[16 + lane] = w;  // inclusive wave prefix
-  }
-  __syncthreads();
-  const int before = wave ? tmp[16 + wave - 1] : 0;
-  *total = tmp[16 + NW - 1];
-  const int r = before + x - v;
-  __syncthreads();
-  return r;
+  return block_scan_dpp<NT>(v, tmp, total);
 }
 
 // Radix select on d = key - kmin (the row's own key range), 11-bit digits from the top of the range down, so the

@@ -47,34 +47,11 @@ DSV41_DEV int row_c(const SelArgs& a, int r) {
   return (int)(c < 0 ? 0 : (c > a.n ? a.n : c));
 }
 
-// Exclusive scan over the threads of a block of NT threads (NT/64 waves); tmp holds >= 2 * NT/64 ints.
+// Exclusive scan over the threads of a block of NT threads (NT/64 waves); tmp holds >= NT/64 ints.  (DPP wave
+// scans, two barriers; tmp may be reused right after.)
 template <int NT>
 DSV41_DEV int block_scan(int v, int* tmp, int* total) {
-  constexpr int NW = NT / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
-  }
-  if (lane == 63) tmp[wave] = x;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc = 0;
-#pragma unroll 1
-    for (int w = 0; w < NW; ++w) {
-      const int t = tmp[w];
-      tmp[NW + w] = acc;
-      acc += t;
-    }
-    tmp[2 * NW] = acc;
-  }
-  __syncthreads();
-  const int r = tmp[NW + wave] + x - v;
-  *total = tmp[2 * NW];
-  __syncthreads();
-  return r;
+  return block_scan_dpp<NT>(v, tmp, total);
 }
 
 // Threshold bin of a row: the bin b with above(b) < k <= above(b) + hist[b], above(b) = sum of bins > b.
