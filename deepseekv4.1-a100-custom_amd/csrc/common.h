@@ -121,6 +121,12 @@ DSV41_DEV float row16_sum(float v) {
   v += dpp_mov<0x141>(v);        // row_half_mirror
   return v + dpp_mov<0x140>(v);  // row_mirror
 }
+// Integer sum over aligned groups of 8 lanes, the result in every lane of the group.
+DSV41_DEV int group8_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);   // quad_perm [2,3,0,1]
+  return v + __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);  // row_half_mirror
+}
 // Whole-wave sum, the result in every lane.
 DSV41_DEV float wave_sum(float v) { return row_sum4(row16_sum(v)); }
 // Maximum over aligned groups of `group` consecutive lanes (a power of two <= 64), the result in every lane.
@@ -283,6 +289,28 @@ DSV41_DEV int block_scan_dpp(int v, int* tmp, int* total) {
   *total = all;
   __syncthreads();
   return before + x - v;
+}
+
+// Exclusive prefix sums of two values over the NT threads of a workgroup, with both totals; ONE barrier (no
+// trailing one): `tmp` (NT/64 int2) must not be written again until a later barrier has passed.
+template <int NT>
+DSV41_DEV int2 block_scan2_dpp(int v0, int v1, int2* tmp, int2* total) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int x0 = wave_incl_scan(v0), x1 = wave_incl_scan(v1);
+  if (lane == 63) tmp[wave] = make_int2(x0, x1);
+  __syncthreads();
+  int2 before = make_int2(0, 0), all = make_int2(0, 0);
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int2 s = tmp[w];
+    before.x += w < wave ? s.x : 0;
+    before.y += w < wave ? s.y : 0;
+    all.x += s.x;
+    all.y += s.y;
+  }
+  *total = all;
+  return make_int2(before.x + x0 - v0, before.y + x1 - v1);
 }
 
 // ---- workgroup groups that exchange data through one XCD's L2

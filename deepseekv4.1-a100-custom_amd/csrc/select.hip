@@ -321,9 +321,15 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
 // the threshold key, and from the prefix over earlier chunks of (above B + taken candidates) writes its own chunk's
 // taken positions in index order (it re-reads its 1024 scores).  Ties at the threshold go to the lowest positions.
 // The work is proportional to the candidates (a few percent of the row) per workgroup, and the row's workgroups run
-// in parallel where finalize ran one workgroup per row.  Workgroup 0 of the row clears its histogram (this kernel
-// reads the threshold bin select_chunks stored, not the histogram).
-constexpr int kEmitCap = 8192;  // candidate keys staged in LDS (more: read from the workspace)
+// in parallel where finalize ran one workgroup per row.  Each workgroup clears a slice of the row's histogram as its
+// last stores (this kernel reads the threshold bin select_chunks stored, not the histogram).
+constexpr int kEmitLead = 32;     // leading candidate keys per chunk brought to LDS with the chunk counts
+constexpr int kEmitChunks = 264;  // chunks per row (kMaxBitmapWords bounds n)
+static_assert(kMaxBitmapWords * 32 <= kEmitChunks * kChunk && kEmitChunks % 8 == 0, "emit chunk bound");
+// Leading keys in LDS: block m (chunks 8m .. 8m+7) at word m * kEmitBlock; key group g (keys 4g .. 4g+3) of chunk q
+// at word (q >> 3) * kEmitBlock + 32 g + 4 (q & 7) -- one direct load per block, and the blocks' 32-word offset in
+// bank keeps 16 consecutive chunks' reads of one key group on 16 distinct bank quads.
+constexpr int kEmitBlock = 8 * kEmitLead + 32;
 #ifndef DSV41_EMIT
 #define DSV41_EMIT 1
 #endif
@@ -332,16 +338,20 @@ constexpr bool kEmit = DSV41_EMIT;
 #define DSV41_EMIT_MAX_GRID 2048
 #endif
 constexpr long kEmitMaxGrid = DSV41_EMIT_MAX_GRID;  // emit grids up to this many workgroups (each redoes the radix)
+
+// Thread t owns chunks t*nch/256 .. (t+1)*nch/256 - 1 (at most CPT = 1 or 2): thread order is chunk order, so block
+// scans over the threads give prefixes over chunks.  The first kEmitLead candidate keys of every chunk come to LDS by
+// direct loads issued with the counts (8 chunks per wave instruction); each pass over the candidates (the two radix
+// histograms, the per-chunk tally) walks the owned chunks' keys there, the rest of a chunk (rare) from the
+// workspace.  Code is kept loop-shaped and LDS traffic low: the kernel is latency-bound.
+template <int CPT>
 __global__ void __launch_bounds__(256) emit_kernel(const SelArgs a) {
-  __shared__ uint32_t ck[kEmitCap];
-  __shared__ uint16_t owner[kEmitCap];  // chunk of staged candidate j
-  __shared__ int pa[1025], pc[1025];  // exclusive prefixes of above / candidates over the row's chunks
-  __shared__ int cout[1024], ceq[1024];  // per chunk: output offset, equal candidates in earlier chunks
-  __shared__ int hist[1024];
-  __shared__ int tmp[16];
-  __shared__ int s_digit, s_rem;
+  __shared__ uint32_t sk[kEmitChunks / 8 * kEmitBlock];
+  __shared__ int hist0[1024], hist1[1024];
+  __shared__ int2 t0[4], t1[4], t2[4], t3[4];
+  __shared__ int s_d0, s_r0, s_d1, s_r1, s_out0, s_eq0;
   DSV41_TS(0);
-  const int ch = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+  const int ch = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = row_c(a, r), k = a.k;
   int* orow = a.out + (long)r * a.out_rstride;
   int* gh = a.hist + (long)r * kBins;
@@ -356,232 +366,173 @@ __global__ void __launch_bounds__(256) emit_kernel(const SelArgs a) {
   }
   const int nch = (c + kChunk - 1) / kChunk;
   if (ch >= nch) return;
-  // chunk scores (4 consecutive positions per thread), loaded first
+  // chunk scores (4 consecutive positions per thread), the owned chunks' counts, every chunk's leading keys
   const int p0 = ch * kChunk + 4 * tid;
   const float* srow = a.score + (long)r * a.ld;
   float v[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[e] = srow[p0 + e < c ? p0 + e : 0];
   const int B = a.rowbin[r];
-  DSV41_TS(1);
-  // ---- chunk counts -> prefixes (thread t: chunks 4t .. 4t+3)
-  int na[4], nc[4], la = 0, lc = 0;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int q = 4 * tid + u;
-    na[u] = nc[u] = 0;
-    if (q < nch) {
-      const int2 cv = *(const int2*)(a.counts + ((long)r * a.nchunks + q) * 2);
-      na[u] = cv.x;
-      nc[u] = cv.y;
-    }
-    la += na[u];
-    lc += nc[u];
-  }
-  int tot_a, tot_c;
-  int ea = block_scan<256>(la, tmp, &tot_a);
-  int ec = block_scan<256>(lc, tmp, &tot_c);
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int q = 4 * tid + u;
-    if (q <= nch) {
-      pa[q] = ea;
-      pc[q] = ec;
-    }
-    ea += na[u];
-    ec += nc[u];
-  }
-  if (tid == 0) {  // (nch == 1024: the loop above stops at chunk 1023)
-    pa[nch] = tot_a;
-    pc[nch] = tot_c;
-  }
-  if (ch == 0) {
-#pragma unroll 1
-    for (int i = tid; i < kBins; i += 256) gh[i] = 0;
-  }
-  __syncthreads();
-  DSV41_TS(2);
-  const int need = k - tot_a;  // candidates to take (<= 0: the above entries alone reach k)
-  const bool staged = tot_c <= kEmitCap;
   const long reg = (long)r * a.rs;
-  auto chunk_of = [&](int j) {  // last chunk q with pc[q] <= j
-    int lo = 0, hi = nch - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (pc[mid] <= j) lo = mid;
-      else hi = mid - 1;
+#pragma unroll 1
+  for (int m = wave; 8 * m < nch; m += 4) {  // (a chunk's region holds kChunk keys: reads past its count stay inside)
+    const int q = min(8 * m + (lane & 7), nch - 1);
+    lds_dma16_at(a.cand_key + reg + (long)q * kChunk + 4 * (lane >> 3), lds_addr_of(sk) + m * kEmitBlock * 4);
+  }
+  const int qb = (tid * nch) >> 8, qe = ((tid + 1) * nch) >> 8;
+  int na[CPT], nc[CPT], la = 0, lc = 0;
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    int2 cv = make_int2(0, 0);
+    if (qb + u < qe) cv = *(const int2*)(a.counts + ((long)r * a.nchunks + qb + u) * 2);
+    na[u] = cv.x;
+    nc[u] = cv.y;
+    la += cv.x;
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    hist0[4 * tid + u] = 0;
+    hist1[4 * tid + u] = 0;
+  }
+  int2 tot;
+  const int2 ex = block_scan2_dpp<256>(la, 0, t0, &tot);  // above-B entries in earlier threads' chunks
+  const int need = k - tot.x;  // candidates to take (<= 0: the above entries alone reach k)
+  int pa_ch = 0;               // above-B entries before chunk ch (meaningful in its owner thread)
+  {
+    int ea = ex.x;
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      pa_ch = qb + u == ch ? ea : pa_ch;
+      ea += na[u];
     }
-    return lo;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the direct loads into sk
+  __syncthreads();
+  DSV41_TS(1);
+  // fn(u, key) for every candidate of owned chunk u: the leading keys from sk (8 per LDS round trip), the rest of a
+  // chunk from the workspace (8 per round trip; reads stay inside the chunk's region)
+  auto visit = [&](auto&& fn) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int q = qb + u, n = nc[u];
+#pragma unroll 1
+      for (int i0 = 0; i0 < min(n, kEmitLead); i0 += 8) {
+        const uint32_t* row = &sk[(q >> 3) * kEmitBlock + (i0 / 4) * 32 + 4 * (q & 7)];
+        const uint4 x = *(const uint4*)row, y = *(const uint4*)(row + 32);
+        const uint32_t kk[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (i0 + e < n) fn(u, kk[e]);
+      }
+      const uint32_t* base = a.cand_key + reg + (long)q * kChunk;
+#pragma unroll 1
+      for (int i0 = kEmitLead; i0 < n; i0 += 8) {
+        const uint4 x = *(const uint4*)(base + i0), y = *(const uint4*)(base + i0 + 4);
+        const uint32_t kk[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (i0 + e < n) fn(u, kk[e]);
+      }
+    }
   };
-  auto key_of = [&](int j) -> uint32_t {  // (staged: ck)
-    if (staged) return ck[j];
-    const int q = chunk_of(j);
-    return a.cand_key[reg + (long)q * kChunk + (j - pc[q])];
+  // the digit (of 1023 - 4t - u, thread t) holding the rank-th largest entry of h, and the rank within it
+  auto find_digit = [&](const int* h, int rank, int2* tmp, int* s_d, int* s_r) {
+    int hb[4], local = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      hb[u] = h[1023 - 4 * tid - u];
+      local += hb[u];
+    }
+    int2 t;
+    int greater = block_scan2_dpp<256>(local, 0, tmp, &t).x;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (greater < rank && rank <= greater + hb[u]) {
+        *s_d = 1023 - 4 * tid - u;
+        *s_r = rank - greater;
+      }
+      greater += hb[u];
+    }
+    __syncthreads();
   };
   uint32_t T = 0xffffffffu;  // threshold key (candidates above it are taken, `remaining` equal ones)
   int remaining = 0;
+  int g[CPT], e[CPT];  // per owned chunk: candidates above / equal to T
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) g[u] = e[u] = 0;
   if (need > 0) {
-    if (staged) {
-      // owner[j] = chunk of candidate j (thread t fills its chunks' ranges), then every key load is independent
+    visit([&](int, uint32_t key) { atomicAdd(&hist0[(key >> 10) & 1023], 1); });  // bits 19..10 (bin: 31..20)
+    __syncthreads();
+    find_digit(hist0, need, t1, &s_d0, &s_r0);
+    const uint32_t d0 = (uint32_t)s_d0;
+    visit([&](int, uint32_t key) {  // bits 9..0 of the candidates with digit d0
+      if (((key >> 10) & 1023) == d0) atomicAdd(&hist1[key & 1023], 1);
+    });
+    __syncthreads();
+    find_digit(hist1, s_r0, t2, &s_d1, &s_r1);
+    T = ((uint32_t)B << 20) | (d0 << 10) | (uint32_t)s_d1;
+    remaining = s_r1;
+    visit([&](int u, uint32_t key) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int q = 4 * tid + u;
-        if (q < nch)
-#pragma unroll 1
-          for (int j = pc[q]; j < pc[q + 1]; ++j) owner[j] = (uint16_t)q;
+      for (int w = 0; w < CPT; ++w) {
+        g[w] += w == u && key > T;
+        e[w] += w == u && key == T;
       }
-      __syncthreads();
-#pragma unroll 1
-      for (int j0 = 0; j0 < tot_c; j0 += 8 * 256) {
-        uint32_t kv[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int j = j0 + u * 256 + tid;
-          const int q = j < tot_c ? owner[j] : 0;
-          kv[u] = j < tot_c ? a.cand_key[reg + (long)q * kChunk + (j - pc[q])] : 0u;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int j = j0 + u * 256 + tid;
-          if (j < tot_c) ck[j] = kv[u];
-        }
-      }
-    }
-    // radix select of the need-th largest candidate on the low 20 key bits (the bin fixes the top 12)
-    uint32_t prefix = 0u, pmask = 0u;
-    remaining = need;
-#pragma unroll 1
-    for (int pass = 0; pass < 2; ++pass) {
-      const int shift = pass == 0 ? 10 : 0;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) hist[4 * tid + u] = 0;
-      __syncthreads();
-#pragma unroll 1
-      for (int j = tid; j < tot_c; j += 256) {
-        const uint32_t d = key_of(j) & 0xfffffu;
-        if ((d & pmask) == prefix) atomicAdd(&hist[(d >> shift) & 1023], 1);
-      }
-      __syncthreads();
-      // thread t owns bins 1023 - 4t .. 1020 - 4t (high to low)
-      int hb[4], local = 0;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        hb[u] = hist[1023 - 4 * tid - u];
-        local += hb[u];
-      }
-      int total;
-      int greater = block_scan<256>(local, tmp, &total);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (greater < remaining && remaining <= greater + hb[u]) {
-          s_digit = 1023 - 4 * tid - u;
-          s_rem = remaining - greater;
-        }
-        greater += hb[u];
-      }
-      __syncthreads();
-      prefix |= (uint32_t)s_digit << shift;
-      pmask |= 1023u << shift;
-      remaining = s_rem;
-      __syncthreads();
-    }
-    T = ((uint32_t)B << 20) | prefix;
+    });
   }
   DSV41_TS(4);
-  // ---- per chunk: candidates above / equal to T (thread t: chunks 4t .. 4t+3)
+  // Equal candidates are taken lowest position first, so the equal ones taken before chunk q are
+  // min(remaining, equal candidates before q), and chunk q's output offset is
+  // (above B before q) + (candidates above T before q) + that.
   {
-    int g4[4], e4[4];
-    if (staged) {  // one thread per candidate, LDS counters per chunk
+    int lg = 0, le = 0;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        cout[4 * tid + u] = 0;
-        ceq[4 * tid + u] = 0;
-      }
-      __syncthreads();
-      if (need > 0) {
-#pragma unroll 1
-        for (int j = tid; j < tot_c; j += 256) {
-          const uint32_t key = ck[j];
-          if (key > T) atomicAdd(&cout[owner[j]], 1);
-          else if (key == T) atomicAdd(&ceq[owner[j]], 1);
-        }
-      }
-      __syncthreads();
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        g4[u] = cout[4 * tid + u];
-        e4[u] = ceq[4 * tid + u];
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int q = 4 * tid + u;
-        g4[u] = e4[u] = 0;
-        if (q < nch && need > 0) {
-#pragma unroll 1
-          for (int j = pc[q]; j < pc[q + 1]; ++j) {
-            const uint32_t key = key_of(j);
-            g4[u] += key > T;
-            e4[u] += key == T;
-          }
-        }
-      }
+    for (int u = 0; u < CPT; ++u) {
+      lg += g[u];
+      le += e[u];
     }
-    int le = e4[0] + e4[1] + e4[2] + e4[3], tot_e;
-    int eb = block_scan<256>(le, tmp, &tot_e);  // equal candidates in earlier chunks
-    int taken[4], lt = 0;
+    int2 gx = block_scan2_dpp<256>(lg, le, t3, &tot);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      int t = remaining - eb;
-      t = t < 0 ? 0 : (t > e4[u] ? e4[u] : t);
-      taken[u] = na[u] + g4[u] + t;
-      ceq[4 * tid + u] = eb;
-      eb += e4[u];
-      lt += taken[u];
-    }
-    int tot_t;
-    int ob = block_scan<256>(lt, tmp, &tot_t);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      cout[4 * tid + u] = ob;
-      ob += taken[u];
+    for (int u = 0; u < CPT; ++u) {
+      if (qb + u == ch) {
+        s_out0 = pa_ch + gx.x + min(remaining, gx.y);
+        s_eq0 = gx.y;
+      }
+      gx.x += g[u];
+      gx.y += e[u];
     }
   }
   __syncthreads();
   DSV41_TS(5);
-  const int out0 = cout[ch], eq0 = ceq[ch];
+  const int out0 = s_out0, avail = max(0, remaining - s_eq0);  // equal candidates this chunk may take
   // ---- this chunk's taken positions in index order
-  int nt = 0, ne = 0;
-  bool is_eq[4], take[4];
-  uint32_t key[4];
+  int ne = 0, ns = 0;
+  bool is_eq[4], strict[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const bool in = p0 + e < c;
-    key[e] = score_key(v[e]);
-    const int b = (int)(key[e] >> 20);
-    is_eq[e] = in && need > 0 && b == B && key[e] == T;
-    take[e] = in && (b > B || (need > 0 && b == B && key[e] > T));
-    ne += is_eq[e];
+  for (int i = 0; i < 4; ++i) {
+    const bool in = p0 + i < c;
+    const uint32_t key = score_key(v[i]);
+    const int b = (int)(key >> 20);
+    is_eq[i] = in && need > 0 && b == B && key == T;
+    strict[i] = in && (b > B || (need > 0 && b == B && key > T));
+    ne += is_eq[i];
+    ns += strict[i];
   }
-  int tot_e2;
-  int er = eq0 + block_scan<256>(ne, tmp, &tot_e2);  // rank of this thread's first equal candidate
+  const int2 px = block_scan2_dpp<256>(ne, ns, t0, &tot);
+  int er = px.x, o = out0 + px.y + min(px.x, avail);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    if (is_eq[e]) {
-      take[e] = er < remaining;
-      ++er;
-    }
-    nt += take[e];
-  }
-  int tot_t2;
-  int o = out0 + block_scan<256>(nt, tmp, &tot_t2);
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-    if (take[e]) {
-      if (o < k) orow[o] = p0 + e + a.offset;
+  for (int i = 0; i < 4; ++i) {
+    if (strict[i] || (is_eq[i] && er < avail)) {
+      if (o < k) orow[o] = p0 + i + a.offset;
       ++o;
     }
+    er += is_eq[i];
+  }
   DSV41_TS(6);
+  // the row's histogram back to zero for the next step, a slice per chunk (last: no wait ever covers these stores)
+  const int per = (kBins + nch - 1) / nch, h1 = min(kBins, (ch + 1) * per);
+#pragma unroll 1
+  for (int i = ch * per + tid; i < h1; i += 256) gh[i] = 0;
 }
 
 // ------------------------------------------------------------------------------------------------ one launch
@@ -876,7 +827,8 @@ int dsv41_select_topk(const float* score, long ld, int R, int n, int k, const lo
   select_chunks_kernel<<<dim3(nch, R), 256, 0, st>>>(a);
   DSV41_CHECK_LAUNCH();
   if ((long)R * nch <= kEmitMaxGrid && kEmit) {  // few rows: every chunk's workgroup emits its own positions
-    emit_kernel<<<dim3(nch, R), 256, 0, st>>>(a);
+    if (nch <= 256) emit_kernel<1><<<dim3(nch, R), 256, 0, st>>>(a);
+    else emit_kernel<2><<<dim3(nch, R), 256, 0, st>>>(a);
   } else {
     finalize_kernel<<<R, kFinThreads, 0, st>>>(a);
   }

@@ -406,6 +406,9 @@ def test_decode_appends_fused():
 
 @pytest.mark.parametrize("n,k,cls", [(32769, 2048, [32768, 32768, 20000, 1500]), (262145, 2048, [262144]),
                                      (4097, 512, [4096, 4000, 511, 0]), (32768, 2048, [32768, 32768, 20000, 1500]),
+                                     (262145, 2048, [262144, 200000]),
+                                     (200000, 2048, [200000, 150000]), (131072, 1024, [131072, 100000] * 5),
+                                     (65536, 2048, [65536] * 9 + [40000, 3000, 2049]), (32768, 512, [32768, 9000] * 10),
                                      (32768, 512, [32768, 30000, 513, 512, 7, 32768]), (36864, 1024, [36864, 33000])])
 def test_select_topk_histogram_path(n, k, cls):
     """Decode top-k from (scores, histogram): bit-exact against the oracle's selection on the same scores,
