@@ -550,22 +550,29 @@ DSV41_DEV int block_excl_scan(int v, int* tmp, int* total) {
   return block_scan_dpp<NT>(v, tmp, total);
 }
 
-// Radix select on d = key - kmin (the row's own key range), 11-bit digits from the top of the range down, so the
-// first histogram already spreads the scores over 2048 bins whatever their magnitude; then an ordered emission in
-// which every wave owns a contiguous chunk and places its selected indices with ballots (ascending order, ties at
-// the threshold taken lowest index first).  Rows with <= kTopkCache valid positions are staged in LDS once.
+// Top-k of a row in ascending index order (ties at the threshold taken lowest index first).  Every wave owns a
+// contiguous chunk of the row for the counting and emission passes.
+// Rows of <= CACHE valid positions (staged in LDS as order-preserving keys): the load also builds a 4096-bin
+// histogram of the keys' top 12 bits (sign, exponent, 3 mantissa bits), whose scan gives the bin Bn holding the k-th
+// largest key; one pass then counts each wave's entries above Bn and lists its bin-Bn candidates, the exact threshold
+// is a radix select over the listed candidates' low 20 bits, and the emission pass places each wave's selected
+// indices with ballots: three passes over the row.  Rows not staged, or with more candidates than a wave's list
+// holds: radix select on d = key - kmin (the row's own key range) with 11-bit digits from the top of the range down,
+// then a counting pass and the emission pass.
 template <int NT, int CACHE>
 __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
   constexpr int kTopkThreads = NT;
   constexpr int kTopkCache = CACHE;
   constexpr int NW = NT / 64;
-  constexpr int B = 8;  // independent loads in flight per thread per batch
+  constexpr int B = 8;              // independent loads in flight per thread per batch
+  constexpr int kList = 2048 / NW;  // candidates listed per wave (the lists reuse the histogram's 8 KB)
   __shared__ uint32_t keys[kTopkCache];
-  __shared__ int hist[2048];
+  __shared__ int hist[2048];    // general path: 2048 bins; staged rows: 4096 16-bit bins, then the candidate lists
+  __shared__ uint32_t h2[512];  // 1024 16-bit bins over the listed candidates' digits
   __shared__ int scan_tmp[32];
   __shared__ uint32_t red_min[NW], red_max[NW];
-  __shared__ int w_gt[NW], w_eq[NW], w_take[NW], w_base[NW];
-  __shared__ int s_digit, s_rem;
+  __shared__ int w_gt[NW], w_eq[NW], w_take[NW], w_base[NW], w_nc[NW];
+  __shared__ int s_digit, s_rem, s_bin, s_over;
   const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* row = a.score + (long)r * a.ld;
   int* orow = a.out + (long)r * a.out_rstride;
@@ -577,10 +584,28 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
     return;
   }
   const bool cached = c <= kTopkCache;
+  uint32_t* hb16 = (uint32_t*)hist;  // 16-bit bin b: half (b & 1) of word b >> 1
+  if (cached) {
+#pragma unroll 1
+    for (int i = tid; i < 2048; i += kTopkThreads) hb16[i] = 0u;
+    if (tid == 0) s_over = 0;
+    __syncthreads();
+  }
   // key of element i (i < c), from LDS when staged
   auto key_at = [&](int i) -> uint32_t { return cached ? keys[i] : score_key(row[i]); };
 
   uint32_t kmin = 0xffffffffu, kmax = 0u;
+  auto stage_key = [&](float v) -> uint32_t {  // the key, counted in the histogram (staged rows) and the range
+    const uint32_t key = score_key(v);
+    if (cached) atomicAdd(&hb16[key >> 21], 1u << ((key >> 16) & 16));  // bin key >> 20
+    kmin = min(kmin, key);
+    kmax = max(kmax, key);
+    return key;
+  };
+  auto stage = [&](int i, float v) {
+    const uint32_t key = stage_key(v);
+    if (cached) keys[i] = key;
+  };
   if ((((uintptr_t)row) & 15) == 0) {  // 16-byte aligned row: float4 loads, 4 x B elements per thread per batch
     for (int i0 = 4 * tid; i0 < c; i0 += 4 * B * kTopkThreads) {
       float4 v[B];
@@ -597,16 +622,20 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
       }
 #pragma unroll
       for (int u = 0; u < B; ++u) {
+        const int i = i0 + 4 * u * kTopkThreads;
         const float vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        if (i + 3 < c) {  // the 4 keys in one 16-byte LDS store (consecutive lanes, consecutive 16 bytes)
+          uint32_t kq[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = i0 + 4 * u * kTopkThreads + e;
-          if (i < c) {
-            const uint32_t key = score_key(vv[e]);
-            if (cached) keys[i] = key;
-            kmin = min(kmin, key);
-            kmax = max(kmax, key);
-          }
+          for (int e = 0; e < 4; ++e) kq[e] = stage_key(vv[e]);
+          if (cached) *(uint4*)&keys[i] = make_uint4(kq[0], kq[1], kq[2], kq[3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (i + e < c) {
+              const uint32_t key = stage_key(vv[e]);
+              if (cached) keys[i + e] = key;
+            }
         }
       }
     }
@@ -621,12 +650,7 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
 #pragma unroll
       for (int u = 0; u < B; ++u) {
         const int i = i0 + u * kTopkThreads;
-        if (i < c) {
-          const uint32_t key = score_key(v[u]);
-          if (cached) keys[i] = key;
-          kmin = min(kmin, key);
-          kmax = max(kmax, key);
-        }
+        if (i < c) stage(i, v[u]);
       }
     }
   }
@@ -639,11 +663,7 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
     red_min[wave] = kmin;
     red_max[wave] = kmax;
   }
-  if (tid == 0) {
-    s_digit = 0;
-    s_rem = k;
-  }
-  __syncthreads();
+  __syncthreads();  // (also completes the staged keys and their histogram)
   kmin = red_min[0];
   kmax = red_max[0];
 #pragma unroll
@@ -651,78 +671,201 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
     kmin = min(kmin, red_min[w]);
     kmax = max(kmax, red_max[w]);
   }
-  const uint32_t range = kmax - kmin;
-  int shift = range ? 32 - __clz((int)range) : 0;
-  uint32_t prefix = 0u, pmask = 0u;
+  const int chunk = ((c + NW * 64 - 1) / (NW * 64)) * 64;
+  const int i0 = min(c, wave * chunk), i1 = min(c, i0 + chunk);
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  uint32_t thr = 0u;  // the k-th largest key; `remaining` elements equal to it are taken
   int remaining = k;
-  while (shift > 0) {
-    const int bits = shift < 11 ? shift : 11;
-    shift -= bits;
-    const int nb = 1 << bits;
-    for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
-    __syncthreads();
-    for (int i0 = tid; i0 < c; i0 += B * kTopkThreads) {
-      uint32_t d[B];
-#pragma unroll
-      for (int u = 0; u < B; ++u) {
-        const int i = i0 + u * kTopkThreads;
-        d[u] = key_at(i < c ? i : 0) - kmin;
-      }
-#pragma unroll
-      for (int u = 0; u < B; ++u)
-        if (i0 + u * kTopkThreads < c && (d[u] & pmask) == prefix) atomicAdd(&hist[(d[u] >> shift) & (nb - 1)], 1);
-    }
-    __syncthreads();
-    // descending suffix counts: thread t owns BPT consecutive bins starting at BPT*u, u = NT-1-t (high -> low)
-    constexpr int BPT = 2048 / NT;
-    const int u = kTopkThreads - 1 - tid;
-    int hb[BPT];
-    int local = 0;
+  bool fast = cached;
+  if (fast) {
+    // ---- threshold bin: thread t owns bins 4095 - BPT t .. 4096 - BPT (t + 1) (high to low)
+    constexpr int BPT = 4096 / NT;
+    int hb[BPT], local = 0;
 #pragma unroll
     for (int i = 0; i < BPT; ++i) {
-      hb[i] = BPT * u + i < nb ? hist[BPT * u + i] : 0;
+      const int b = 4095 - BPT * tid - i;
+      hb[i] = (int)((hb16[b >> 1] >> ((b & 1) * 16)) & 0xffffu);
       local += hb[i];
     }
     int total;
-    int greater = block_excl_scan<NT>(local, scan_tmp, &total);  // elements in bins above this thread's range
+    int greater = block_excl_scan<NT>(local, scan_tmp, &total);
 #pragma unroll
-    for (int i = BPT - 1; i >= 0; --i) {
-      if (BPT * u + i < nb && greater < remaining && remaining <= greater + hb[i]) {
-        s_digit = BPT * u + i;
-        s_rem = remaining - greater;
+    for (int i = 0; i < BPT; ++i) {
+      if (greater < k && k <= greater + hb[i]) {
+        s_bin = 4095 - BPT * tid - i;
+        s_rem = k - greater;
       }
       greater += hb[i];
     }
     __syncthreads();
-    prefix |= (uint32_t)s_digit << shift;
-    pmask |= (uint32_t)(nb - 1) << shift;
-    remaining = s_rem;
+    const uint32_t bn = (uint32_t)s_bin;
+    const int need = s_rem;  // candidates of bin bn to take
+    // ---- per wave: entries above bn, and the list of bin-bn candidates
+    uint32_t* wl = hb16 + wave * kList;
+    int gt = 0, nc = 0;
+    for (int b0 = i0; b0 < i1; b0 += 64 * B) {
+      uint32_t kk[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int i = b0 + u * 64 + lane;
+        kk[u] = keys[i < i1 ? i : i0];
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const bool in = b0 + u * 64 + lane < i1;
+        const uint32_t bin = kk[u] >> 20;
+        gt += in && bin > bn;
+        const bool cand = in && bin == bn;
+        const unsigned long long bc = __ballot(cand);
+        const int p = nc + __popcll(bc & lt);
+        if (cand && p < kList) wl[p] = kk[u];
+        nc += __popcll(bc);
+      }
+    }
+    gt = __reduce_add_sync(~0ull, gt);
+    if (lane == 0) {
+      w_gt[wave] = gt;
+      w_nc[wave] = nc;
+      if (nc > kList) s_over = 1;
+    }
     __syncthreads();
-  }
-  const uint32_t thr = kmin + prefix;  // the k-th largest key; `remaining` elements equal to it are taken
-  // ---- ordered emission: wave w owns [w*chunk, (w+1)*chunk) of the row, 64 positions per step
-  const int chunk = ((c + NW * 64 - 1) / (NW * 64)) * 64;
-  const int i0 = min(c, wave * chunk), i1 = min(c, i0 + chunk);
-  int gt = 0, eq = 0;
-  for (int b0 = i0; b0 < i1; b0 += 64 * B) {
-    uint32_t kk[B];
+    if (s_over == 0) {
+      // ---- radix select of the need-th largest listed candidate on the low 20 bits (10 + 10)
+      uint32_t prefix = 0u, pmask = 0u;
+      int rem = need;
+#pragma unroll 1
+      for (int pass = 0; pass < 2; ++pass) {
+        const int shift = pass == 0 ? 10 : 0;
+        for (int i = tid; i < 512; i += kTopkThreads) h2[i] = 0u;
+        __syncthreads();
+#pragma unroll 1
+        for (int w = 0; w < NW; ++w) {
+          const int n = w_nc[w];
+#pragma unroll 1
+          for (int j = tid; j < n; j += kTopkThreads) {
+            const uint32_t d = hb16[w * kList + j] & 0xfffffu;
+            if ((d & pmask) == prefix) {
+              const uint32_t dg = (d >> shift) & 1023u;
+              atomicAdd(&h2[dg >> 1], 1u << ((dg & 1u) * 16));
+            }
+          }
+        }
+        __syncthreads();
+        constexpr int BP2 = 1024 / NT;  // thread t owns digits 1023 - BP2 t .. (high to low)
+        int hd[BP2], loc2 = 0;
 #pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const int i = b0 + u * 64 + lane;
-      kk[u] = key_at(i < i1 ? i : i0);
-    }
+        for (int i = 0; i < BP2; ++i) {
+          const int dg = 1023 - BP2 * tid - i;
+          hd[i] = (int)((h2[dg >> 1] >> ((dg & 1) * 16)) & 0xffffu);
+          loc2 += hd[i];
+        }
+        int tot2;
+        int gr = block_excl_scan<NT>(loc2, scan_tmp, &tot2);
 #pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const bool in = b0 + u * 64 + lane < i1;
-      gt += in && kk[u] > thr;
-      eq += in && kk[u] == thr;
+        for (int i = 0; i < BP2; ++i) {
+          if (gr < rem && rem <= gr + hd[i]) {
+            s_digit = 1023 - BP2 * tid - i;
+            s_rem = rem - gr;
+          }
+          gr += hd[i];
+        }
+        __syncthreads();
+        prefix |= (uint32_t)s_digit << shift;
+        pmask |= 1023u << shift;
+        rem = s_rem;
+        __syncthreads();
+      }
+      thr = (bn << 20) | prefix;
+      remaining = rem;
+      // per wave: its listed candidates above / equal to the threshold
+      int g2 = 0, e2 = 0;
+#pragma unroll 1
+      for (int j = lane; j < nc; j += 64) {
+        const uint32_t key = wl[j];
+        g2 += key > thr;
+        e2 += key == thr;
+      }
+      g2 = __reduce_add_sync(~0ull, g2);
+      e2 = __reduce_add_sync(~0ull, e2);
+      if (lane == 0) {
+        w_gt[wave] += g2;
+        w_eq[wave] = e2;
+      }
+    } else {
+      fast = false;  // (uniform: s_over is read after the barrier)
     }
   }
-  gt = __reduce_add_sync(~0ull, gt);
-  eq = __reduce_add_sync(~0ull, eq);
-  if (lane == 0) {
-    w_gt[wave] = gt;
-    w_eq[wave] = eq;
+  if (!fast) {
+    const uint32_t range = kmax - kmin;
+    int shift = range ? 32 - __clz((int)range) : 0;
+    uint32_t prefix = 0u, pmask = 0u;
+    remaining = k;
+    while (shift > 0) {
+      const int bits = shift < 11 ? shift : 11;
+      shift -= bits;
+      const int nb = 1 << bits;
+      for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
+      __syncthreads();
+      for (int j0 = tid; j0 < c; j0 += B * kTopkThreads) {
+        uint32_t d[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const int i = j0 + u * kTopkThreads;
+          d[u] = key_at(i < c ? i : 0) - kmin;
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u)
+          if (j0 + u * kTopkThreads < c && (d[u] & pmask) == prefix) atomicAdd(&hist[(d[u] >> shift) & (nb - 1)], 1);
+      }
+      __syncthreads();
+      // descending suffix counts: thread t owns BPT consecutive bins starting at BPT*u, u = NT-1-t (high -> low)
+      constexpr int BPT = 2048 / NT;
+      const int u = kTopkThreads - 1 - tid;
+      int hb[BPT];
+      int local = 0;
+#pragma unroll
+      for (int i = 0; i < BPT; ++i) {
+        hb[i] = BPT * u + i < nb ? hist[BPT * u + i] : 0;
+        local += hb[i];
+      }
+      int total;
+      int greater = block_excl_scan<NT>(local, scan_tmp, &total);  // elements in bins above this thread's range
+#pragma unroll
+      for (int i = BPT - 1; i >= 0; --i) {
+        if (BPT * u + i < nb && greater < remaining && remaining <= greater + hb[i]) {
+          s_digit = BPT * u + i;
+          s_rem = remaining - greater;
+        }
+        greater += hb[i];
+      }
+      __syncthreads();
+      prefix |= (uint32_t)s_digit << shift;
+      pmask |= (uint32_t)(nb - 1) << shift;
+      remaining = s_rem;
+      __syncthreads();
+    }
+    thr = kmin + prefix;
+    int gt = 0, eq = 0;
+    for (int b0 = i0; b0 < i1; b0 += 64 * B) {
+      uint32_t kk[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const int i = b0 + u * 64 + lane;
+        kk[u] = key_at(i < i1 ? i : i0);
+      }
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const bool in = b0 + u * 64 + lane < i1;
+        gt += in && kk[u] > thr;
+        eq += in && kk[u] == thr;
+      }
+    }
+    gt = __reduce_add_sync(~0ull, gt);
+    eq = __reduce_add_sync(~0ull, eq);
+    if (lane == 0) {
+      w_gt[wave] = gt;
+      w_eq[wave] = eq;
+    }
   }
   __syncthreads();
   if (tid == 0) {
@@ -737,9 +880,9 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
     }
   }
   __syncthreads();
+  // ---- ordered emission over the wave's chunk, 64 positions per step
   const int take = w_take[wave];
   int base = w_base[wave], eq_seen = 0;
-  const unsigned long long lt = (1ull << lane) - 1ull;
   for (int b0 = i0; b0 < i1; b0 += 64 * B) {
     uint32_t kk[B];
 #pragma unroll
