@@ -594,11 +594,13 @@ int is_slots(int n_pos) { return (n_pos + kIsChunk - 1) / kIsChunk; }
 // one-launch selection takes (the selection follows as its own launches, dsv41_select_topk).  Score grid: chunks of
 // 1024 positions, 16 waves x 64 keys (the layout of the long-row score kernel: chunk x of row r runs on XCD x mod 8),
 // the row's e4m3 queries prepared in every workgroup (the first 512 threads, into LDS) while its keys are in flight.
-// After the score grid, 3 append-only workgroups per row: the ring row, the compressed row and the index key; for a
+// Before the score grid (dispatched first: a score workgroup holds a CU alone, so workgroups placed after a full
+// score grid would wait for one to finish), 3 append-only workgroups per row: the ring row, the compressed row and
+// the index key; for a
 // row whose step closes a group the last one also scores the new key (position cl - 1: the same MFMA tile as the
 // chunks', one valid column) and adds it to the row's histogram, and the chunk holding that position skips it (its
 // table row is read before it is written).  The launch boundary orders all of it before the selection.
-constexpr int kDsWaves = 16;
+constexpr int kDsWaves = 16;  // (8-wave workgroups, two per CU: 21.2 against 16.8 us at C4)
 constexpr int kDsThreads = 64 * kDsWaves;
 constexpr int kDsChunk = kDsWaves * kKeysPerWave;
 
@@ -613,7 +615,7 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
   const IsAppend& ap = d.app;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int l16 = lane & 15, g = lane >> 4;
-  const int main_wgs = (d.nx + kXcds - 1) / kXcds * kXcds * a.R;
+  const int app_wgs = (3 * a.R + kXcds - 1) / kXcds * kXcds;  // (a multiple of 8: the score grid keeps its XCDs)
   __shared__ int lhist[kHistBins];
   __shared__ __align__(16) uint8_t qs[64 * 128];
   __shared__ float wfl[64];
@@ -643,22 +645,27 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
       for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[ht], 4 * g + i, 64);
   };
   uint4 qa16[kHT][4];  // (unused: e4m3 keys)
-  if ((int)blockIdx.x >= main_wgs) {  // ---- append-only workgroups: (row, which) = (e / 3, e % 3)
-    const int e = (int)blockIdx.x - main_wgs, r = e / 3, which = e % 3;
+  if ((int)blockIdx.x < app_wgs) {  // ---- append-only workgroups: (row, which) = (e / 3, e % 3)
+    const int e = (int)blockIdx.x, r = e / 3, which = e % 3;
+    if (e >= 3 * a.R) return;
+    DSV41_PH(6);
     const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
     const long ppos = ap.pos[r];
     const bool closes = ((ppos + 1) % ap.ratio) == 0;
     if (which == 1 && !(ap.latent && ap.ckv)) return;
     if (which == 0) {  // (constant operation indices: the row operation's fields stay in registers)
       row_op<kDsThreads>(is_app_op(ap, r, slot, ppos, 0, nullptr, nullptr), redf);
+      DSV41_PH(7);
       return;
     }
     if (which == 1) {
       row_op<kDsThreads>(is_app_op(ap, r, slot, ppos, 1, nullptr, nullptr), redf);
+      DSV41_PH(7);
       return;
     }
     if (!closes) {
       row_op<kDsThreads>(is_app_op(ap, r, slot, ppos, 2, nullptr, nullptr), redf);
+      DSV41_PH(7);
       return;
     }
     Qprep512 qp;
@@ -684,10 +691,11 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
         atomicAdd(a.hist + (long)r * kHistBins + (score_key(v) >> 20), 1);
       }
     }
+    DSV41_PH(7);
     return;
   }
   // ---- score grid (block b on XCD b % 8; chunk x of every row on XCD x % 8)
-  const int bxcd = blockIdx.x % kXcds, bj = blockIdx.x / kXcds;
+  const int bxcd = (blockIdx.x - app_wgs) % kXcds, bj = (blockIdx.x - app_wgs) / kXcds;
   const int r = bj % a.R, bx = (bj / a.R) * kXcds + bxcd;
   if (bx >= d.nx) return;
   long cl = row_cl(a, r);
@@ -696,6 +704,7 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
   const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
   const long ppos = ap.pos[r];
   const long knew_row = ((ppos + 1) % ap.ratio) == 0 ? (ppos + 1) / ap.ratio - 1 : -1;  // (-1: no new key)
+  DSV41_PH(0);
   Qprep512 qp;
   stage_queries(r, qp, true);
 #pragma unroll 1
@@ -715,7 +724,12 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
     ksc[nt] = pv ? a.kscale[slot * a.ks_sstride + p] : 0.0f;
   }
   stage_queries(r, qp, false);
+#ifdef DSV41_TIMING
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#endif
+  DSV41_PH(1);
   __syncthreads();  // queries staged, histogram cleared
+  DSV41_PH(2);
   i32x8_t qa8[kHT];
   float wr[kHT][4];
   read_queries(qa8, wr);
@@ -730,13 +744,19 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
       atomicAdd(&lhist[score_key(v) >> 20], 1);
     }
   }
+  DSV41_PH(3);
   __syncthreads();
+  DSV41_PH(4);
   int* gh = a.hist + (long)r * kHistBins;
 #pragma unroll 1
   for (int i = t; i < kHistBins / 2; i += kDsThreads) {  // bins in pairs: one 64-bit add (no carry out of a bin)
     const uint32_t lo = (uint32_t)lhist[2 * i], hi = (uint32_t)lhist[2 * i + 1];
     if (lo | hi) atomicAdd((unsigned long long*)(gh + 2 * i), ((unsigned long long)hi << 32) | lo);
   }
+#ifdef DSV41_TIMING
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#endif
+  DSV41_PH(5);
 }
 
 }  // namespace
@@ -893,7 +913,7 @@ int dsv41_decode_score(const void* kv_raw, const void* kv_norm, void* ring, long
                    (const uint16_t*)k_norm, (uint16_t*)kbf, kbf_sstride, (uint8_t*)k8, k8_sstride, ks, ks_sstride,
                    kcap, pos, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx};
   d.nx = (n_pos + kDsChunk - 1) / kDsChunk;
-  const int grid = (d.nx + kXcds - 1) / kXcds * kXcds * R + 3 * R;
+  const int grid = (3 * R + kXcds - 1) / kXcds * kXcds + (d.nx + kXcds - 1) / kXcds * kXcds * R;
   decode_score_kernel<<<grid, kDsThreads, 0, (hipStream_t)stream>>>(d);
   DSV41_CHECK_LAUNCH();
   return 0;
