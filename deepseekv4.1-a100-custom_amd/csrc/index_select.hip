@@ -700,7 +700,10 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
   if (bx >= d.nx) return;
   long cl = row_cl(a, r);
   if (cl > a.n_pos) cl = a.n_pos;
-  if ((long)bx * kDsChunk >= cl) return;
+  // Positions: chunk bx (its 16 waves x 4 tiles of 16), and past the d.nx chunks of the row one more tile per wave
+  // (tile 64 nx + 16 bx + wave), so that a grid capped at the free CUs still covers the row.
+  const long x0 = (64L * d.nx + 16 * bx) * 16;  // first position of this workgroup's extra tiles
+  if ((long)bx * kDsChunk >= cl && x0 >= cl) return;
   const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
   const long ppos = ap.pos[r];
   const long knew_row = ((ppos + 1) % ap.ratio) == 0 ? (ppos + 1) / ap.ratio - 1 : -1;  // (-1: no new key)
@@ -711,13 +714,15 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
   for (int i = t; i < kHistBins; i += kDsThreads) lhist[i] = 0;
   const int lim = (int)cl;
   const int kt0 = bx * kDsChunk + wave * kKeysPerWave;
-  constexpr int NT = 4;
+  constexpr int NT = 5;  // 4 tiles of the chunk, the extra tile
+  const bool extra = x0 + 16 * wave < cl;  // (wave-uniform)
+  auto tile_pos = [&](int nt) { return nt < 4 ? kt0 + nt * 16 + l16 : (int)x0 + 16 * wave + l16; };
   uint4 k0[NT], k1[NT];
   float ksc[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int p = kt0 + nt * 16 + l16;
-    const bool pv = p < lim;
+    const int p = tile_pos(nt);
+    const bool pv = p < lim && (nt < 4 || extra);
     const uint8_t* krow = (const uint8_t*)a.keys + slot * a.k_sstride + (long)p * 128 + g * 32;
     k0[nt] = pv ? *(const uint4*)krow : make_uint4(0, 0, 0, 0);
     k1[nt] = pv ? *(const uint4*)(krow + 16) : make_uint4(0, 0, 0, 0);
@@ -736,7 +741,8 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
   float* orow = a.out + (long)r * a.out_rstride;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int p = kt0 + nt * 16 + l16;
+    if (nt == 4 && !extra) break;
+    const int p = tile_pos(nt);
     const float sum = score_tile<1>(qa8, qa16, wr, nht, k0[nt], k1[nt], nullptr);
     if (g == 0 && p < lim && p != knew_row) {  // (the new key's position is its append workgroup's)
       const float v = is_cand(a, r, p) ? sum * ksc[nt] : -__builtin_inff();
@@ -837,6 +843,20 @@ int select_launch(const IsArgs& g, hipStream_t st) {
 
 }  // namespace
 
+namespace {
+// Compute units of the current device (queried once per device; 256 when the query fails).
+int ds_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
+}
+}  // namespace
+
 extern "C" {
 
 int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_rstride, int R, int HI,
@@ -912,8 +932,15 @@ int dsv41_decode_score(const void* kv_raw, const void* kv_norm, void* ring, long
                    (const uint16_t*)latent, (uint16_t*)ckv, ckv_sstride, cap, (const uint16_t*)k_raw,
                    (const uint16_t*)k_norm, (uint16_t*)kbf, kbf_sstride, (uint8_t*)k8, k8_sstride, ks, ks_sstride,
                    kcap, pos, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx};
-  d.nx = (n_pos + kDsChunk - 1) / kDsChunk;
-  const int grid = (3 * R + kXcds - 1) / kXcds * kXcds + (d.nx + kXcds - 1) / kXcds * kXcds * R;
+  // chunks per row: the row's chunks rounded up to a multiple of 8, or, when that overfills the CUs the append
+  // workgroups leave, as many as fit (a multiple of 8 again) provided one extra tile per wave covers the rest
+  const int app_wgs = (3 * R + kXcds - 1) / kXcds * kXcds;
+  int nx = (n_pos + kDsChunk - 1) / kDsChunk;
+  nx = (nx + kXcds - 1) / kXcds * kXcds;
+  const int fit = (ds_cus() - app_wgs) / R / kXcds * kXcds;
+  if (fit >= kXcds && nx > fit && (64L * fit + 16L * fit) * 16 >= n_pos) nx = fit;
+  d.nx = nx;
+  const int grid = app_wgs + nx * R;
   decode_score_kernel<<<grid, kDsThreads, 0, (hipStream_t)stream>>>(d);
   DSV41_CHECK_LAUNCH();
   return 0;
