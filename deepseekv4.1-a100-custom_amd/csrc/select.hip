@@ -768,9 +768,13 @@ __global__ void __launch_bounds__(256) select_group_kernel(const GroupArgs g) {
 // each (rs = n rounded up to 32, so rows never share a cache line; the one-launch path uses the first two as 64-bit
 // candidate slots [R, rs]) | threshold bins [R] (padded to 8 bytes) | arrival counters [R] (64-bit) | timeout flag.
 long row_stride(int n) { return ((long)n + 31) / 32 * 32; }
+// Chunk count pairs, rounded up to 16 bytes: the per-chunk regions after them stay 16-byte aligned (the emission's
+// vector and direct-to-LDS loads of candidate keys).
+long count_ints(int R, long nch) { return ((long)R * nch * 2 + 3) / 4 * 4; }
+
 long select_base_bytes(int R, int n) {
   const long nch = (n + kChunk - 1) / kChunk;
-  return ((long)R * kBins + (long)R * nch * 2 + 3L * R * row_stride(n) + (R + 1L) / 2 * 2) * 4;  // (+ row bins)
+  return ((long)R * kBins + count_ints(R, nch) + 3L * R * row_stride(n) + (R + 1L) / 2 * 2) * 4;  // (+ row bins)
 }
 
 }  // namespace
@@ -805,7 +809,7 @@ int dsv41_select_topk(const float* score, long ld, int R, int n, int k, const lo
   a.hist = w;
   a.counts = w + (long)R * kBins;
   a.rs = row_stride(n);
-  a.above = a.counts + (long)R * nch * 2;
+  a.above = a.counts + count_ints(R, nch);
   a.cand_idx = a.above + (long)R * a.rs;
   a.cand_key = (uint32_t*)(a.cand_idx + (long)R * a.rs);
   a.nchunks = nch;
