@@ -169,6 +169,11 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   DSV41_PH(0);
   DSV41_PX(0);
   DSV41_TS(48);
+  Qprep512 qp;
+  // (FUSED) the row's queries first, in flight with the row data: issued after the key loads instead, they were
+  // waited for before the key addresses could reuse their address registers
+  if constexpr (FUSED)
+    if (!extra) qprep512_load(g.app.q_idx + (long)r * a.HI * 128, g.app.w_idx + (long)r * a.HI, a.HI, qp);
   const long clr = row_cl(a, r);
   const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
   // this launch's epoch: one more than the one this chunk's count word holds (earlier launches have completed)
@@ -190,7 +195,6 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   const IsAppend& ap = g.app;
   long ppos = 0, knew_row = -1;
   bool holder = false;  // (FUSED) this chunk holds the new key's position
-  Qprep512 qp;
   auto make_op = [&](int which) { return is_app_op(ap, r, slot, ppos, which, knew, &ksnew); };
   if constexpr (FUSED) {
     ppos = ap.pos[r];
@@ -249,7 +253,6 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
       return;
     }
     holder = closes && knew_row >= 0 && knew_row < c && ch == (int)(knew_row / kIsChunk);
-    qprep512_load(ap.q_idx + (long)r * a.HI * 128, ap.w_idx + (long)r * a.HI, a.HI, qp);
   } else {
     // the row's queries (64 heads x 128 e4m3 = 512 chunks of 16 bytes) go to LDS once, one direct load per thread
     // (every wave needs all of them); heads >= HI are never read back
@@ -264,20 +267,22 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   }
   DSV41_TS(49);
   DSV41_PX(1);
-#pragma unroll 1
-  for (int i = t; i < kHistBins; i += kIsThreads) lhist[i] = 0;
+  static_assert(kHistBins % kIsThreads == 0, "histogram clear");
+#pragma unroll
+  for (int j = 0; j < kHistBins / kIsThreads; ++j) lhist[t + j * kIsThreads] = 0;  // (no loop between the loads)
   constexpr int NT = kIsKeysPerWave / 16;  // column tiles of 16 keys per wave, all loads issued up front
   uint4 k0[NT], k1[NT];
   float ksc[NT];
   const int pw = ch * kIsChunk + wave * kIsKeysPerWave;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int p = pw + nt * 16 + l16;
-    const bool pv = p < c;
-    const uint8_t* krow = (const uint8_t*)a.keys + slot * a.k_sstride + (long)p * 128 + g4 * 32;
-    k0[nt] = pv ? *(const uint4*)krow : make_uint4(0, 0, 0, 0);
-    k1[nt] = pv ? *(const uint4*)(krow + 16) : make_uint4(0, 0, 0, 0);
-    ksc[nt] = pv ? a.kscale[slot * a.ks_sstride + p] : 0.0f;
+    // positions past the row load row 0 (unconditional loads: a select on a loaded value would make the compiler
+    // wait for it before the later tiles' loads are issued); their scores are not recorded
+    const int p = pw + nt * 16 + l16, pl = p < c ? p : 0;
+    const uint8_t* krow = (const uint8_t*)a.keys + slot * a.k_sstride + (long)pl * 128 + g4 * 32;
+    k0[nt] = *(const uint4*)krow;
+    k1[nt] = *(const uint4*)(krow + 16);
+    ksc[nt] = a.kscale[slot * a.ks_sstride + pl];
   }
   DSV41_TS(50);
   DSV41_PX(2);
@@ -698,6 +703,8 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
   const int bxcd = (blockIdx.x - app_wgs) % kXcds, bj = (blockIdx.x - app_wgs) / kXcds;
   const int r = bj % a.R, bx = (bj / a.R) * kXcds + bxcd;
   if (bx >= d.nx) return;
+  Qprep512 qp;
+  stage_queries(r, qp, true);  // (first: in flight with the row data)
   long cl = row_cl(a, r);
   if (cl > a.n_pos) cl = a.n_pos;
   // Positions: chunk bx (its 16 waves x 4 tiles of 16), and past the d.nx chunks of the row one more tile per wave
@@ -708,10 +715,9 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
   const long ppos = ap.pos[r];
   const long knew_row = ((ppos + 1) % ap.ratio) == 0 ? (ppos + 1) / ap.ratio - 1 : -1;  // (-1: no new key)
   DSV41_PH(0);
-  Qprep512 qp;
-  stage_queries(r, qp, true);
-#pragma unroll 1
-  for (int i = t; i < kHistBins; i += kDsThreads) lhist[i] = 0;
+  static_assert(kHistBins % kDsThreads == 0, "histogram clear");
+#pragma unroll
+  for (int j = 0; j < kHistBins / kDsThreads; ++j) lhist[t + j * kDsThreads] = 0;  // (no loop between the loads)
   const int lim = (int)cl;
   const int kt0 = bx * kDsChunk + wave * kKeysPerWave;
   constexpr int NT = 5;  // 4 tiles of the chunk, the extra tile
@@ -721,12 +727,14 @@ __global__ void __launch_bounds__(kDsThreads) decode_score_kernel(const DsArgs d
   float ksc[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int p = tile_pos(nt);
-    const bool pv = p < lim && (nt < 4 || extra);
-    const uint8_t* krow = (const uint8_t*)a.keys + slot * a.k_sstride + (long)p * 128 + g * 32;
-    k0[nt] = pv ? *(const uint4*)krow : make_uint4(0, 0, 0, 0);
-    k1[nt] = pv ? *(const uint4*)(krow + 16) : make_uint4(0, 0, 0, 0);
-    ksc[nt] = pv ? a.kscale[slot * a.ks_sstride + p] : 0.0f;
+    // positions past the row load row 0 (unconditional loads: a select on a loaded value would make the compiler
+    // wait for it before the later tiles' loads are issued); their scores are not recorded
+    const int p = tile_pos(nt), pl = p < lim ? p : 0;
+    if (nt == 4 && !extra) break;
+    const uint8_t* krow = (const uint8_t*)a.keys + slot * a.k_sstride + (long)pl * 128 + g * 32;
+    k0[nt] = *(const uint4*)krow;
+    k1[nt] = *(const uint4*)(krow + 16);
+    ksc[nt] = a.kscale[slot * a.ks_sstride + pl];
   }
   stage_queries(r, qp, false);
 #ifdef DSV41_TIMING

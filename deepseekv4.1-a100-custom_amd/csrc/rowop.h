@@ -224,7 +224,7 @@ DSV41_DEV void qprep_op(const uint16_t* q, const uint16_t* w_bf16, const float* 
 // arithmetic are separate calls so that the loads can be issued ahead.
 struct Qprep512 {
   uint4 raw[2];
-  float wv;
+  uint32_t wbits;  // the head weight's bf16 bits (converted where used: a conversion here would wait for the load)
 };
 
 DSV41_DEV void qprep512_load(const uint16_t* q, const uint16_t* w_bf16, int HI, Qprep512& g) {
@@ -233,7 +233,7 @@ DSV41_DEV void qprep512_load(const uint16_t* q, const uint16_t* w_bf16, int HI, 
   const uint4* src = (const uint4*)(q + (long)hc * 128 + part * 16);
   g.raw[0] = src[0];
   g.raw[1] = src[1];
-  g.wv = bf2f(w_bf16[hc]);
+  g.wbits = w_bf16[hc];
 }
 
 DSV41_DEV void qprep512_store(const Qprep512& g, int HI, uint8_t* q8, float* wf) {
@@ -263,7 +263,7 @@ DSV41_DEV void qprep512_store(const Qprep512& g, int HI, uint8_t* q8, float* wf)
     pk[d] = (uint32_t)wd;
   }
   *(uint4*)(q8 + h * 128 + part * 16) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-  if (part == 0) wf[h] = h < HI ? g.wv * pow2i(ex) : 0.0f;
+  if (part == 0) wf[h] = h < HI ? bf2f((uint16_t)g.wbits) * pow2i(ex) : 0.0f;
 }
 
 bool row_ok(int D, int group) {
