@@ -316,10 +316,10 @@ __global__ void __launch_bounds__(kFinThreads) finalize_kernel(const SelArgs a) 
 }
 
 // Per-chunk emission (replaces finalize for rows of few chunk groups): grid (chunks, rows) as select_chunks.  Every
-// workgroup of a row resolves the row's exact threshold itself -- the chunk counts, the candidates' keys (bin B, in
-// index order) and two 10-bit radix passes over them in LDS -- then counts per chunk the candidates above / equal to
-// the threshold key, and from the prefix over earlier chunks of (above B + taken candidates) writes its own chunk's
-// taken positions in index order (it re-reads its 1024 scores).  Ties at the threshold go to the lowest positions.
+// workgroup of a row resolves the row's exact threshold itself -- the chunk counts, the candidates' keys (bin B) and
+// two 10-bit radix passes over them in LDS -- then counts per chunk the candidates above / equal to the threshold
+// key, and from the prefix over earlier chunks of (above B + taken candidates) writes its own chunk's taken positions
+// in index order (it re-reads its 1024 scores).  Ties at the threshold go to the lowest positions.
 // The work is proportional to the candidates (a few percent of the row) per workgroup, and the row's workgroups run
 // in parallel where finalize ran one workgroup per row.  Each workgroup clears a slice of the row's histogram as its
 // last stores (this kernel reads the threshold bin select_chunks stored, not the histogram).
