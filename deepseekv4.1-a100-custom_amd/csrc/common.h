@@ -121,12 +121,6 @@ DSV41_DEV float row16_sum(float v) {
   v += dpp_mov<0x141>(v);        // row_half_mirror
   return v + dpp_mov<0x140>(v);  // row_mirror
 }
-// Integer sum over aligned groups of 8 lanes, the result in every lane of the group.
-DSV41_DEV int group8_sum(int v) {
-  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
-  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);   // quad_perm [2,3,0,1]
-  return v + __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);  // row_half_mirror
-}
 // Whole-wave sum, the result in every lane.
 DSV41_DEV float wave_sum(float v) { return row_sum4(row16_sum(v)); }
 // Maximum over aligned groups of `group` consecutive lanes (a power of two <= 64), the result in every lane.
