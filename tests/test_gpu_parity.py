@@ -759,44 +759,47 @@ def test_decode_appends_select_one_launch():
         _fp8_close(host(B.ring), host(A.ring), f"decode_select ring step {step}")
 
 
-def test_decode_score_appends_long_rows():
+@pytest.mark.parametrize("ctx", [[524288, 300000], [1048576]], ids=["two-rows", "C4-shape"])
+def test_decode_score_appends_long_rows(ctx):
     """dsv41_decode_score (the decode step's cache appends and the indexer scores with their histogram in one
     launch, rows past the one-launch selection) then the top-k == the appends launch, the score launch and the
     top-k (dsv41/decode.py:129-164, :284-294): the same indices and scores bit for bit, the index keys, scales and
     compressed rows bit for bit, the ring rows up to rare one-step fp8 flips, over a step that closes every row's
     group (the new key is scored by its append workgroup) and one that does not (spare rows), with a candidate
-    mask on the second."""
+    mask on the second.  The C4 shape (one row of 262144 positions) caps the score grid at the CUs the append
+    workgroups leave and covers the rest of the row with one extra tile per wave."""
     from dsv41_amd.decode import DecodeLayer
     from dsv41_amd.workloads import DecodeConfig, make_decode_inputs
-    cfg = DecodeConfig("T", [524288, 300000], topk=2048)
+    cfg = DecodeConfig("T", ctx, topk=2048)
+    R = len(ctx)
     layers, st = make_decode_inputs(cfg, DEV, seed=4)
     rd = 64
-    ang = torch.outer(torch.arange(524300, dtype=torch.float32),
+    ang = torch.outer(torch.arange(max(ctx) + 16, dtype=torch.float32),
                       1.0 / (10000.0 ** (torch.arange(0, rd, 2, dtype=torch.float32) / rd)))
     cos, sin = torch.cos(ang).to(DEV), torch.sin(ang).to(DEV)
     l0 = layers[0]
     mk = lambda: DecodeLayer(l0["ring"].clone(), l0["ckv"].clone(), l0["k8"].clone(), l0["ks"].clone(), st["sink"],  # noqa: E731
                              cos, sin, cfg.ratio, cfg.topk, rd=rd)
     A, B = mk(), mk()
-    assert not A.selector(2, DEV).one_launch
+    assert not A.selector(R, DEV).one_launch
     g = torch.Generator(device=DEV).manual_seed(6)
     for step in range(2):
         pos = st["pos"] + step  # step 0 closes both rows' groups, step 1 does not
-        kv_raw = torch.randn(2, 576, generator=g, device=DEV).to(torch.bfloat16)
-        latent = torch.randn(2, 1, 576, generator=g, device=DEV).to(torch.bfloat16)
-        k_raw = (torch.randn(2, 128, generator=g, device=DEV) * 2).to(torch.bfloat16)
+        kv_raw = torch.randn(R, 576, generator=g, device=DEV).to(torch.bfloat16)
+        latent = torch.randn(R, 1, 576, generator=g, device=DEV).to(torch.bfloat16)
+        k_raw = (torch.randn(R, 128, generator=g, device=DEV) * 2).to(torch.bfloat16)
         q_idx = st["q_idx"] * (1 + step)
-        cand = torch.rand(2, 1, A.k8.shape[1], generator=g, device=DEV) < 0.8 if step == 1 else None
+        cand = torch.rand(R, 1, A.k8.shape[1], generator=g, device=DEV) < 0.8 if step == 1 else None
         print(f"[decode_score] step {step} pos {pos.tolist()}", flush=True)
         A.appends(kv_raw, st["kv_norm"], latent, k_raw, st["k_norm"], pos, st["seq"], q_idx, st["w_idx"])
         cl = torch.div(pos + 1, cfg.ratio, rounding_mode="floor")
-        sa = A.selector(2, DEV)
+        sa = A.selector(R, DEV)
         want = sa(q_idx, A.k8, st["w_idx"], st["seq"], cl, k_scale=A.ks, prepared=A._prepared, cand=cand).clone()
         got = B.appends_select(kv_raw, st["kv_norm"], latent, k_raw, st["k_norm"], pos, st["seq"], q_idx,
                                st["w_idx"], cl=cl, cand=cand).clone()
         torch.cuda.synchronize()
         np.testing.assert_array_equal(got.cpu().numpy(), want.cpu().numpy(), err_msg=f"step {step}")
-        sb = B.selector(2, DEV)
+        sb = B.selector(R, DEV)
         for b, c in enumerate(cl.tolist()):
             np.testing.assert_array_equal(sb.score[b, :c].cpu().numpy(), sa.score[b, :c].cpu().numpy(),
                                           err_msg=f"scores row {b} step {step}")
