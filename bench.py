@@ -4,10 +4,11 @@
 A "step" is one decode layer-step of config C2 (4 slots x 131072 context, k 2048): the SWA ring append, the
 compressed-KV and index-key appends, the indexer score over the e4m3 keys, the top-k and the sparse attention over
 ring + top-k rows.  Inputs are resident in HBM; NL independent copies of the layer's caches are rotated so every
-step misses the 256 MB last-level cache.  The timed region replays a HIP graph of NL layer-steps K/NL times
-(rounded up) with events on the launch stream; the per-kernel durations behind `roofline` come from an eager pass
-with events around each launch, on the same stream; each heavy kernel is also replayed alone from a graph of NL
-launches for its average launch duration.
+step misses the 256 MB last-level cache.  The timed region replays a HIP graph of NL layer-steps max(20, K/NL)
+times, each replay between two events on the launch stream: the value is the median replay / NL (min, max and the
+whole region's mean are reported beside it); `steps` counts the layer-steps the timed region ran (replays x NL).
+Each heavy kernel is also replayed alone from a graph of NL launches for its average launch duration (the
+roofline denominator).  C4 and C5 are measured the same way and reported under decode_other_configs.
 
 Prints ONE JSON line (rank 0, N = 1)."""
 from __future__ import annotations
@@ -54,31 +55,38 @@ def decode_bytes(cfg, idx_sets=None, fused=True):
     return per_kernel
 
 
-def step_algorithmic_bytes(cfg):
-    """The per-step algorithmic byte count (keys incl. scale, gathered rows, ring, q,
-    index q, output, idx write + read), used for the headline roofline fraction."""
+def step_algorithmic_bytes(cfg, sel_union=None):
+    """The per-step algorithmic byte count (keys incl. scale, gathered rows, ring, q, index q, output, idx write +
+    read), used for the headline roofline fraction.  Gathered rows per slot: the union of its rows' selections
+    (sel_union, measured), or min(k, n) when not given (one row per slot: the same number)."""
     from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN
     tot = 0
     for s in range(cfg.slots):
         n = cfg.n_c(s)
         r = cfg.rows_per_slot
-        tot += n * (DI + 4) + min(cfg.topk, n) * DQK * 2 + WIN * DQK * 2
+        rows = min(cfg.topk, n) if sel_union is None else sel_union[s]
+        tot += n * (DI + 4) + rows * DQK * 2 + WIN * DQK * 2
         tot += r * (H * DQK * 2 + HI * DI + H * DV * 2 + cfg.topk * 4 * 2)
     return tot
 
 
-def run_decode(args, dev):
+def run_decode(args, dev, name: str, full: bool = True):
+    """One decode config: NL cache copies, the layer-step (the step's cache appends + scores + top-k in one launch,
+    then the attention; with --separate-appends the appends launch first) captured as a HIP graph of NL layer-steps
+    (one per copy).  The graph is replayed max(20, ceil(steps / NL)) times, each replay between two events on the
+    launch stream; the value is the median replay / NL, with the min and max.  full: also the eager per-launch
+    times (events around each launch) and each heavy kernel alone (a graph of NL launches of it, replayed; its
+    average launch duration is the roofline denominator)."""
+    import numpy as np
     import torch
     from dsv41_amd.decode import DecodeLayer
     from dsv41_amd.workloads import CONFIGS, make_decode_inputs
 
-    cfg = CONFIGS[args.config]
+    cfg = CONFIGS[name]
     NL = args.layers
-    log(f"[bench] building {args.config}: {cfg.slots} slots x {cfg.ctx[0]} ctx, {NL} cache copies")
+    log(f"[bench] building {name}: {cfg.slots} slots x {cfg.rows_per_slot} rows, ctx {cfg.ctx}, {NL} cache copies")
     layers, st = make_decode_inputs(cfg, dev, seed=0, cache_copies=NL)
-    cos = torch.zeros(1, 32, device=dev)
     rd = 64
-    import numpy as np
     max_pos = max(cfg.ctx) + 8
     ang = torch.outer(torch.arange(max_pos, dtype=torch.float32),
                       1.0 / (10000.0 ** (torch.arange(0, rd, 2, dtype=torch.float32) / rd)))
@@ -88,9 +96,8 @@ def run_decode(args, dev):
     pos, seq, pmax = st["pos"], st["seq"], st["pmax"]
     cl = torch.div(pos + 1, cfg.ratio, rounding_mode="floor")  # once per token, shared by every layer
 
-    fused = not args.separate_appends and cfg.rows_per_slot == 1  # (the one-launch appends need one row per slot)
+    fused = not args.separate_appends and cfg.rows_per_slot == 1  # (the fused appends need one row per slot)
     R = cfg.slots * cfg.rows_per_slot
-    one = fused and args.one_launch and L[0].fused_fits(R, st["q"].shape[2])  # the whole step in one launch
 
     def appends_select(lay):
         if fused:
@@ -101,9 +108,6 @@ def run_decode(args, dev):
         return lay.select(st["q_idx"], st["w_idx"], pos, seq, cl)
 
     def layer_step(lay):
-        if one:
-            return lay.step_fused(st["q"], st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos,
-                                  seq, st["q_idx"], st["w_idx"], pmax, plim=pos, cl=cl)
         idx = appends_select(lay)
         return lay.attend(st["q"], idx, pos, seq, pmax, plim=pos)
 
@@ -112,49 +116,36 @@ def run_decode(args, dev):
         for lay in L:
             layer_step(lay)
     torch.cuda.synchronize(dev)
-
-    # ---- per-phase durations (eager, events around each launch on the launch stream): indexer (the step's cache
-    # appends + scores + top-k: one launch; with --separate-appends the appends launch is timed apart), sattn
-    # (attention, splits merged in-kernel)
     E = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    phases = ({"step": []} if one else {"indexer": [], "sattn": []} if fused else
-              {"appends": [], "indexer": [], "sattn": []})
-    reps = max(2, min(args.steps, 20))
-    sel_union = None
-    for rep in range(reps):
-        for lay in L:
-            ev = [E() for _ in range(len(phases) + 1)]
-            ev[0].record(stream)
-            if one:
-                idx = torch.empty(R, cfg.topk, dtype=torch.int32, device=dev)
-                lay.step_fused(st["q"], st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos,
-                               seq, st["q_idx"], st["w_idx"], pmax, plim=pos, cl=cl, idx_out=idx)
+
+    # ---- the selection's union per slot (gathered rows of the attention, for the algorithmic bytes)
+    ids = appends_select(L[0]).view(cfg.slots, cfg.rows_per_slot, -1).cpu()
+    sel_union = [int(torch.unique(ids[s][ids[s] >= 0]).numel()) for s in range(cfg.slots)]
+
+    # ---- per-phase durations (eager, events around each launch on the launch stream)
+    kern_us = {}
+    if full:
+        phases = {"indexer": [], "sattn": []} if fused else {"appends": [], "indexer": [], "sattn": []}
+        for rep in range(max(2, min(args.steps, 20))):
+            for lay in L:
+                ev = [E() for _ in range(len(phases) + 1)]
+                ev[0].record(stream)
+                if fused:
+                    idx = appends_select(lay)
+                else:
+                    lay.appends(st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos, seq,
+                                st["q_idx"], st["w_idx"])
+                    ev[1].record(stream)
+                    idx = lay.select(st["q_idx"], st["w_idx"], pos, seq, cl)
+                ev[-2].record(stream)
+                lay.attend(st["q"], idx, pos, seq, pmax, plim=pos)
                 ev[-1].record(stream)
                 torch.cuda.synchronize(dev)
-                phases["step"].append(ev[0].elapsed_time(ev[1]) * 1000.0)
-                if sel_union is None:
-                    ids = idx.view(cfg.slots, cfg.rows_per_slot, -1).cpu()
-                    sel_union = [int(torch.unique(ids[s][ids[s] >= 0]).numel()) for s in range(cfg.slots)]
-                continue
-            if fused:
-                idx = appends_select(lay)
-            else:
-                lay.appends(st["kv_raw"], st["kv_norm"], st["latent"], st["k_raw"], st["k_norm"], pos, seq,
-                            st["q_idx"], st["w_idx"])
-                ev[1].record(stream)
-                idx = lay.select(st["q_idx"], st["w_idx"], pos, seq, cl)
-            ev[-2].record(stream)
-            lay.attend(st["q"], idx, pos, seq, pmax, plim=pos)
-            ev[-1].record(stream)
-            torch.cuda.synchronize(dev)
-            for i, k in enumerate(phases):
-                phases[k].append(ev[i].elapsed_time(ev[i + 1]) * 1000.0)
-            if sel_union is None:
-                ids = idx.view(cfg.slots, cfg.rows_per_slot, -1).cpu()
-                sel_union = [int(torch.unique(ids[s][ids[s] >= 0]).numel()) for s in range(cfg.slots)]
-    kern_us = {k: float(np.median(v)) for k, v in phases.items()}
+                for i, k in enumerate(phases):
+                    phases[k].append(ev[i].elapsed_time(ev[i + 1]) * 1000.0)
+        kern_us = {k: float(np.median(v)) for k, v in phases.items()}
 
-    # ---- graph of NL layer-steps, replayed; timed region bracketed by synchronize
+    # ---- graph of NL layer-steps, replayed; the timed region is bracketed by synchronize
     g = torch.cuda.CUDAGraph()
     s2 = torch.cuda.Stream(dev)
     s2.wait_stream(stream)
@@ -170,34 +161,38 @@ def run_decode(args, dev):
     for _ in range(2):
         g.replay()
     torch.cuda.synchronize(dev)
-    replays = max(1, math.ceil(args.steps / NL))
-    e0, e1 = E(), E()
+    replays = max(20, math.ceil(args.steps / NL))
+    ev = [E() for _ in range(replays + 1)]
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(replays):
+    ev[0].record(stream)
+    for i in range(replays):
         g.replay()
-    e1.record(stream)
+        ev[i + 1].record(stream)
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
-    step_us = e0.elapsed_time(e1) * 1000.0 / (replays * NL)
-    log(f"[bench] graph: {replays} replays x {NL} layer-steps: {step_us:.2f} us/layer-step (wall {wall*1e3:.1f} ms)")
+    per = np.array([ev[i].elapsed_time(ev[i + 1]) * 1000.0 / NL for i in range(replays)])
+    step_us = float(np.median(per))
+    total_us = ev[0].elapsed_time(ev[-1]) * 1000.0 / (replays * NL)
+    log(f"[bench] {name} graph: {replays} replays x {NL} layer-steps: median {step_us:.2f} us/layer-step "
+        f"(min {per.min():.2f}, max {per.max():.2f}; whole region {total_us:.2f}; wall {wall*1e3:.1f} ms)")
+    timing = {"replays": replays, "layer_steps_per_replay": NL, "median_us": round(step_us, 3),
+              "min_us": round(float(per.min()), 3), "max_us": round(float(per.max()), 3),
+              "region_mean_us": round(total_us, 3)}
+    res = dict(cfg=cfg, step_us=step_us, timing=timing, kern_us=kern_us, steps=replays * NL, sel_union=sel_union,
+               fused=fused, one_launch=L[0].selector(R, dev).one_launch)
+    if not full:
+        return res
 
     # ---- each heavy kernel alone: a graph of NL launches of it (one per cache copy), replayed; the average launch
     # duration (events on the launch stream around the replays) is the roofline denominator
-    if one:  # the step is one kernel: its graph above is the kernel alone
-        alone_us = {"step": step_us}
-        log(f"[bench] eager per-kernel medians (us): {kern_us}")
-        kb = {"step": step_algorithmic_bytes(cfg)}
-        return dict(cfg=cfg, step_us=step_us, kern_us=kern_us, kern_bytes=kb, steps=replays * NL,
-                    sel_union=sel_union, alone_us=alone_us, fused=fused, one_launch=True, one=True)
     idxs = [appends_select(lay).clone() for lay in L]
     torch.cuda.synchronize(dev)
     only = {"indexer": lambda lay, i: appends_select(lay) if fused else lay.select(st["q_idx"], st["w_idx"], pos,
                                                                                  seq, cl),
             "sattn": lambda lay, i: lay.attend(st["q"], idxs[i], pos, seq, pmax, plim=pos)}
     alone_us = {}
-    for name, fn in only.items():
+    for kname, fn in only.items():
         gk = torch.cuda.CUDAGraph()
         with torch.cuda.stream(s2):
             for i, lay in enumerate(L):
@@ -214,12 +209,11 @@ def run_decode(args, dev):
             gk.replay()
         e3.record(stream)
         torch.cuda.synchronize(dev)
-        alone_us[name] = e2.elapsed_time(e3) * 1000.0 / (replays * NL)
-        log(f"[bench] {name} kernel alone: {alone_us[name]:.2f} us/launch")
+        alone_us[kname] = e2.elapsed_time(e3) * 1000.0 / (replays * NL)
+        log(f"[bench] {kname} kernel alone: {alone_us[kname]:.2f} us/launch")
     log(f"[bench] eager per-kernel medians (us): {kern_us}")
-    kb = decode_bytes(cfg, sel_union, fused)
-    return dict(cfg=cfg, step_us=step_us, kern_us=kern_us, kern_bytes=kb, steps=replays * NL, sel_union=sel_union,
-                alone_us=alone_us, fused=fused, one_launch=L[0].selector(pos.shape[0], dev).one_launch, one=False)
+    res.update(alone_us=alone_us, kern_bytes=decode_bytes(cfg, sel_union, fused))
+    return res
 
 
 def run_prefill(args, dev):
@@ -423,104 +417,94 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def _blas_threads() -> int:
+def _cpu_threads() -> int:
+    """Threads for the CPU baseline: the job's CPU share (OMP_NUM_THREADS when set, as on the GPU box), else every
+    host CPU."""
     try:
-        from threadpoolctl import threadpool_info
-        return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        return 1
+        return max(1, int(os.environ.get("OMP_NUM_THREADS", "")))
+    except ValueError:
+        return os.cpu_count() or 1
 
 
 def cpu_baseline(cfg, budget_s: float):
-    """The oracle (numpy port of the reference's decode path) on the host, one whole layer-step of the workload per
-    repetition: every row's cache appends (ring row, compressed row, index-key row), index score + top-k and sattn2
-    over ring + selected rows, for every slot; repeated until the budget is spent (at least one repetition); the
-    median repetition is the value."""
+    """The reference's PyTorch path on the host in its own precision (oracle/dsv41_torch_cpu.py: the decode indexer's
+    bf16 einsum with an fp32 head sum, top-k, and kernels.sparse_attn over ring + selected rows; DSV41_INDEX_BF16=1),
+    one whole layer-step of the workload per repetition (every query row of every slot), repeated until the budget
+    is spent; the median repetition is the value.  The step's cache appends (a few rows) are left out."""
     import numpy as np
+    import torch
     sys.path.insert(0, ROOT)
-    from oracle import dsv41_oracle as O
-    from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN
-    rng = np.random.default_rng(0)
+    from oracle import dsv41_torch_cpu as TC
+    from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN, fp4_round
+    torch.set_num_threads(_cpu_threads())
+    g = torch.Generator().manual_seed(0)
     S, rps = cfg.slots, cfg.rows_per_slot
-    ns = [cfg.n_c(s) for s in range(S)]
-    rd = 64
-    cos, sin = O.rope_tables(rd, max(cfg.ctx) + 8, 0, 10000.0, 1.0, 32, 1)
-    keys = [O.fake_quant_fp4(rng.standard_normal((1, n + 1, DI)).astype(np.float32) * 0.1, 32) for n in ns]
-    enc = [O.key_encode_fp8(k) for k in keys]
-    ckv = [O.bf16(rng.standard_normal((1, n + 1, DQK)).astype(np.float32) * 0.1) for n in ns]
-    ring = O.bf16(rng.standard_normal((S, WIN, DQK)).astype(np.float32) * 0.1)
-    R = S * rps
-    q = O.bf16(rng.standard_normal((R, 1, H, DQK)).astype(np.float32) * 0.1)
-    qi = O.fake_quant_fp4(rng.standard_normal((R, 1, HI, DI)).astype(np.float32), 32)
-    w = (rng.standard_normal((R, HI)) * 0.01).astype(np.float32)
-    x = O.bf16(rng.standard_normal((R, DQK)).astype(np.float32))
-    lat = O.bf16(rng.standard_normal((R, DQK)).astype(np.float32))
-    kraw = O.bf16(rng.standard_normal((R, DI)).astype(np.float32))
-    nw, kn = np.ones(DQK, np.float32), np.ones(DI, np.float32)
-    sink = rng.standard_normal(H).astype(np.float32)
+    keys = [fp4_round(torch.randn(1, cfg.n_c(s) + 1, DI, generator=g) * 0.1) for s in range(S)]
+    ckv = [(torch.randn(1, WIN + cfg.n_c(s) + 1, DQK, generator=g) * 0.1).to(torch.bfloat16) for s in range(S)]
+    q = (torch.randn(S, rps, H, DQK, generator=g) * 0.1).to(torch.bfloat16)
+    qi = fp4_round(torch.randn(S, rps, HI, DI, generator=g))
+    w = (torch.randn(S, rps, HI, generator=g) * (DI ** -0.5 * HI ** -0.5)).to(torch.bfloat16)
+    sink = torch.randn(H, generator=g)
     times = []
     t_end = time.perf_counter() + budget_s
     while time.perf_counter() < t_end or not times:
         t0 = time.perf_counter()
         for s in range(S):
-            for j in range(rps):
-                r = s * rps + j
-                pos = cfg.ctx[s] - rps + j
-                O.kv_write(x[r:r + 1], nw, cos, sin, [pos], [0], ring[s:s + 1], rd, 1e-6)
-                O.compress_row(lat[r], cos, sin, np.int64(pos + 1 - cfg.ratio), rd)
-                O.index_key_row(kraw[r], kn, cos, sin, np.int64(pos + 1 - cfg.ratio), rd, 1e-6)
-                cl = (pos + 1) // cfg.ratio
-                sc = O.index_score(qi[r:r + 1], enc[s][0], w[r:r + 1], [0], [cl], k_scale=enc[s][1][..., 0])
-                idx = O.topk_indices(sc, cfg.topk, [cl])
-                O.sattn2(q[r:r + 1], ring[s:s + 1], ckv[s], idx[:, None], [pos], [0], [cfg.ctx[s] - 1], [pos], sink,
-                         None, None, 0, DQK ** -0.5, dv=DV)
+            pos = torch.tensor([cfg.ctx[s] - rps + j for j in range(rps)])
+            cl = (pos + 1) // cfg.ratio
+            idx = TC.decode_index_topk(qi[s:s + 1].transpose(0, 1), keys[s].expand(rps, -1, -1),
+                                       w[s:s + 1].transpose(0, 1), cl, cfg.topk)[:, 0]
+            # [ring rows 0..W-1 | compressed rows at W + idx]: the reference's cat of both sources (model.py:1442)
+            full = torch.cat([torch.arange(WIN, dtype=torch.int32).expand(rps, -1),
+                              torch.where(idx >= 0, idx + WIN, -1)], dim=1)
+            TC.sparse_attn(q[s:s + 1], ckv[s], sink, full[None], DQK ** -0.5, dv=DV)
         times.append(time.perf_counter() - t0)
-    return {"value": float(np.median(times)) * 1e6, "unit": "us/layer-step", "cores": _blas_threads(),
+    return {"value": round(float(np.median(times)) * 1e6, 1), "unit": "us/layer-step", "cores": torch.get_num_threads(),
             "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(), "kind": "port",
-            "sample": f"oracle (numpy): one whole layer-step of {cfg.name} per repetition ({R} rows over {S} slots: "
-                      f"appends, index score + top-k {cfg.topk}, sattn2), {len(times)} reps in ~{budget_s:.0f} s, "
-                      f"median; cores = BLAS threads"}
+            "precision": "reference default DSV41_INDEX_BF16=1: bf16 matmuls, fp32 head sum and softmax",
+            "sample": f"torch CPU restatement of the reference's decode indexer + kernels.sparse_attn: one whole "
+                      f"layer-step of {cfg.name} per repetition ({S * rps} query rows over {S} slots; appends "
+                      f"excluded), {len(times)} reps in ~{budget_s:.0f} s, median"}
 
 
-def cpu_baseline_prefill(budget_s: float, rows: int = 32):
-    """The oracle on the host for C3: `rows` evenly spaced query rows of the 2048-token chunk, each through the
-    indexer (score over its causal compressed keys, top-2048) and the sparse attention over its 128 window + 2048
-    selected rows (the reference's prefill rounding), timed as one batch and scaled to the chunk: tok/s = 2048 /
-    (batch time x 2048 / rows)."""
+def cpu_baseline_prefill(budget_s: float, rows: int = 64):
+    """The reference's prefill path on the host in its own precision for C3: `rows` query rows of the 2048-token chunk
+    (one query chunk of the reference's indexer loop, evenly spaced over the chunk) through the indexer (per-head
+    bf16 bmm over the causal compressed keys, fp32 head sum, top-2048; dsv41/model.py:780-893) and kernels.sparse_attn
+    over the 128 window + 2048 selected rows, timed and scaled to the chunk: tok/s = 2048 / (time x 2048 / rows)."""
     import numpy as np
+    import torch
     sys.path.insert(0, ROOT)
-    from oracle import dsv41_oracle as O
-    from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN, PREFILL
+    from oracle import dsv41_torch_cpu as TC
+    from dsv41_amd.workloads import DQK, DV, H, HI, DI, WIN, PREFILL, fp4_round
+    torch.set_num_threads(_cpu_threads())
     cfg = PREFILL["C3"]
-    rng = np.random.default_rng(1)
+    g = torch.Generator().manual_seed(1)
     T = cfg.n_c
-    keys = O.fake_quant_fp4(rng.standard_normal((1, T, DI)).astype(np.float32) * 0.1, 32)
-    k8, s8 = O.key_encode_fp8(keys)
-    kv = O.bf16(rng.standard_normal((1, WIN - 1 + cfg.chunk + T, DQK)).astype(np.float32) * 0.1)
-    sel_rows = np.linspace(0, cfg.chunk - 1, rows).astype(int)
-    qi = O.fake_quant_fp4(rng.standard_normal((1, rows, HI, DI)).astype(np.float32), 32)
-    w = (rng.standard_normal((1, rows, HI)) * 0.01).astype(np.float32)
-    q = O.bf16(rng.standard_normal((1, rows, H, DQK)).astype(np.float32) * 0.1)
-    sink = rng.standard_normal(H).astype(np.float32)
+    keys = fp4_round(torch.randn(1, T, DI, generator=g) * 0.1)
     off = WIN - 1 + cfg.chunk
+    kv = (torch.randn(1, off + T, DQK, generator=g) * 0.1).to(torch.bfloat16)
+    sel = torch.linspace(0, cfg.chunk - 1, rows).long()
+    qi = fp4_round(torch.randn(1, cfg.chunk, HI, DI, generator=g))
+    w = (torch.randn(1, cfg.chunk, HI, generator=g) * (DI ** -0.5 * HI ** -0.5)).to(torch.bfloat16)
+    q = (torch.randn(1, rows, H, DQK, generator=g) * 0.1).to(torch.bfloat16)
+    sink = torch.randn(H, generator=g)
+    widx = (sel[:, None] + torch.arange(WIN)[None, :]).to(torch.int32)  # the 127 history rows + the row itself
     times = []
     t_end = time.perf_counter() + budget_s
     while time.perf_counter() < t_end or not times:
         t0 = time.perf_counter()
-        for n, i in enumerate(sel_rows):
-            cl = (cfg.prior + i + 1) // cfg.ratio
-            sc = O.index_score(qi[:, n], k8, w[:, n], [0], [cl], k_scale=s8[..., 0])
-            cidx = O.topk_indices(sc, cfg.topk, [cl])[0]
-            widx = np.arange(i, i + WIN, dtype=np.int32)  # the 127 history rows + the row itself
-            idx = np.concatenate([widx, np.where(cidx >= 0, cidx + off, -1)])[None, None]
-            O.sparse_attn(q[:, n:n + 1], kv, sink, idx, DQK ** -0.5, dv=DV)
+        cidx = TC.prefill_index_topk(qi, w, keys, cfg.prior, cfg.ratio, cfg.topk, off, rows=sel)[0]
+        TC.sparse_attn(q, kv, sink, torch.cat([widx, cidx], dim=1)[None], DQK ** -0.5, dv=DV)
         times.append(time.perf_counter() - t0)
     t = float(np.median(times)) * cfg.chunk / rows
-    return {"value": round(cfg.chunk / t, 2), "unit": "tok/s", "cores": _blas_threads(), "host_cpus": os.cpu_count(),
-            "cpu_model": _cpu_model(), "kind": "port",
-            "sample": f"oracle (numpy): {rows} of the chunk's {cfg.chunk} query rows (indexer over {T} keys + top-"
-                      f"{cfg.topk}, sparse attention over {WIN} + {cfg.topk} rows), {len(times)} reps in "
-                      f"~{budget_s:.0f} s, median, scaled to the chunk"}
+    return {"value": round(cfg.chunk / t, 2), "unit": "tok/s", "cores": torch.get_num_threads(),
+            "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(), "kind": "port",
+            "precision": "reference default DSV41_INDEX_BF16=1: bf16 matmuls, fp32 head sum and softmax",
+            "sample": f"torch CPU restatement of the reference's prefill indexer + kernels.sparse_attn: {rows} of the "
+                      f"chunk's {cfg.chunk} query rows timed (indexer over their causal keys of {T}, top-{cfg.topk}, "
+                      f"attention over {WIN} + {cfg.topk} rows), {len(times)} reps in ~{budget_s:.0f} s, median, "
+                      f"scaled to the chunk"}
 
 
 def main():
@@ -529,14 +513,14 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="C2")
+    ap.add_argument("--extra-configs", default="C4,C5",
+                    help="decode configs also measured (graph replays only) and reported beside the headline")
     ap.add_argument("--layers", type=int, default=8, help="independent cache copies rotated per step")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-proj", action="store_true", help="skip the FP8 projection GEMVs")
     ap.add_argument("--proj-only", action="store_true", help="only the FP8 projection GEMVs (for profiling)")
-    ap.add_argument("--one-launch", action="store_true",
-                    help="decode: the whole layer-step as one launch (dsv41_decode_step) instead of indexer + attention")
     ap.add_argument("--separate-appends", action="store_true",
                     help="decode: the cache appends as their own launch before the indexer (default: one launch)")
     ap.add_argument("--prefill-reps", type=int, default=5)
@@ -564,7 +548,7 @@ def main():
     if args.proj_only:
         print(json.dumps({"projections": run_projections(args, dev)}), flush=True)
         return
-    r = run_decode(args, dev)
+    r = run_decode(args, dev, args.config)
     cfg = r["cfg"]
     kb, ku = r["kern_bytes"], r["kern_us"]
     R = cfg.slots * cfg.rows_per_slot
@@ -575,8 +559,7 @@ def main():
                 "score kernel with histogram + select kernels (multi-launch)")
     att_name = ("attn_decode_kernel<576, 512> (splits merged in-kernel)" if R < 16 else
                 "attn_prefill_ws_kernel<576, 512> + attn_decode_combine_kernel (key splits)")
-    kernel_names = {"indexer": sel_name, "sattn": att_name,
-                    "step": "decode_step_kernel<576, 512> (appends + scores + top-k + attention, one launch)"}
+    kernel_names = {"indexer": sel_name, "sattn": att_name}
     roof = {}
     for name, us in r["alone_us"].items():
         achieved = kb[name] / (us * 1e-6) / 1e9
@@ -591,6 +574,19 @@ def main():
     dom = max(r["alone_us"], key=r["alone_us"].get)  # the kernel with the longest launch
     alg = step_algorithmic_bytes(cfg)
     frac_step = alg / (r["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS
+    extra = {}
+    for name in [c for c in args.extra_configs.split(",") if c and c != args.config]:
+        torch.cuda.empty_cache()
+        e = run_decode(args, dev, name, full=False)
+        ab = step_algorithmic_bytes(e["cfg"], e["sel_union"])
+        extra[name] = {"us_per_layer_step": round(e["step_us"], 3), "timing": e["timing"],
+                       "algorithmic_bytes_per_step": ab,
+                       "hbm_roofline_pct": round(100.0 * ab / (e["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
+                       "gathered_rows_per_slot": e["sel_union"],
+                       "workload": f"{name}: {e['cfg'].slots} slots x {e['cfg'].rows_per_slot} query rows, ctx "
+                                   f"{e['cfg'].ctx}, top-k {e['cfg'].topk}"}
+        del e
+    torch.cuda.empty_cache()
     pre = None if args.no_prefill else run_prefill(args, dev)
     proj = None if args.no_proj else run_projections(args, dev)
     cpu = None if args.no_cpu else cpu_baseline(cfg, args.cpu_budget)
@@ -601,7 +597,8 @@ def main():
         "value": round(r["step_us"], 3),
         "unit": "us/layer-step",
         "n_gpus": 1,
-        "steps": r["steps"],
+        "steps": r["steps"],  # layer-steps in the timed region: the graph replays x their layer-steps
+        "steps_requested": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(r["step_us"] / 1000.0, 6),
         "higher_is_better": False,
@@ -613,10 +610,12 @@ def main():
                                f"{cfg.ratio}, top-k {cfg.topk}, SWA {128}, 64 heads x 576 (V 512)",
                    "cache_copies": args.layers},
         "hbm_roofline_pct": round(100.0 * frac_step, 2),
+        "timing": r["timing"],
         "algorithmic_bytes_per_step": alg,
         "eager_launch_us": {k: round(v, 3) for k, v in ku.items()},  # eager, one launch each, host gaps included
         "roofline": roof[dom],
         "roofline_other": {k: v for k, v in roof.items() if k != dom},
+        "decode_other_configs": extra,
         "prefill": pre,
         "projections": proj,
         "cpu_baseline": cpu,

@@ -151,6 +151,7 @@ struct DecAppArgs {
   int kcap, Dk;
   const long* pos;
   const long* seq;
+  const long* nw_tab;  // [S] no-write row per sequence, or null (the tables' spare last row)
   int ratio, rd;
   const float* cos_t;
   const float* sin_t;
@@ -189,7 +190,7 @@ __global__ void __launch_bounds__(kRowThreads) decode_appends_kernel(const DecAp
     o.out = a.ring + s * a.ring_sstride + (o.pos % a.W) * (long)a.Dw;
   } else if (op == 1) {
     if (!a.latent || !a.ckv) return;
-    const long row = closes ? (p + 1) / a.ratio - 1 : a.cap - 1;
+    const long row = closes ? (p + 1) / a.ratio - 1 : a.nw_tab ? a.nw_tab[s] : a.cap - 1;
     o.x = a.latent + (long)r * a.Dw;
     o.D = a.Dw;
     o.pos = p + 1 - a.ratio;
@@ -198,7 +199,7 @@ __global__ void __launch_bounds__(kRowThreads) decode_appends_kernel(const DecAp
     o.out = a.ckv + s * a.ckv_sstride + row * (long)a.Dw;
   } else {
     if (!a.k_raw || (!a.kbf && !a.k8)) return;
-    const long row = closes ? (p + 1) / a.ratio - 1 : a.kcap - 1;
+    const long row = closes ? (p + 1) / a.ratio - 1 : a.nw_tab ? a.nw_tab[s] : a.kcap - 1;
     o.x = a.k_raw + (long)r * a.Dk;
     o.D = a.Dk;
     o.norm_w = a.k_norm;
@@ -413,9 +414,9 @@ int dsv41_append_rows(const void* x, long x_rstride, const void* norm_w, float e
 int dsv41_decode_appends(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
                          const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
                          const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
-                         long ks_sstride, int kcap, int Dk, const long* pos, const long* seq, int ratio,
-                         const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
-                         const void* w_idx, int HI, void* q8, float* wf, int B, void* stream) {
+                         long ks_sstride, int kcap, int Dk, const long* pos, const long* seq,
+                         const long* nw_tab, int ratio, const float* cos_t, const float* sin_t, int rd, float eps,
+                         const void* q_idx, const void* w_idx, int HI, void* q8, float* wf, int B, void* stream) {
   if (B <= 0) return 0;
   if (!row_ok(Dw, 32) || !row_ok(Dk, 32) || ratio <= 0 || rd % 2 != 0 || rd > Dw || rd > Dk || W <= 0 ||
       cap <= 0 || kcap <= 0 || (q_idx && (!w_idx || !q8 || !wf || HI <= 0 || HI > 64)))
@@ -423,8 +424,8 @@ int dsv41_decode_appends(const void* kv_raw, const void* kv_norm, void* ring, lo
   DecAppArgs a{(const uint16_t*)kv_raw, (const uint16_t*)kv_norm, (uint16_t*)ring, ring_sstride, W, Dw,
                (const uint16_t*)latent, (uint16_t*)ckv, ckv_sstride, cap, (const uint16_t*)k_raw,
                (const uint16_t*)k_norm, (uint16_t*)kbf, kbf_sstride, (uint8_t*)k8, k8_sstride, ks, ks_sstride, kcap,
-               Dk, pos, seq, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx, HI,
-               (uint8_t*)q8, wf};
+               Dk, pos, seq, nw_tab, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx,
+               HI, (uint8_t*)q8, wf};
   decode_appends_kernel<<<dim3(B, q_idx ? 4 : 3), kRowThreads, 0, (hipStream_t)stream>>>(a);
   DSV41_CHECK_LAUNCH();
   return 0;

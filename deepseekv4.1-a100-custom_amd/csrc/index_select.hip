@@ -71,6 +71,7 @@ struct IsAppend {
   long ks_sstride;
   int kcap;
   const long* pos;
+  const long* nw_tab;      // [S] no-write row per sequence (null: the tables' spare last row cap - 1 / kcap - 1)
   int ratio, rd;
   const float* cos_t;
   const float* sin_t;
@@ -81,7 +82,9 @@ struct IsAppend {
 
 // Row operation `which` of row r's appends (0: the SWA ring row, 1: the compressed row, 2: the index key, with an
 // LDS copy of its e4m3 bytes and scale in knew / ksnew when given); position ppos, sequence slot.  Compressed /
-// index-key rows go to compress_len - 1 when the step closes a group, else to the table's spare last row.
+// index-key rows go to compress_len - 1 when the step closes a group, else to the sequence's no-write row
+// (nw_tab[slot]: the last row of the slot's own capacity, dsv41/decode.py:176-181) or, without a table, to the
+// table's spare last row.
 DSV41_DEV RowOp is_app_op(const IsAppend& ap, int r, long slot, long ppos, int which, uint8_t* knew, float* ksnew) {
   RowOp o{};
   o.cos_t = ap.cos_t;
@@ -98,7 +101,7 @@ DSV41_DEV RowOp is_app_op(const IsAppend& ap, int r, long slot, long ppos, int w
     o.group = 32;
     o.out = ap.ring + slot * ap.ring_sstride + (o.pos % ap.W) * (long)ap.Dw;
   } else if (which == 1) {
-    const long row = closes ? (ppos + 1) / ap.ratio - 1 : ap.cap - 1;
+    const long row = closes ? (ppos + 1) / ap.ratio - 1 : ap.nw_tab ? ap.nw_tab[slot] : ap.cap - 1;
     o.x = ap.latent + (long)r * ap.Dw;
     o.D = ap.Dw;
     o.pos = ppos + 1 - ap.ratio;
@@ -106,7 +109,7 @@ DSV41_DEV RowOp is_app_op(const IsAppend& ap, int r, long slot, long ppos, int w
     o.group = 16;
     o.out = ap.ckv + slot * ap.ckv_sstride + row * (long)ap.Dw;
   } else {
-    const long row = closes ? (ppos + 1) / ap.ratio - 1 : ap.kcap - 1;
+    const long row = closes ? (ppos + 1) / ap.ratio - 1 : ap.nw_tab ? ap.nw_tab[slot] : ap.kcap - 1;
     o.x = ap.k_raw + (long)r * 128;
     o.D = 128;
     o.norm_w = ap.k_norm;
@@ -883,8 +886,8 @@ int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_r
 int dsv41_decode_select(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
                         const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
                         const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
-                        long ks_sstride, int kcap, const long* pos, const long* seq, int R, int ratio,
-                        const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
+                        long ks_sstride, int kcap, const long* pos, const long* seq, const long* nw_tab, int R,
+                        int ratio, const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
                         const void* w_idx, int HI, const long* cl, int n_pos, int k, int offset, void* ws,
                         long ws_bytes, float* score_out, long score_rstride, int* out, long out_rstride,
                         const void* cand, long cand_rstride, void* stream) {
@@ -900,7 +903,7 @@ int dsv41_decode_select(const void* kv_raw, const void* kv_norm, void* ring, lon
   g.app = IsAppend{(const uint16_t*)kv_raw, (const uint16_t*)kv_norm, (uint16_t*)ring, ring_sstride, W, Dw,
                    (const uint16_t*)latent, (uint16_t*)ckv, ckv_sstride, cap, (const uint16_t*)k_raw,
                    (const uint16_t*)k_norm, (uint16_t*)kbf, kbf_sstride, (uint8_t*)k8, k8_sstride, ks, ks_sstride,
-                   kcap, pos, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx};
+                   kcap, pos, nw_tab, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx};
   return select_launch<true>(g, (hipStream_t)stream);
 }
 
@@ -908,8 +911,8 @@ int dsv41_decode_select(const void* kv_raw, const void* kv_norm, void* ring, lon
 int dsv41_decode_score(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
                        const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
                        const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
-                       long ks_sstride, int kcap, const long* pos, const long* seq, int R, int ratio,
-                       const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
+                       long ks_sstride, int kcap, const long* pos, const long* seq, const long* nw_tab, int R,
+                       int ratio, const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
                        const void* w_idx, int HI, const long* cl, int n_pos, float* score, long score_rstride,
                        int* hist, const void* cand, long cand_rstride, void* stream) {
   if (R <= 0 || n_pos <= 0) return 0;
@@ -939,7 +942,7 @@ int dsv41_decode_score(const void* kv_raw, const void* kv_norm, void* ring, long
   d.app = IsAppend{(const uint16_t*)kv_raw, (const uint16_t*)kv_norm, (uint16_t*)ring, ring_sstride, W, Dw,
                    (const uint16_t*)latent, (uint16_t*)ckv, ckv_sstride, cap, (const uint16_t*)k_raw,
                    (const uint16_t*)k_norm, (uint16_t*)kbf, kbf_sstride, (uint8_t*)k8, k8_sstride, ks, ks_sstride,
-                   kcap, pos, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx};
+                   kcap, pos, nw_tab, ratio, rd, cos_t, sin_t, eps, (const uint16_t*)q_idx, (const uint16_t*)w_idx};
   // chunks per row: the row's chunks rounded up to a multiple of 8, or, when that overfills the CUs the append
   // workgroups leave, as many as fit (a multiple of 8 again) provided one extra tile per wave covers the rest
   const int app_wgs = (3 * R + kXcds - 1) / kXcds * kXcds;

@@ -39,21 +39,16 @@ SIGNATURES = {
     "dsv41_append_rows": [_P, _L, _P, _F, _P, _P, _I, _P, _L, _L, _L, _P, _I, _P, _L, _P, _L, _I, _I, _P, _L, _P, _L,
                           _I, _I, _P],
     "dsv41_decode_appends": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _I, _P, _P,
-                             _I, _P, _P, _I, _F, _P, _P, _I, _P, _P, _I, _P],
+                             _P, _I, _P, _P, _I, _F, _P, _P, _I, _P, _P, _I, _P],
     "dsv41_index_qprep": [_P, _P, _I, _I, _P, _P, _P],
     "dsv41_fake_quant": [_P, _P, _L, _I, _I, _I, _P],
     "dsv41_rope": [_P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _P],
     "dsv41_rmsnorm": [_P, _P, _P, _L, _I, _F, _P],
     "dsv41_norm_quant": [_P, _P, _F, _P, _L, _I, _P],
-    "dsv41_decode_select": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _I,
+    "dsv41_decode_select": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _P, _I,
                             _I, _P, _P, _I, _F, _P, _P, _I, _P, _I, _I, _I, _P, _L, _P, _L, _P, _L, _P, _L, _P],
-    "dsv41_decode_score": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _I,
+    "dsv41_decode_score": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _P, _I,
                            _I, _P, _P, _I, _F, _P, _P, _I, _P, _I, _P, _L, _P, _P, _L, _P],
-    "dsv41_decode_step_workspace_bytes": [_I, _I, _I, _I],
-    "dsv41_decode_step_fits": [_I, _I, _I, _I, _I, _I, _I],
-    "dsv41_decode_step": [_P, _P, _P, _L, _I, _I, _P, _P, _L, _I, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _I, _I,
-                          _P, _P, _I, _F, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P, _P, _P, _I, _F, _P, _P, _L, _P, _L,
-                          _P, _L, _P],
     "dsv41_index_keys_encode": [_P, _L, _P, _P, _P],
     "dsv41_index_keys_decode": [_P, _P, _L, _P, _P],
     "dsv41_fp8_gemm_workspace_bytes": [_I, _I, _I],
@@ -64,7 +59,7 @@ SIGNATURES = {
 }
 _RESTYPE = {"dsv41_attn_workspace_bytes": _L, "dsv41_select_workspace_bytes": _L,
             "dsv41_index_select_workspace_bytes": _L, "dsv41_candidate_blocks_workspace_bytes": _L,
-            "dsv41_fp8_gemm_workspace_bytes": _L, "dsv41_decode_step_workspace_bytes": _L}
+            "dsv41_fp8_gemm_workspace_bytes": _L}
 
 _lib = None
 
@@ -97,9 +92,7 @@ CHECK_ERRORS = os.environ.get("DSV41_CHECK_ERRORS", "0") == "1"
 
 _ERR_TEXT = {("index_select", 1): "a row barrier wait gave up (the row's workgroups were not resident together)",
              ("index_select", 2): "a valid count cl exceeded the positions scored (clamped)",
-             ("attention", 1): "a split merge stopped waiting for its unit (workgroups not resident together)",
-             ("decode_step", 1): "a row-wide wait gave up (the workgroups were not resident together)",
-             ("decode_step", 2): "a valid count cl exceeded the positions scored (clamped)"}
+             ("attention", 1): "a split merge stopped waiting for its unit (workgroups not resident together)"}
 
 
 def check_error_word(kind: str, word: torch.Tensor) -> None:
@@ -148,3 +141,4 @@ def as_i64(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
     if t.device != dev or t.dtype != torch.int64 or not t.is_contiguous():
         t = t.to(device=dev, dtype=torch.int64, non_blocking=True).contiguous()
     return t
+

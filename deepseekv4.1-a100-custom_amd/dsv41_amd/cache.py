@@ -155,11 +155,18 @@ def append_index_k_decode(cache: torch.Tensor, k_raw: torch.Tensor, norm_w: torc
          stream(dev))
 
 
+def _nw(nw_tab, dev):
+    """The no-write row table as contiguous int64 on the launch device (None stays None)."""
+    return None if nw_tab is None else as_i64(nw_tab.reshape(-1), dev)
+
+
 def decode_appends(kv_raw, kv_norm, ring, latent, ckv, k_raw, k_norm, kbf, k8, k_scale, pos, seq, ratio: int,
-                   cos, sin, rd: int, eps: float, q_idx=None, w_idx=None, q8=None, wf=None) -> None:
+                   cos, sin, rd: int, eps: float, q_idx=None, w_idx=None, q8=None, wf=None, nw_tab=None) -> None:
     """Every cache write of one decode step in one launch (dsv41/decode.py:129-164, :270-282): the SWA ring row
     (kv_write), the compressed-KV row and the index-key row (bf16 table kbf and/or e4m3 table k8 + k_scale), each at
-    compress_len - 1 when the step closes a compression group, else at the table's spare last row.  latent / k_raw
+    compress_len - 1 when the step closes a compression group, else at the sequence's no-write row: nw_tab[seq]
+    (int64 [S], the reference's per-slot table of the last row of each slot's own capacity under DSV41_SLOT_CAPS,
+    dsv41/decode.py:62-68, :176-181) or, without a table, the table's spare last row.  latent / k_raw
     may be None (layers that own no compressor / indexer keys).  With q_idx ([B, 1, HI, 128] bf16) and w_idx
     ([B, HI] bf16) it also writes the prepared e4m3 index queries q8 [B, 64, 128] (uint8) and folded weights
     wf [B, 64] of the e4m3 score path."""
@@ -179,7 +186,7 @@ def decode_appends(kv_raw, kv_norm, ring, latent, ckv, k_raw, k_norm, kbf, k8, k
          ptr(k_norm.to(torch.bfloat16).contiguous()) if k_norm is not None else None, ptr(kbf),
          kbf.stride(0) if kbf is not None else 0, ptr(k8), k8.stride(0) if k8 is not None else 0, ptr(k_scale),
          k_scale.stride(0) if k_scale is not None else 0, kcap, Dk, ptr(as_i64(pos.reshape(-1), dev)),
-         ptr(as_i64(seq.reshape(-1), dev)), int(ratio), ptr(cos), ptr(sin), int(rd), float(eps),
+         ptr(as_i64(seq.reshape(-1), dev)), ptr(_nw(nw_tab, dev)), int(ratio), ptr(cos), ptr(sin), int(rd), float(eps),
          ptr(q_idx.contiguous()) if q_idx is not None else None,
          ptr(w_idx.to(torch.bfloat16).contiguous()) if q_idx is not None else None,
          q_idx.shape[-2] if q_idx is not None else 0, ptr(q8), ptr(wf), B, stream(dev))

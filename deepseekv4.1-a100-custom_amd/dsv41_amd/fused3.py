@@ -148,8 +148,8 @@ class DecodeSelector:
         """The decode step's cache appends and scores + top-k: in one launch (dsv41_decode_select) when the selection
         fits one, else the appends and the scores with their histogram in one launch (dsv41_decode_score) and the
         top-k after it.  app: the arguments of cache.decode_appends as keywords (kv_raw, kv_norm, ring, latent, ckv,
-        k_raw, k_norm, kbf, k8, k_scale, ratio, cos, sin, rd, eps, q_idx [B, 1, HI, 128], w_idx [B, HI]); the rows'
-        sequences must be distinct.  The keys scored are app["k8"] / app["k_scale"]."""
+        k_raw, k_norm, kbf, k8, k_scale, ratio, cos, sin, rd, eps, q_idx [B, 1, HI, 128], w_idx [B, HI], optional
+        nw_tab: int64 [S] no-write row per sequence, dsv41/decode.py:176-181); the rows' sequences must be distinct.  The keys scored are app["k8"] / app["k_scale"]."""
         dev = self.score.device
         ring, ckv, k8, ks, kbf = app["ring"], app.get("ckv"), app["k8"], app["k_scale"], app.get("kbf")
         Dw = ring.shape[-1]
@@ -161,6 +161,8 @@ class DecodeSelector:
         q_idx, w_idx = app["q_idx"], app["w_idx"]
         HI = q_idx.shape[-2]
         assert ring.stride(2) == 1 and ring.stride(1) == Dw and ks.dtype == torch.float32
+        nw = app.get("nw_tab")
+        nw = as_i64(nw.reshape(-1), dev) if nw is not None else None
         if not self.one_launch:
             cp, cs = _cand_args(cand, self.rows, self.n_pos)
             call("dsv41_decode_score", ptr(x), ptr(app["kv_norm"].to(torch.bfloat16).contiguous()), ptr(ring),
@@ -168,8 +170,8 @@ class DecodeSelector:
                  ckv.shape[1] if ckv is not None else 1, ptr(app["k_raw"].reshape(B, -1).contiguous()),
                  ptr(app["k_norm"].to(torch.bfloat16).contiguous()), ptr(kbf),
                  kbf.stride(0) if kbf is not None else 0, ptr(k8), k8.stride(0), ptr(ks), ks.stride(0), k8.shape[1],
-                 ptr(pos), ptr(seq), B, int(app["ratio"]), ptr(app["cos"]), ptr(app["sin"]), int(app["rd"]),
-                 float(app["eps"]), ptr(q_idx.contiguous()), ptr(w_idx.to(torch.bfloat16).contiguous()), HI, ptr(cl),
+                 ptr(pos), ptr(seq), ptr(nw), B, int(app["ratio"]), ptr(app["cos"]), ptr(app["sin"]),
+                 int(app["rd"]), float(app["eps"]), ptr(q_idx.contiguous()), ptr(w_idx.to(torch.bfloat16).contiguous()), HI, ptr(cl),
                  self.n_pos, ptr(self.score), self.score.stride(0), ptr(self.ws), cp, cs, stream(dev))
             return self.select(cl)
         cp, cs = _cand_args(cand, self.rows, self.n_sel)
@@ -177,8 +179,9 @@ class DecodeSelector:
              ring.stride(0), ring.shape[1], Dw, ptr(lat), ptr(ckv), ckv.stride(0) if ckv is not None else 0,
              ckv.shape[1] if ckv is not None else 1, ptr(app["k_raw"].reshape(B, -1).contiguous()),
              ptr(app["k_norm"].to(torch.bfloat16).contiguous()), ptr(kbf), kbf.stride(0) if kbf is not None else 0,
-             ptr(k8), k8.stride(0), ptr(ks), ks.stride(0), k8.shape[1], ptr(pos), ptr(seq), B, int(app["ratio"]),
-             ptr(app["cos"]), ptr(app["sin"]), int(app["rd"]), float(app["eps"]), ptr(q_idx.contiguous()),
+             ptr(k8), k8.stride(0), ptr(ks), ks.stride(0), k8.shape[1], ptr(pos), ptr(seq), ptr(nw), B,
+             int(app["ratio"]), ptr(app["cos"]), ptr(app["sin"]), int(app["rd"]), float(app["eps"]),
+             ptr(q_idx.contiguous()),
              ptr(w_idx.to(torch.bfloat16).contiguous()), HI, ptr(cl), self.n_sel, self.k, 0, ptr(self.fws),
              self.fnbytes, ptr(self.score) if self.keep_scores else None, self.score.stride(0), ptr(self.out), self.k,
              cp, cs, stream(dev))

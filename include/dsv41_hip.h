@@ -161,46 +161,19 @@ int dsv41_index_select(const void* q8, long q_rstride, const float* wf, long w_r
                        long score_rstride, int* out, long out_rstride, const void* cand, long cand_rstride,
                        void* stream);
 
-/* Workspace of dsv41_decode_step for R rows of n_pos positions, h heads, output width dv (256-byte aligned; allocate
- * it zeroed once per (R, n_pos): every launch leaves its count words and merge counters consistent for the next;
- * launches sharing it must be stream-ordered).  Its first int32 is the error word: 1 = a row-wide wait gave up (the
- * workgroups were not resident together), 2 = a cl[r] above n_pos was clamped. */
-long dsv41_decode_step_workspace_bytes(int R, int n_pos, int h, int dv);
-
-/* 1 when dsv41_decode_step takes these shapes on the current device: 64 heads, dqk/dv 576/512 or 512/512, k <= 2048,
- * W a multiple of 64, n_pos <= 32768, R * NC a multiple of 32 and at most the device's compute units
- * (NC = ceil(n_pos / 512) rounded up to a multiple of 4; one workgroup per compute unit). */
-int dsv41_decode_step_fits(int R, int n_pos, int h, int k, int W, int dqk, int dv);
-
-/* One decode layer-step in one launch (DecodeRuntime.attention2 between the projections and the o-projection,
- * dsv41/decode.py:106-174, with the indexer of :267-319): the cache appends of dsv41_decode_select (ring row,
- * compressed row, index key), the indexer scores over the e4m3 keys and the exact top-k (the set of
- * dsv41_topk_indices: ties lowest index first), then fused2.sattn2 (dsv41/fused2.py:334-446) of query q [R, h, Dw]
- * over the SWA ring and the selected compressed rows (Dw = 576: absorbed MLA, V = the first 512 columns; Dw = 512:
- * K = V), sink in the denominator, inverse rope on the last out_rd output columns; out [R, h, dv] bf16.  Rows must
- * belong to distinct sequences (seq distinct).  idx_out [R, k] (may be null) receives the selection (+ offset, -1
- * padding); score_out (may be null) the scores.  Same results as dsv41_decode_select followed by dsv41_sattn2. */
-int dsv41_decode_step(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
-                      const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw, const void* k_norm,
-                      void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks, long ks_sstride, int kcap,
-                      const long* pos, const long* seq, int R, int ratio, const float* cos_t, const float* sin_t,
-                      int rd, float eps, const void* q_idx, const void* w_idx, int HI, const long* cl, int n_pos,
-                      int k, int offset, const void* q, int h, const long* pmax, const long* plim, const float* sink,
-                      int out_rd, float scale, void* out, int* idx_out, long idx_rstride, float* score_out,
-                      long score_rstride, void* ws, long ws_bytes, void* stream);
-
 /* The decode step's cache appends and the one-launch indexer in one launch: the operations of dsv41_decode_appends
  * (the SWA ring row, the compressed row and the index-key row of every row, dsv41/decode.py:129-164, :270-282; the
  * e4m3 preparation of the index queries q_idx [R, HI, 128] / w_idx [R, HI] bf16) followed by dsv41_index_select over
  * the e4m3 key table k8 / ks, the new key of a row whose step closes a group included (it is scored from the
  * values this launch computes).  Same results as dsv41_decode_appends followed by dsv41_index_select.  Every row
  * must belong to a different sequence (seq distinct: a row's new key is not visible to other rows of the launch);
- * the index-key width is 128; limits and workspace as dsv41_index_select. */
+ * the index-key width is 128; nw_tab (may be null) as in dsv41_decode_appends; limits and workspace as
+ * dsv41_index_select. */
 int dsv41_decode_select(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
                         const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
                         const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
-                        long ks_sstride, int kcap, const long* pos, const long* seq, int R, int ratio,
-                        const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
+                        long ks_sstride, int kcap, const long* pos, const long* seq, const long* nw_tab, int R,
+                        int ratio, const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
                         const void* w_idx, int HI, const long* cl, int n_pos, int k, int offset, void* ws,
                         long ws_bytes, float* score_out, long score_rstride, int* out, long out_rstride,
                         const void* cand, long cand_rstride, void* stream);
@@ -212,12 +185,13 @@ int dsv41_decode_select(const void* kv_raw, const void* kv_norm, void* ring, lon
  * (zero on entry; dsv41_select_topk leaves it zero), scores into score [R, n_pos] for positions < cl[r]; the new key
  * of a row whose step closes a group is scored from the values this launch computes.  Same results as
  * dsv41_decode_appends followed by dsv41_index_score (e4m3 keys, with the histogram).  Rows must belong to distinct
- * sequences (a row's new key is not visible to other rows of the launch); index-key width 128, HI <= 64. */
+ * sequences (a row's new key is not visible to other rows of the launch); index-key width 128, HI <= 64; nw_tab
+ * (may be null) as in dsv41_decode_appends. */
 int dsv41_decode_score(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
                        const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
                        const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
-                       long ks_sstride, int kcap, const long* pos, const long* seq, int R, int ratio,
-                       const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
+                       long ks_sstride, int kcap, const long* pos, const long* seq, const long* nw_tab, int R,
+                       int ratio, const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
                        const void* w_idx, int HI, const long* cl, int n_pos, float* score, long score_rstride,
                        int* hist, const void* cand, long cand_rstride, void* stream);
 
@@ -280,13 +254,17 @@ int dsv41_append_rows(const void* x, long x_rstride, const void* norm_w, float e
  *   kbf[seq, row], k8/ks      <- fq4/32(rope(rmsnorm(k_raw[r], k_norm), pos + 1 - ratio))     (Dk = 128; k_raw may be
  *                                                                                               null; kbf or k8 may be null)
  *   q8[r], wf[r]              <- dsv41_index_qprep(q_idx[r], w_idx[r] (bf16))                  (q_idx may be null)
- * with row = (pos + 1) / ratio - 1 when (pos + 1) % ratio == 0, else the table's spare last row (cap - 1 / kcap - 1). */
+ * with row = (pos + 1) / ratio - 1 when (pos + 1) % ratio == 0, else the no-write row of the sequence: nw_tab[seq]
+ * when nw_tab (int64 [S]) is given -- the reference's per-slot table under DSV41_SLOT_CAPS, the last row of each
+ * slot's own capacity (dsv41/decode.py:62-68, :176-181), needed when the tables are as_strided views whose slot
+ * stride is smaller than their row count (dsv41/slots.py:1-11) -- else the table's spare last row (cap - 1 /
+ * kcap - 1).  Both tables take the same row (the reference passes one row to both appends, :157-164, :270-282). */
 int dsv41_decode_appends(const void* kv_raw, const void* kv_norm, void* ring, long ring_sstride, int W, int Dw,
                          const void* latent, void* ckv, long ckv_sstride, int cap, const void* k_raw,
                          const void* k_norm, void* kbf, long kbf_sstride, void* k8, long k8_sstride, float* ks,
-                         long ks_sstride, int kcap, int Dk, const long* pos, const long* seq, int ratio,
-                         const float* cos_t, const float* sin_t, int rd, float eps, const void* q_idx,
-                         const void* w_idx, int HI, void* q8, float* wf, int B, void* stream);
+                         long ks_sstride, int kcap, int Dk, const long* pos, const long* seq,
+                         const long* nw_tab, int ratio, const float* cos_t, const float* sin_t, int rd, float eps,
+                         const void* q_idx, const void* w_idx, int HI, void* q8, float* wf, int B, void* stream);
 
 /* Index-key table conversion for cache snapshots (dsv41/engine.py:1072-1230 copies the cache tensors as they are;
  * the reference's index_k is bf16 [.., 128], this build's e4m3 + fp32 per-row power-of-two scale): encode rows of
