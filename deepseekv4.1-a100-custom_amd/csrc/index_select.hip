@@ -1,13 +1,21 @@
-// Decode lightning indexer in one launch: the scores of a row's compressed positions, their histogram and the top-k
-// selection (dsv41/decode.py:284-294, index_score followed by topk_indices; scores as dsv41/fused3.py:20-62, the
-// k largest of score[r, 0..cl) in ascending index order with -1 padding as dsv41/fused3.py:65-75, ties lowest index
-// first).
+// Decode lightning indexer in one launch: the scores of a row's compressed positions and the top-k selection
+// (dsv41/decode.py:284-294, index_score followed by topk_indices; scores as dsv41/fused3.py:20-62, the k largest of
+// score[r, 0..cl) in ascending index order with -1 padding as dsv41/fused3.py:65-75, ties lowest index first).
 //
 // Grid: R x nslots workgroups of 512 threads (chunk ch of row r is workgroup ch * R + r, so a row's chunks spread
-// over the XCDs), all resident at once (at most kIsMaxWG: 2 per CU).  Each workgroup:
-//   A. scores its 512 positions (8 waves x 64 keys, every key load issued up front, e4m3 keys against the prepared e4m3 queries, fp8 MFMA), keeps
-//      them in LDS, builds their 4096-bin histogram (top 12 bits of the order-preserving key) in LDS and adds it to
-//      the row's histogram with device-scope atomics
+// over the XCDs; FUSED: 3 R append workgroups first), all resident at once (at most kIsMaxWG: 2 per CU).  Each
+// workgroup scores its 512 positions (8 waves x 64 keys, every key load issued up front, e4m3 keys against the
+// prepared e4m3 queries, fp8 MFMA) and keeps them in LDS.  Then, on the one-exchange path (pub_m > 0):
+//   P. publishes the keys at or above a cut that keeps at least pub_m of its positions (4096 bins over its own key
+//      range) and the largest key it leaves out, then a flag word with the launch epoch;
+//   Q. reads every chunk's flag until all carry this epoch (the row barrier), then every published list (16-byte
+//      loads); LB = the largest left-out key of the row, T = the k-th largest published key above LB;
+//   R. when T exists and no key ties with T across the cut, writes its keys >= T at the offset counted from the
+//      earlier chunks' published keys >= T (ascending positions).  Every chunk of a row reads the same published
+//      data and takes the same decision; otherwise (a chunk holding more of the selection than it published, ties at
+//      T) the row takes the two-exchange path, which is also the whole path when pub_m == 0:
+//   A. the chunk's 4096-bin histogram (top 12 bits of the order-preserving key) added to the row's with device-scope
+//      atomics
 //   B. reads the row histogram until its total reaches the row's valid count (every chunk's additions have landed:
 //      this read is the row barrier and its data at once); threshold bin B (where the running count from the top
 //      reaches k) and need = k - (entries above B)
@@ -17,10 +25,15 @@
 //      epoch (the second row barrier and the gather in one round trip); clears its slice of the row histogram
 //   E. threshold candidate T (exact ranks / radix passes over the candidates)
 //   F. writes its taken positions (above B, or candidates >= T) at their global offset.
-// Data exchanged between workgroups (histogram, counts, candidates) is written and read with device-scope atomic
-// operations, which the hardware keeps coherent across the XCDs' L2 caches, so no cache maintenance is needed.  The
-// epoch of a launch is one more than the one the chunk's count word holds from the previous launch.  A wait gives up
-// after kIsSpinLimit polls and sets the error word, so every wave exits.
+// Data exchanged between workgroups (lists, flags, histogram, counts, candidates) is written and read with
+// device-scope operations (sc1), which the hardware keeps coherent across the XCDs' L2 caches, so no cache
+// maintenance is needed; a publisher waits for its data stores to complete (s_waitcnt) before it stores the flag or
+// count word a reader polls, and relies on the hardware keeping that order for device-scope accesses (an agent-scope
+// release / acquire would write back / invalidate whole L2 caches).  The epoch of a launch is one more than the one
+// the chunk's count word holds from the previous launch.  A wait gives up after kIsSpinLimit polls and sets the error
+// word, so every wave exits.
+#include <cstdlib>
+
 #include "rowop.h"
 #include "score_core.h"
 #include "select_core.h"
@@ -40,6 +53,11 @@ constexpr int kIsMaxChunks = 512;              // chunks per row (rows up to 262
 constexpr int kIsMaxWG = 512;                  // resident workgroups: 2 per CU
 constexpr int kIsSpinLimit = 1 << 20;
 
+constexpr int kIsLst = kIsChunk + 4;           // published-list slots per chunk (16-byte aligned lists)
+constexpr int kIsRd = 16;                      // published-list slots read per thread (more: the two-exchange path)
+// 16-byte reads of the published lists with the device-scope cache policy (sc1) of the atomics that wrote them
+typedef unsigned is_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kIsCpolDevice = 16;
 constexpr int kIsTagShift = 18;  // candidate low word: epoch tag (14 bits) << 18 | (~position & 0x3ffff)
 static_assert(kIsMaxChunks * kIsChunk <= (1 << kIsTagShift), "positions fit below the epoch tag");
 
@@ -125,6 +143,60 @@ DSV41_DEV RowOp is_app_op(const IsAppend& ap, int r, long slot, long ppos, int w
   return o;
 }
 
+// Largest u32 over the 64 lanes of a wave, in every lane: DPP lane moves as wave_incl_scan (lanes a move does not
+// reach keep their own value), then lane 63's result.
+DSV41_DEV uint32_t wave_umax(uint32_t x) {
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x111, 0xf, 0xf, false));  // row_shr:1
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x112, 0xf, 0xf, false));  // row_shr:2
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x114, 0xf, 0xf, false));  // row_shr:4
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x118, 0xf, 0xf, false));  // row_shr:8
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+// Largest of two u32 values each over the NT threads of a workgroup (red: 2 * NT / 64 words); one barrier, and
+// red must not be written again before a later barrier.
+template <int NT>
+DSV41_DEV void block_umax2(uint32_t& x0, uint32_t& x1, uint32_t* red) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  x0 = wave_umax(x0);
+  x1 = wave_umax(x1);
+  if (lane == 0) red[wave] = x0, red[NW + wave] = x1;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NW; ++w) x0 = max(x0, red[w]), x1 = max(x1, red[NW + w]);
+}
+
+// Shift that maps a key range [0, range] onto at most 4096 bins.
+DSV41_DEV int bin_shift(uint32_t range) {
+  const int b = 32 - __clz(range);
+  return b > 12 ? b - 12 : 0;
+}
+
+// Over 4096 LDS bins h (bin 0 first), the bin where the running count reaches x (1 <= x <= total): *bin and the
+// count before it, *before (into shared s_out[0], s_out[1]); NT = 512 threads, 8 bins each.  Barriers inside.
+DSV41_DEV void bins_reach(const int* h, int x, int* tmp, int* s_out) {
+  const int t = threadIdx.x;
+  int v[8], local = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = h[8 * t + i], local += v[i];
+  int tot;
+  int before = block_scan_dpp<512>(local, tmp, &tot);
+  if (before < x && x <= before + local) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (before < x && x <= before + v[i]) {
+        s_out[0] = 8 * t + i;
+        s_out[1] = before;
+      }
+      before += v[i];
+    }
+  }
+  __syncthreads();
+}
+
 struct IsArgs {
   ScoreArgs s;                // prepared e4m3 queries, folded weights, e4m3 keys + scales, seq, cl, n_pos; out or null
   int k, offset;
@@ -137,6 +209,10 @@ struct IsArgs {
   int* err;
   unsigned long long* pub;    // (FUSED) [R]: epoch << 32 | the score of the row's new key (its append workgroup's)
   IsAppend app;               // FUSED instances only
+  // one-exchange selection (pub_m > 0): every chunk publishes its top entries (at least pub_m of the chunk's keys)
+  int pub_m;
+  unsigned long long* fl;     // [R, nslots]: epoch << 32 | entries published
+  uint32_t* lst;              // [R, nslots, kIsLst]: entry 0 the largest unpublished key (0: none), then the keys
 };
 
 #ifdef DSV41_TIMING
@@ -150,8 +226,10 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   static_assert(MAXC <= kIsThreads && MAXC % 64 == 0, "one thread per chunk");
   const ScoreArgs& a = g.s;
   const int R = a.R, ns = g.nslots;
-  const bool extra = FUSED && (int)blockIdx.x >= R * ns;  // (FUSED) an append-only workgroup after the row grid
-  const int bx = extra ? (int)blockIdx.x - R * ns : (int)blockIdx.x;
+  // (FUSED) the 3 R append-only workgroups come first in the grid: the new key's score, which its row's selection
+  // waits for, is then computed from the launch's start
+  const bool extra = FUSED && (int)blockIdx.x < 3 * R;
+  const int bx = FUSED ? (extra ? (int)blockIdx.x : (int)blockIdx.x - 3 * R) : (int)blockIdx.x;
   const int r = extra ? bx / 3 : bx % R, ch = extra ? 0 : bx / R;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
@@ -167,6 +245,8 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   __shared__ float wfl[FUSED ? 64 : 1];            // (FUSED) the prepared head weights
   __shared__ __align__(16) uint8_t knew[FUSED ? 128 : 16];  // (FUSED) the new index key, e4m3, and its scale
   __shared__ float ksnew, redf[kIsThreads / 64];
+  __shared__ uint32_t ured[4 * kIsThreads / 64], s_T;  // (one-exchange path) reductions and scans
+  __shared__ int s_ro[2], s_m1, s_tie;
 
   // ---- A. row data (independent loads), scores, histogram
   DSV41_PH(0);
@@ -244,10 +324,12 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
         if (lane == 0 && knew_row < c) {
           const float v = is_cand(a, r, knew_row) ? sum * ksnew : -__builtin_inff();
           if (a.out && knew_row < a.n_pos) a.out[(long)r * a.out_rstride + knew_row] = v;
-          if (c > k) {  // (otherwise nobody reads the histogram)
+          if (c > k) {  // (otherwise nobody reads the histogram or the score)
             DSV41_PH(1);
-            __hip_atomic_fetch_add(g.hist + (long)r * kHistBins + (score_key(v) >> 20), 1, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+            // (one-exchange path: the chunk holding the position adds it to its own counts, even when it falls back)
+            if (g.pub_m == 0)
+              __hip_atomic_fetch_add(g.hist + (long)r * kHistBins + (score_key(v) >> 20), 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(g.pub + r, (unsigned long long)epoch << 32 | __float_as_uint(v), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
           }
@@ -316,6 +398,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   DSV41_TS(52);
   const bool sel = c > k;  // (otherwise every valid position is taken)
   float* orow = a.out ? a.out + (long)r * a.out_rstride : nullptr;
+  uint32_t kmax = 0u, kmin_c = 0u;  // (one-exchange path) largest key and complement of the smallest, this lane
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int p = pw + nt * 16 + l16;
@@ -323,15 +406,25 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     if (g4 == 0) {
       const float v = p < c ? (is_cand(a, r, p) ? sum * ksc[nt] : -__builtin_inff()) : 0.0f;
       sc[p - ch * kIsChunk] = v;
+      if (p < c && !(FUSED && holder && p == knew_row)) {
+        const uint32_t kv = score_key(v);
+        kmax = max(kmax, kv);
+        kmin_c = max(kmin_c, ~kv);
+      }
       // (FUSED: the new key's position is its append workgroup's: scored, counted and written there)
       if (!(FUSED && holder && p == knew_row)) {
-        if (p < c && sel) atomicAdd(&lhist[score_key(v) >> 20], 1);
+        if (p < c && sel && g.pub_m == 0) atomicAdd(&lhist[score_key(v) >> 20], 1);
         if (orow && p < a.n_pos) orow[p] = p < c ? v : -__builtin_inff();
       }
     }
   }
   DSV41_TS(53);
   DSV41_PX(6);
+  if (g.pub_m > 0) {  // the chunk's key range, for the one-exchange path's cut (read after the barrier below)
+    kmax = wave_umax(kmax);
+    kmin_c = wave_umax(kmin_c);
+    if (lane == 0) ured[wave] = kmax, ured[8 + wave] = kmin_c;
+  }
   __syncthreads();
   DSV41_PH(1);
   DSV41_TS(54);
@@ -346,6 +439,220 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     if (t == 0)
       __hip_atomic_store(rcnt + ch, (unsigned long long)epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
+  }
+  // ---- one-exchange selection.  Each chunk publishes the keys at or above a cut that keeps at least pub_m of its
+  // valid positions (the cut falls between bins of the chunk's own key range: 4096 bins down from its largest key),
+  // and the largest key it leaves out; then every chunk reads all published keys of the row.  Let LB be the largest
+  // left-out key of any chunk and T the k-th largest published key: when T > LB and no published key ties with T
+  // across the cut, the selection is exactly the keys >= T -- each chunk emits its own at the offset counted from
+  // the earlier chunks' published keys, with no second exchange.  Otherwise (a chunk holding more of the selection
+  // than it published, or a tie at T) every chunk of the row, reading the same published data, takes the same
+  // decision and falls back to the histogram and candidate exchanges below.  Only keys above LB can reach the
+  // selection on this path, so T is searched among them: 4096 bins over [LB, the largest key], then ranks in T's bin.
+  if (g.pub_m > 0) {
+    static_assert(kIsPer == 1, "one position per thread");
+    DSV41_PX(10);
+    if constexpr (FUSED) {
+      if (holder) {  // the new key's score comes from its append workgroup
+        if (t == 0) {
+          unsigned long long pv = 0ull;
+#pragma unroll 1
+          for (int sp = 0;; ++sp) {
+            pv = __hip_atomic_load(g.pub + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((uint32_t)(pv >> 32) == epoch) break;
+            if (sp >= kIsSpinLimit) {
+              __hip_atomic_store(g.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+          sc[knew_row - ch * kIsChunk] = __uint_as_float((uint32_t)pv);
+        }
+        __syncthreads();
+      }
+    }
+    const int pp = ch * kIsChunk + t;
+    const bool valid = pp < c;
+    const uint32_t kk = valid ? score_key(sc[t]) : 0u;
+    const int nvalid = min(max(c - ch * kIsChunk, 0), kIsChunk);
+    bool pubd = valid;
+    if (nvalid > g.pub_m) {
+      uint32_t mx = 0u, nmn = 0u;  // the largest key and the complement of the smallest (the scoring loop's)
+#pragma unroll
+      for (int w = 0; w < 8; ++w) mx = max(mx, ured[w]), nmn = max(nmn, ured[8 + w]);
+      if (FUSED && holder) {  // (the new key's score arrived after the scoring loop)
+        const uint32_t kn = score_key(sc[knew_row - ch * kIsChunk]);
+        mx = max(mx, kn);
+        nmn = max(nmn, ~kn);
+      }
+      const int sh = bin_shift(mx - ~nmn);
+      DSV41_PX(11);
+      if (valid) atomicAdd(&lhist[(mx - kk) >> sh], 1);  // bin 0: the chunk's largest key (lhist is zero here)
+      __syncthreads();
+      bins_reach(lhist, g.pub_m, tmp, s_ro);
+      DSV41_PX(12);
+      pubd = valid && (int)((mx - kk) >> sh) <= s_ro[0];
+    }
+    const unsigned long long bal = __ballot(pubd);
+    const int wo = __popcll(bal & ((1ull << lane) - 1));
+    if (lane == 0) wcnt[wave][0] = __popcll(bal);
+    uint32_t out_max = valid && !pubd ? kk : 0u, unused = 0u;
+    block_umax2<kIsThreads>(out_max, unused, ured);  // (its barrier also publishes wcnt)
+    int wbase = 0, npub = 0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      wbase += w < wave ? wcnt[w][0] : 0;
+      npub += wcnt[w][0];
+    }
+    uint32_t* const lrow = g.lst + (long)r * ns * kIsLst;
+    uint32_t* const mine = lrow + (long)ch * kIsLst;
+    if (pubd) __hip_atomic_store(mine + 1 + wbase + wo, kk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == 0) __hip_atomic_store(mine, out_max, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    DSV41_PX(13);
+    // the flag goes out after this workgroup's list has landed: a reader that sees this epoch finds the list
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    unsigned long long* const frow = g.fl + (long)r * ns;
+    if (t == 0)
+      __hip_atomic_store(frow + ch, (unsigned long long)epoch << 32 | (uint32_t)npub, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    DSV41_PH(2);
+    DSV41_PX(14);
+#pragma unroll
+    for (int j = 0; j < kHistBins / kIsThreads; ++j) lhist[t + j * kIsThreads] = 0;  // (read after the barriers below)
+    if (t == 0) s_m1 = 0, s_tie = 1;
+    {  // the row barrier: every chunk's flag carries this epoch
+      unsigned long long fv = 0ull;
+#pragma unroll 1
+      for (int spins = 0;; ++spins) {
+        if (t < ns) fv = __hip_atomic_load(frow + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__syncthreads_and(t >= ns || (uint32_t)(fv >> 32) == epoch)) break;
+        if (spins >= kIsSpinLimit) {
+          if (t == 0) __hip_atomic_store(g.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (t < ns) na_q[t] = (int)(fv & 0xffffu);
+    }
+    DSV41_PH(3);
+    DSV41_PX(15);
+    const int nq = t < ns ? na_q[t] : 0;
+    uint32_t nmax = (uint32_t)nq, unused2 = 0u;
+    block_umax2<kIsThreads>(nmax, unused2, ured + 2 * kIsThreads / 64);  // (its barrier also publishes na_q)
+    const int per = ((int)nmax + 4) & ~3, slots = ns * per;  // list slots read per chunk: entry 0 + nmax keys
+    bool fast = slots <= kIsRd * kIsThreads;
+    uint32_t T = 0u;
+    uint32_t v[kIsRd];
+    int vq[kIsRd / 4];  // chunk of v[4u .. 4u+3] (-1: none); list entry 0 is the chunk's largest left-out key
+    int ve[kIsRd / 4];  // list entry of v[4u]
+    bool key[kIsRd];    // v[u] is a published key above the largest left-out key
+    if (fast) {
+      // every published list, 16-byte device-scope loads all in flight together
+      const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(lrow, 0, 0x7fffffff, 0x00020000);
+#pragma unroll
+      for (int u = 0; u < kIsRd / 4; ++u) {
+        const int id = 4 * (u * kIsThreads + t), q = id / per, e = id - q * per;
+        const is_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(lrs, id < slots ? (q * kIsLst + e) * 4 : 0, 0,
+                                                                  kIsCpolDevice);
+        v[4 * u] = x[0], v[4 * u + 1] = x[1], v[4 * u + 2] = x[2], v[4 * u + 3] = x[3];
+        vq[u] = id < slots && e <= na_q[q] ? q : -1;
+        ve[u] = e;
+      }
+      uint32_t lb = 0u, ux = 0u;
+#pragma unroll
+      for (int u = 0; u < kIsRd; ++u) {
+        const int q = vq[u / 4], e = ve[u / 4] + (u & 3);
+        key[u] = q >= 0 && e > 0 && e <= na_q[q];  // (above lb: refined below)
+        if (q >= 0 && e == 0) lb = max(lb, v[u]);
+        if (key[u]) ux = max(ux, v[u]);
+      }
+      block_umax2<kIsThreads>(lb, ux, ured);
+      DSV41_PH(4);
+      DSV41_PX(16);
+      // T: the k-th largest key above lb
+      const int sh = bin_shift(ux > lb ? ux - lb - 1 : 0u);
+#pragma unroll
+      for (int u = 0; u < kIsRd; ++u) {
+        key[u] = key[u] && v[u] > lb;
+        if (key[u]) atomicAdd(&lhist[(ux - v[u]) >> sh], 1);
+      }
+      __syncthreads();
+      DSV41_PX(17);
+      int above_lb;
+      {
+        int hv[8], local = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hv[i] = lhist[8 * t + i], local += hv[i];
+        int before = block_scan_dpp<kIsThreads>(local, tmp, &above_lb);
+        if (before < k && k <= before + local) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (before < k && k <= before + hv[i]) {
+              s_ro[0] = 8 * t + i;
+              s_ro[1] = before;
+            }
+            before += hv[i];
+          }
+        }
+      }
+      fast = above_lb >= k;  // (uniform: the block total)
+      __syncthreads();
+      DSV41_PX(18);
+      if (fast) {
+        const int B = s_ro[0], need = k - s_ro[1], m1 = lhist[B];
+        uint32_t* const lcu = (uint32_t*)lc;
+#pragma unroll
+        for (int u = 0; u < kIsRd; ++u)
+          if (key[u] && (int)((ux - v[u]) >> sh) == B) lcu[atomicAdd(&s_m1, 1)] = v[u];
+        __syncthreads();
+        DSV41_PX(19);
+#pragma unroll 1
+        for (int i = t; i < m1; i += kIsThreads) {
+          const uint32_t x = lcu[i];
+          int gt = 0, ge = 0;
+#pragma unroll 4
+          for (int j = 0; j < m1; ++j) {
+            const uint32_t y = lcu[j];
+            gt += y > x;
+            ge += y >= x;
+          }
+          if (gt < need && need <= ge) {  // (threads holding equal keys write the same values)
+            s_T = x;
+            s_tie = ge != need;
+          }
+        }
+        __syncthreads();
+        DSV41_PX(20);
+        T = s_T;
+        fast = !s_tie;
+      }
+    }
+    DSV41_PH(5);
+    if (fast) {
+      // ---- ordered emission: this chunk's keys >= T after the earlier chunks' (their published keys >= T)
+      int sb = 0;  // (T > lb: the keys >= T are published keys above lb)
+#pragma unroll
+      for (int u = 0; u < kIsRd; ++u) sb += key[u] && vq[u / 4] < ch && v[u] >= T;
+      const bool take = valid && kk >= T;
+      int2 tot2;
+      const int2 ex2 = block_scan2_dpp<kIsThreads>(sb, (int)take, (int2*)ured, &tot2);
+      DSV41_PX(21);
+      if (take) oidx[tot2.x + ex2.y] = pp + g.offset;
+      if (t == 0)  // (the next launch's epoch)
+        __hip_atomic_store(rcnt + ch, (unsigned long long)epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      DSV41_PH(7);
+#ifdef DSV41_TIMING
+      if (t == 0 && blockIdx.x < 1024) g_is_spins[blockIdx.x][1] = -1;  // took the one-exchange path
+#endif
+      return;
+    }
+    // fall back: this chunk's histogram of all its valid keys (a new key included), then the two exchanges
+#pragma unroll
+    for (int j = 0; j < kHistBins / kIsThreads; ++j) lhist[t + j * kIsThreads] = 0;
+    __syncthreads();
+    if (valid) atomicAdd(&lhist[kk >> 20], 1);
+    __syncthreads();
   }
 #pragma unroll 1
   for (int i = t; i < kHistBins / 2; i += kIsThreads) {  // bins in pairs: one 64-bit add (no carry out of a bin)
@@ -789,7 +1096,8 @@ int dsv41_read_ts_is(long long* host) { return (int)hipMemcpyFromSymbol(host, HI
 
 long dsv41_index_select_workspace_bytes(int R, int n_pos) {
   const long ns = is_slots(n_pos);
-  return (long)R * kHistBins * 4 + (long)R * ns * 8 + (long)R * ns * kIsChunk * 8 + (long)R * ns * 8 + 16;
+  return (long)R * kHistBins * 4 + (long)R * ns * 8 + (long)R * ns * kIsChunk * 8 + (long)R * ns * 8 +
+         (long)R * ns * 8 + 16 + (long)R * ns * kIsLst * 4 + 16;
 }
 
 }  // extern "C"
@@ -837,13 +1145,20 @@ int select_setup(IsArgs& g, const void* q8, long q_rstride, const float* wf, lon
   g.cnt = (unsigned long long*)(w + (long)R * kHistBins * 4);
   g.cand = g.cnt + (long)R * ns;
   g.pub = g.cand + (long)R * ns * kIsChunk;                       // [R] u64 (in a spare [R, nslots] u64 region)
-  g.err = (int*)(g.cand + (long)R * ns * kIsChunk + (long)R * ns);
+  g.fl = g.pub + (long)R * ns;
+  g.lst = (uint32_t*)(((uintptr_t)(g.fl + (long)R * ns) + 15) & ~(uintptr_t)15);  // (16-byte list reads)
+  g.err = (int*)(w + dsv41_index_select_workspace_bytes(R, n_pos) - 16);
+  // published keys per chunk on the one-exchange path: twice a chunk's share of k, plus a margin (a chunk holding
+  // more of the selection than it published sends the row to the two-exchange path); DSV41_IS_PUB_M overrides it
+  // (0: the two-exchange path only)
+  g.pub_m = (int)min((long)kIsChunk, 2L * ((k + ns - 1) / ns) + 8);
+  if (const char* e = getenv("DSV41_IS_PUB_M")) g.pub_m = atoi(e) < 0 ? 0 : min(atoi(e), kIsChunk);
   return 0;
 }
 
 template <bool FUSED>
 int select_launch(const IsArgs& g, hipStream_t st) {
-  const int grid = g.s.R * g.nslots + (FUSED ? 3 * g.s.R : 0);  // (FUSED: the append-only workgroups last)
+  const int grid = g.s.R * g.nslots + (FUSED ? 3 * g.s.R : 0);  // (FUSED: the append-only workgroups first)
   if (g.nslots <= 128)
     index_select_kernel<128, FUSED><<<grid, kIsThreads, 0, st>>>(g);
   else
