@@ -259,10 +259,15 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     if (!extra) qprep512_load(g.app.q_idx + (long)r * a.HI * 128, g.app.w_idx + (long)r * a.HI, a.HI, qp);
   const long clr = row_cl(a, r);
   const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
-  // this launch's epoch: one more than the one this chunk's count word holds (earlier launches have completed)
-  const uint32_t epoch =
-      (uint32_t)(__hip_atomic_load(g.cnt + (long)r * ns + ch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32) + 1;
-  const uint32_t tag = epoch & ((1u << (32 - kIsTagShift)) - 1);
+  // this launch's epoch: one more than the one this chunk's count word holds (earlier launches have completed).
+  // Read after the key loads are issued: the device-scope load returns late, and a wait for any later load (loads
+  // return in order) would wait for it too
+  uint32_t epoch = 0, tag = 0;
+  auto read_epoch = [&]() {
+    epoch = (uint32_t)(__hip_atomic_load(g.cnt + (long)r * ns + ch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >>
+                       32) + 1;
+    tag = epoch & ((1u << (32 - kIsTagShift)) - 1);
+  };
   const int c = (int)(clr < 0 ? 0 : (clr > a.n_pos ? a.n_pos : clr)), k = g.k;
   if (clr > a.n_pos && ch == 0 && t == 0)  // positions beyond n_pos were promised never to be valid
     __hip_atomic_store(g.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -284,6 +289,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     const bool closes = ((ppos + 1) % ap.ratio) == 0;
     if (closes) knew_row = (ppos + 1) / ap.ratio - 1;
     if (extra) {  // the ring row, the compressed row or the index-key row; then done
+      read_epoch();
       const int which = bx % 3;
       if (which == 1 && !(ap.latent && ap.ckv)) return;
       if (which == 0) {  // (constant operation indices: the row operation's fields stay in registers)
@@ -369,6 +375,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     k1[nt] = *(const uint4*)(krow + 16);
     ksc[nt] = a.kscale[slot * a.ks_sstride + pl];
   }
+  read_epoch();
   DSV41_TS(50);
   DSV41_PX(2);
   if constexpr (FUSED) {
@@ -1148,10 +1155,10 @@ int select_setup(IsArgs& g, const void* q8, long q_rstride, const float* wf, lon
   g.fl = g.pub + (long)R * ns;
   g.lst = (uint32_t*)(((uintptr_t)(g.fl + (long)R * ns) + 15) & ~(uintptr_t)15);  // (16-byte list reads)
   g.err = (int*)(w + dsv41_index_select_workspace_bytes(R, n_pos) - 16);
-  // published keys per chunk on the one-exchange path: twice a chunk's share of k, plus a margin (a chunk holding
+  // published keys per chunk on the one-exchange path: 1.5 times a chunk's share of k, plus 8 (a chunk holding
   // more of the selection than it published sends the row to the two-exchange path); DSV41_IS_PUB_M overrides it
   // (0: the two-exchange path only)
-  g.pub_m = (int)min((long)kIsChunk, 2L * ((k + ns - 1) / ns) + 8);
+  g.pub_m = (int)min((long)kIsChunk, 3L * ((k + ns - 1) / ns) / 2 + 8);
   if (const char* e = getenv("DSV41_IS_PUB_M")) g.pub_m = atoi(e) < 0 ? 0 : min(atoi(e), kIsChunk);
   return 0;
 }
