@@ -682,6 +682,351 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   DSV41_WG_TS(1);
 }
 
+// ------------------------------------------------------------------------------------------------ decode kernel, 32 heads
+// Few query rows (decode), one gather round trip per workgroup: a workgroup owns one query row, 32 heads and a split
+// of at most 128 key positions, all gathered into LDS at once (two 64-key halves in flight; the QK of the first half
+// runs while the second lands).  Against attn_decode_kernel the rows of a split are gathered by two workgroups
+// instead of four, in one round trip instead of one per 64-key tile.  8 waves:
+//   QK  wave w = (hb = w & 1: heads 16hb..16hb+15 of the group, kp = w >> 1: keys 16kp..16kp+15 of each half):
+//       S^T for its 32 keys (16x16x32 bf16 MFMA, A = K from LDS, B = Q in VGPRs); one maximum per head over the whole
+//       split (exchanged through LDS: no online rescale), p = 2^(s - M), the bf16 probabilities into LDS in the PV
+//       MFMA's operand order (k = 8g + j: key 16kp + 4g + j of half 0 for j < 4, of half 1 for j >= 4), the partial
+//       sums into LDS;
+//   PV  wave w = (hb, cq = w >> 1: columns cq*DV/4 ..): O[16 heads x DV/4] = P V over the split (4 k-steps of the
+//       16x16x32 bf16 MFMA, V fragments by the LDS transpose read of both halves).
+// The partial (bf16, normalised by the split's sum) and (m, l) are stored with device-scope stores, staged through
+// LDS for 16-byte stores; the splits of a (row, 32-head) unit then merge cooperatively in the same launch, as in
+// attn_decode_kernel (every workgroup of the launch is resident at once: the host plans it so).  The head groups of
+// a (row, split) are placed on one XCD, so the rows they both gather come through one L2.
+// Cooperative merge of the 32-head kernel's partials (register-layout tiles): split workgroup sp of unit (r, hg)
+// merges tiles [sp*NT/ns, (sp+1)*NT/ns) of the unit's NT = 8 * DV / 64 tiles, one wave per tile (the host keeps
+// NT / ns <= 8).  Each wave issues its tile's partial loads first (device-scope, 8 bytes per lane and split), while
+// the workgroup turns the unit's (m, l) into per-(split, head) weights in LDS (wts: >= 64 * 32 floats):
+// w_s = l_s e^(m_s - M) / (sum_s l_s e^(m_s - M) + e^(sink - M)).  Output: bf16 round, inverse rope on the last rd
+// columns (the partner column of a pair is the neighbouring lane).
+template <int DV>
+DSV41_DEV void merge_tiles32(const AttnArgs& a, int r, int hg, int HG, long pr, int sp, float* wts) {
+  constexpr int CT = DV / 64, NT = 8 * CT, MS = 32;
+  const int ns = a.nsplit, H = a.H, h0 = hg * 32;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
+  const int ti = (int)((long)sp * NT / ns) + wave;
+  const bool act = ti < (int)((long)(sp + 1) * NT / ns);  // wave-uniform
+  const __amdgpu_buffer_rsrc_t rs = pacc_rsrc(a.pacc);
+  const long ub0 = ((long)r * HG + hg) * ns * (32L * DV) + ((long)ti * 64 + lane) * 4;  // split 0's entry of the lane
+  auto load_batch = [&](int s0, uint2 (&v)[MS]) {
+#pragma unroll
+    for (int u = 0; u < MS; ++u) {
+      const int s = s0 + u < ns ? s0 + u : ns - 1;
+      const auto x = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)((ub0 + (long)s * (32L * DV)) * 2), 0, kCpolDevice);
+      v[u] = make_uint2(x[0], x[1]);
+    }
+  };
+  uint2 v[MS];
+  if (act) load_batch(0, v);
+  // weights: thread (head hh = tid >> 4, q = tid & 15) takes splits q, q + 16, q + 32, q + 48 (one batch of loads);
+  // the head's maximum and sum over its 16 lanes
+  {
+    const int hh = tid >> 4, q = tid & 15, h = h0 + hh;
+    float m[4], l[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int sq = q + 16 * u;
+      const bool ok = sq < ns && h < H;
+      const long pi = ((long)r * H + (ok ? h : 0)) * ns + (ok ? sq : 0);
+      m[u] = ok ? __hip_atomic_load(a.pm + pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -1e30f;
+      l[u] = ok ? __hip_atomic_load(a.pl + pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+    }
+    const float M = group_max(fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3])), 16);
+    float w[4], den = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      w[u] = l[u] * exp2f((m[u] - M) * kLog2e);
+      den += w[u];
+    }
+    den = row16_sum(den) + exp2f((a.sink[h < H ? h : H - 1] - M) * kLog2e);
+    const float inv = 1.0f / den;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (q + 16 * u < ns) wts[(q + 16 * u) * 32 + hh] = w[u] * inv;
+  }
+  lds_barrier();
+  if (!act) return;
+  const int hb = ti / (4 * CT), cq = (ti / CT) & 3, ct = ti % CT;
+  const int hl = hb * 16 + 4 * g;  // heads hl .. hl + 3 of the unit
+  float num[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+  for (int s0 = 0; s0 < ns; s0 += MS) {
+    if (s0 > 0) load_batch(s0, v);
+#pragma unroll
+    for (int u = 0; u < MS; ++u) {
+      if (s0 + u < ns) {
+        const float4 w = *(const float4*)(wts + (s0 + u) * 32 + hl);
+        num[0] += w.x * __uint_as_float(v[u].x << 16);
+        num[1] += w.y * __uint_as_float(v[u].x & 0xffff0000u);
+        num[2] += w.z * __uint_as_float(v[u].y << 16);
+        num[3] += w.w * __uint_as_float(v[u].y & 0xffff0000u);
+      }
+    }
+  }
+  const int c = cq * (DV / 4) + ct * 16 + l16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float val = round_bf16(num[i]);
+    const float partner = dpp_mov<0xB1>(val);  // lane ^ 1: column c ^ 1 of the same head
+    if (a.rd > 0 && c >= DV - a.rd) {
+      const int jj = (c - (DV - a.rd)) >> 1;
+      const float cs = a.cos_t[pr * (a.rd / 2) + jj];
+      const float sn = -a.sin_t[pr * (a.rd / 2) + jj];
+      val = (c & 1) ? (partner * sn + val * cs) : (val * cs - partner * sn);
+    }
+    const int h = h0 + hl + i;
+    if (h < H) a.out[(long)r * a.out_rstride + (long)h * DV + c] = f2bf(val);
+  }
+}
+
+template <int DQK, int DV>
+__global__ void __launch_bounds__(512) attn_decode32_kernel(const AttnArgs a) {
+  DSV41_WG_TS(0);
+  constexpr int KS = DQK / 32;
+  constexpr int U = DQK / 8;           // 16-byte chunks per row; chunk c of row j stored at j*U + (c ^ (j & 7))
+  constexpr int HALF = 64;             // keys per half
+  constexpr int HALF_ELEMS = HALF * DQK;
+  constexpr int kLd = HALF * U / 512;  // 16-byte direct-to-LDS loads per lane per half
+  constexpr int CT = DV / 64;          // 16-column output tiles per PV wave (a quarter of DV)
+  static_assert(U % 8 == 0 && HALF * U % 512 == 0 && kLd < 16, "row width");
+  static_assert(32 * DQK <= HALF_ELEMS && 32 * U % 64 == 0, "Q staging fits one half, whole waves");
+  static_assert(32 * DV <= 2 * HALF_ELEMS && CT >= 1, "output staging fits the key buffer");
+  __shared__ __align__(16) uint16_t kbuf[2 * HALF_ELEMS];  // keys (half 0 | half 1); Q staging, then the output
+  __shared__ const uint16_t* rptr[2 * HALF];              // row of each key of the split (null: invalid)
+  __shared__ uint4 pex[2][4][64];                          // [hb][kp][lane]: probabilities, PV operand order
+  __shared__ float smax[2][4][16], ssum[2][4][16];         // [hb][kp][head]: partial maxima (log2 units) and sums
+  __shared__ int ixs[2 * HALF];                             // index entries of the split
+
+  const int HG = (a.H + 31) / 32;
+  const int x = blockIdx.x % kXcds, jx = blockIdx.x / kXcds;
+  const int grp = x + kXcds * (jx / HG);  // (row, split) pair; its HG head groups share XCD x
+  if (grp >= a.R * a.nsplit) return;
+  const int hg = jx % HG, r = grp / a.nsplit, sp = grp % a.nsplit;
+  if (hg * 32 >= a.H) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hb = wave & 1, kp = wave >> 1, cq = wave >> 1;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int H = a.H, h0 = hg * 32;
+  DSV41_PH(0);
+
+  // the row's position data first: scalar loads, before any inline-assembly load clobbers memory
+  long slot, pos = 0, pmax = 0, plim = 0;
+  if (a.mode == 1) {
+    slot = a.seq[r];
+    pos = a.pos[r];
+    pmax = a.pmax[r];
+    plim = a.plim ? a.plim[r] : pos;
+  } else {
+    slot = r / a.rows_per_slot;
+  }
+  // ---- index entries (waves 0-1, direct to LDS) and Q of the 32 heads staged into half 1, issued before any wait (the compiler's waits cannot tell these loads apart, so the waits are explicit)
+  const int W = a.n1;
+  const int* irow = a.t > 0 ? a.idx + (long)r * a.idx_rstride : nullptr;
+  const int j0 = sp * a.chunk, j1 = min(a.L, j0 + a.chunk);
+  const bool two = j1 - j0 > HALF;  // workgroup-uniform: the second half holds keys
+  constexpr int QCH = 32 * U;
+  constexpr int NQ01 = (QCH + 511) / 512;  // Q loads of waves 0 and 1 (QCH is a multiple of 256)
+  if (wave < 2) {
+    const int j = j0 + tid, jj = a.mode == 1 ? j - W : j;
+    const bool ok = j < j1 && jj >= 0 && irow;  // (other entries read a valid word and are ignored)
+    lds_dma4_at(ok ? (const void*)(irow + jj) : (const void*)g_zero_row, lds_addr_of(ixs) + (uint32_t)(wave * 256));
+  }
+  uint16_t* const qlds = kbuf + HALF_ELEMS;
+#pragma unroll
+  for (int u = 0; u < NQ01; ++u) {
+    const int cid = u * 512 + wave * 64 + lane;
+    if (u * 512 + wave * 64 < QCH) {  // wave-uniform (QCH % 64 == 0)
+      const int hh = cid / U, part = cid - hh * U;
+      const int h = h0 + hh < H ? h0 + hh : H - 1;  // rows of missing heads repeat the last head (never stored)
+      lds_dma16(a.q + (long)r * a.q_rstride + (long)h * DQK + part * 8, qlds + (u * 512 + wave * 64) * 8);
+    }
+  }
+  if (wave < 2) {  // row pointer of key j0 + tid (the same validity rules as attn_decode_kernel)
+    __builtin_amdgcn_s_waitcnt(NQ01 | (0x7 << 4) | (0xf << 8));  // vmcnt(NQ01): this wave's index entries landed
+    const int jj = a.mode == 1 ? j0 + tid - W : j0 + tid;
+    const int ix = j0 + tid < j1 && jj >= 0 && irow ? ixs[tid] : -1;
+    const uint16_t* base1 = a.kv1 + slot * a.kv1_sstride;
+    const uint16_t* base2 = a.kv2 ? a.kv2 + slot * a.kv2_sstride : nullptr;
+    const int j = j0 + tid;
+    const uint16_t* p = nullptr;
+    if (j < j1) {
+      if (a.mode == 1 && j < W) {
+        int m = (int)(pmax - j) % W;
+        m = m < 0 ? m + W : m;
+        const long held = pmax - m;
+        if (held >= 0 && held <= plim && pos - held < W) p = base1 + (long)j * DQK;
+      } else if (a.mode == 1) {
+        if (ix >= 0 && ix < a.n2) p = base2 + (long)ix * DQK;
+      } else if (ix >= 0 && ix < a.n1 + a.n2) {
+        p = ix < a.n1 ? base1 + (long)ix * DQK : base2 + (long)(ix - a.n1) * DQK;
+      }
+    }
+    rptr[tid] = p;
+  }
+  lds_barrier();  // (an LDS-only barrier: __syncthreads would wait for the Q loads in flight)
+  auto issue = [&](int hf) {  // direct-to-LDS loads of half hf (inline assembly: no compiler waits around them)
+    uint16_t* buf = kbuf + hf * HALF_ELEMS;
+    const uint16_t* src[kLd];  // all row pointers read before the first load (the loads clobber memory)
+#pragma unroll
+    for (int rd = 0; rd < kLd; ++rd) {
+      const int q = rd * 512 + wave * 64 + lane;  // LDS chunk position
+      const int jr = q / U, cs = q - jr * U;
+      const uint16_t* p = rptr[hf * HALF + jr];
+      src[rd] = p ? p + (cs ^ (jr & 7)) * 8 : g_zero_row;
+    }
+#pragma unroll
+    for (int rd = 0; rd < kLd; ++rd) lds_dma16(src[rd], buf + (rd * 512 + wave * 64) * 8);
+  };
+  issue(0);
+  DSV41_PH(1);
+  // Q has landed once at most half 0's loads of this wave remain (loads complete in order)
+  __builtin_amdgcn_s_waitcnt(kLd | (0x7 << 4) | (0xf << 8));  // vmcnt(kLd)
+  lds_barrier();  // every wave's Q chunks have landed (half 0's loads stay in flight)
+  uint4 qf[KS];  // B operand: Q of head 16hb + l16, k = 32 ks + 8g ..
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qlds + (hb * 16 + l16) * DQK + ks * 32 + g * 8);
+  lds_barrier();  // (Q has been read: half 1 takes its keys)
+  if (two) issue(1);
+  DSV41_PH(2);
+
+  // ---- S^T of this wave's 16 keys of each half (key row 16kp + l16 of the half as the A operand)
+  auto qk = [&](int hf) {
+    const int jr = kp * 16 + l16;
+    const uint16_t* krow = kbuf + hf * HALF_ELEMS + jr * DQK;
+    f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      acc = mfma_bf16_16x16x32(*(const uint4*)(krow + (((ks * 4 + g) ^ (jr & 7)) * 8)), qf[ks], acc);
+    return acc;  // acc[i] = score of key 16kp + 4g + i of the half, head 16hb + l16
+  };
+  if (two)
+    __builtin_amdgcn_s_waitcnt(kLd | (0x7 << 4) | (0xf << 8));  // vmcnt(kLd): half 0 has landed
+  else
+    __builtin_amdgcn_s_waitcnt(0);
+  lds_barrier();
+  const f32x4_t s0 = qk(0);
+  f32x4_t s1 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if (two) {
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
+    s1 = qk(1);
+  }
+  DSV41_PH(3);
+
+  // ---- softmax over the split: one maximum per head (log2 units), probabilities and partial sums
+  const float sl2 = a.scale * kLog2e;
+  float xv[8];
+  float mx = -1e30f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int kk = (e >> 2) * HALF + kp * 16 + 4 * g + (e & 3);
+    xv[e] = rptr[kk] ? (e < 4 ? s0[e & 3] : s1[e & 3]) * sl2 : -1e30f;
+    mx = fmaxf(mx, xv[e]);
+  }
+  mx = row_max4(mx);
+  if (g == 0) smax[hb][kp][l16] = mx;
+  lds_barrier();
+  const float M = fmaxf(fmaxf(smax[hb][0][l16], smax[hb][1][l16]), fmaxf(smax[hb][2][l16], smax[hb][3][l16]));
+  float pv[8];
+  float ps = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int kk = (e >> 2) * HALF + kp * 16 + 4 * g + (e & 3);
+    pv[e] = rptr[kk] ? exp2f(xv[e] - M) : 0.0f;
+    ps += pv[e];
+  }
+  ps = row_sum4(ps);
+  if (g == 0) ssum[hb][kp][l16] = ps;
+  pex[hb][kp][lane] = make_uint4(pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
+                                 pack_bf16x2(pv[6], pv[7]));
+  lds_barrier();  // probabilities and sums visible
+
+  // ---- PV: O[heads 16hb + 4g + i][columns cq*DV/4 + 16ct + l16]
+  f32x4_t o[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) o[ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const int vj = 4 * g + (l16 >> 2);
+#pragma unroll
+  for (int k4 = 0; k4 < 4; ++k4) {
+    const uint4 pa = pex[hb][k4][lane];
+    const int jr = k4 * 16 + vj;  // V rows jr (half 0) and jr of half 1: (jr + 64) & 7 = jr & 7
+    const uint16_t* vrow = kbuf + jr * DQK + ((l16 & 1) << 2);
+    const int vsw = jr & 7;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int cch = ((cq * (DV / 4) + ct * 16) >> 3) + ((l16 & 3) >> 1);  // chunk of column col0 + 4*(l16&3)
+      const uint16_t* pp = vrow + ((cch ^ vsw) << 3);
+      const uint2 v0 = lds_read_tr16(pp);
+      const uint2 v1 = two ? lds_read_tr16(pp + HALF_ELEMS) : make_uint2(0u, 0u);
+      o[ct] = mfma_bf16_16x16x32(pa, make_uint4(v0.x, v0.y, v1.x, v1.y), o[ct]);
+    }
+  }
+  DSV41_PH(4);
+
+  // ---- the split's partial: O / l in bf16 in the MFMA's register layout (tile (hb, cq, ct): 64 lanes x 4 heads, one
+  // 8-byte device-scope store per lane and tile), m (natural-log units) and l per head
+  const long pr = pos < 0 ? 0 : pos;
+  {
+    float invl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hl = 4 * g + i;
+      const float l = ssum[hb][0][hl] + ssum[hb][1][hl] + ssum[hb][2][hl] + ssum[hb][3][hl];
+      invl[i] = l > 0.0f ? 1.0f / l : 0.0f;
+    }
+    const long ub = (((long)r * HG + hg) * a.nsplit + sp) * (32L * DV);  // this split's partial (bf16 elements)
+    const __amdgpu_buffer_rsrc_t rs = pacc_rsrc(a.pacc);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const long off = ub + ((long)((hb * 4 + cq) * CT + ct) * 64 + lane) * 4;
+      __builtin_amdgcn_raw_buffer_store_b64(
+          u32x2_t{pack_bf16x2(o[ct][0] * invl[0], o[ct][1] * invl[1]), pack_bf16x2(o[ct][2] * invl[2], o[ct][3] * invl[3])},
+          rs, (int)(off * 2), 0, kCpolDevice);
+    }
+  }
+  if (tid < 32 && h0 + tid < H) {
+    const int hb2 = tid >> 4, hl = tid & 15;
+    const float Mh = fmaxf(fmaxf(smax[hb2][0][hl], smax[hb2][1][hl]), fmaxf(smax[hb2][2][hl], smax[hb2][3][hl]));
+    const float Lh = ssum[hb2][0][hl] + ssum[hb2][1][hl] + ssum[hb2][2][hl] + ssum[hb2][3][hl];
+    const long pi = ((long)r * H + h0 + tid) * a.nsplit + sp;
+    __hip_atomic_store(a.pm + pi, Mh * 0.6931471805599453f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.pl + pi, Lh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  DSV41_PH(5);
+
+  // ---- every split workgroup of the unit merges a slice once all have published.  Counter = epoch * 256 +
+  // arrivals: the last arrival of a launch moves it to the next epoch (any nsplit <= 255, any history)
+  unsigned long long* cnt = a.coop + (long)r * HG + hg;
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned long long old = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long base = old & ~255ull;
+    if ((int)(old & 255) + 1 == a.nsplit) {
+      __hip_atomic_fetch_add(cnt, 256ull - a.nsplit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      int spins = 0;
+#pragma unroll 1
+      while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < base + a.nsplit &&
+             ++spins < kCoopSpinLimit)
+        __builtin_amdgcn_s_sleep(1);
+      // gave up waiting (the unit's workgroups were not co-resident): the merge below may read unpublished
+      // partials, so the launch reports it through the workspace's error word
+      if (spins >= kCoopSpinLimit) __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  DSV41_PH(6);
+  merge_tiles32<DV>(a, r, hg, HG, pr, sp, (float*)kbuf);
+  DSV41_PH(7);
+  DSV41_WG_TS(1);
+}
+
 // ------------------------------------------------------------------------------------------------ prefill kernel
 // Many query rows (prefill chunk): one workgroup per (query row, 64 heads), whole key list, no split.  8 waves (2 per
 // SIMD), two roles per 64-key tile:
@@ -1421,6 +1766,12 @@ bool use_decode_kernel(int R, int H) { return (long)R * ((H + 63) / 64) < 16; }
 
 template <int DQK, int DV>
 int launch_attn(AttnArgs& a, hipStream_t st) {
+  if (use_decode_kernel(a.R, a.H) && a.dec32) {
+    const int HG2 = (a.H + 31) / 32;
+    attn_decode32_kernel<DQK, DV><<<dim3(kXcds * HG2 * ((a.R * a.nsplit + kXcds - 1) / kXcds)), 512, 0, st>>>(a);
+    DSV41_CHECK_LAUNCH();
+    return 0;
+  }
   if (use_decode_kernel(a.R, a.H)) {
     const int HG = (a.H + 15) / 16;
     const dim3 grid = a.coop && a.hg_share ? dim3(kXcds * HG * ((a.R * a.nsplit + kXcds - 1) / kXcds))
@@ -1485,7 +1836,25 @@ constexpr int kDecWG = DSV41_DEC_WG;
 
 // Split plan.  Decode kernel: <= 192 workgroups over (rows x 16-head groups x splits), >= 2 tiles of 64 keys per
 // split.  64-head kernel: splits up to one workgroup per CU when rows are few, >= 2 tiles of 32 keys per split.
+// The 32-head decode kernel's plan (automatic split count only): splits of 128 keys (64 when that leaves fewer than
+// 96 workgroups), 8 to 64 of them, every workgroup resident at once (one per CU; the head groups of a (row, split) on one
+// XCD).  DSV41_ATTN_DEC32=0 selects the 16-head kernel instead.  Returns false when it does not apply.
+bool plan_dec32(int R, int H, int L, int* nsplit, int* chunk) {
+  const char* env = getenv("DSV41_ATTN_DEC32");
+  if ((env && atoi(env) == 0) || !use_decode_kernel(R, H)) return false;
+  const int HG2 = (H + 31) / 32;
+  int ch = 128;
+  if ((long)R * HG2 * ((L + 127) / 128) < 96) ch = 64;
+  const int ns = (L + ch - 1) / ch;
+  if (ns < 8 || ns > 64) return false;  // (the merge: <= 8 of 64 output tiles per workgroup, <= 64 splits)
+  if ((long)HG2 * (((long)R * ns + kXcds - 1) / kXcds) > cus_per_xcd()) return false;
+  *nsplit = ns;
+  *chunk = ch;
+  return true;
+}
+
 void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
+  if (want <= 0 && plan_dec32(R, H, L, nsplit, chunk)) return;
   const bool dec = use_decode_kernel(R, H);
   const int tile = dec ? 64 : 32;
   const int tiles = (L + tile - 1) / tile < 1 ? 1 : (L + tile - 1) / tile;
@@ -1531,7 +1900,8 @@ long counter_bytes(int R, int H) {
 
 long workspace_bytes(int R, int H, int ns, int dv) {
   if (ns <= 1) return 0;
-  if (use_decode_kernel(R, H)) return counter_bytes(R, H) + (long)R * H * ns * (8 + 2L * dv);
+  // (the 32-head kernel's partials cover whole 32-head groups)
+  if (use_decode_kernel(R, H)) return counter_bytes(R, H) + (long)R * H * ns * 8 + (long)R * ((H + 31) / 32 * 32) * ns * 2L * dv;
   return (long)R * H * ns * (2 + dv) * 4;
 }
 
@@ -1548,7 +1918,11 @@ int finish_plan(AttnArgs& a, int want_nsplit, void* ws, long ws_bytes, int dv) {
     a.pm = f;
     a.pl = f + (long)a.R * a.H * ns;
     a.pacc = f + 2L * a.R * a.H * ns;
-    if (dec && fuse_merge(a.R, a.H, ns)) {
+    if (dec && want_nsplit <= 0 && plan_dec32(a.R, a.H, a.L, &ns, &chunk)) {
+      a.dec32 = 1;
+      a.err = (int*)ws;
+      a.coop = (unsigned long long*)((char*)ws + kCounterBase + ((long)a.R * ((a.H + 15) / 16) * 4 + 7) / 8 * 8);
+    } else if (dec && fuse_merge(a.R, a.H, ns)) {
       a.units = a.R * ((a.H + 15) / 16);
       a.upx = (a.units + kXcds - 1) / kXcds;
       a.err = (int*)ws;
@@ -1782,7 +2156,7 @@ int dsv41_sattn2_noalloc(const void* q, const void* kv_win, long win_sstride, in
   rc = finish_plan(a, want_nsplit, ws, DSV41_SCRATCH_BYTES, dv);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
-  if (a.arrive) {  // the split counters (and error word) start at zero: a previous call may have used another layout
+  if (a.arrive || a.dec32) {  // the split counters (and error word) start at zero: a previous call may have used another layout
     const long words = counter_bytes(a.R, a.H) / 4;
     zero_words_kernel<<<(int)((words + 255) / 256 < 64 ? (words + 255) / 256 : 64), 256, 0, st>>>(
         (unsigned int*)ws, words);

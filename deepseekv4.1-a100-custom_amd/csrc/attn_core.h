@@ -41,6 +41,7 @@ struct AttnArgs {
   int* err;     // with arrive: the workspace error word (set to 1 when a merge stopped waiting for its unit)
   int units;    // with arrive: (row, 16-head group) units, placed upx per XCD (1-D grid of kXcds * upx * nsplit)
   int hg_share; // with coop: the head groups of a (row, split) placed on one XCD instead
+  int dec32;    // decode: the 32-head kernel (one gather round trip per split of <= 128 keys), cooperative merge
   int upx;
   const float* cos_t;
   const float* sin_t;
@@ -69,27 +70,23 @@ DSV41_DEV uint2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
-// Cooperative merge, run by every split workgroup sp of a unit once all nsplit have published: it merges
-// (head, 8-column group) elements [sp*E/ns, (sp+1)*E/ns) of the unit's E = 16 * DV / 8, one per thread.  The partials
-// were written with device-scope stores and are read with device-scope loads (coherent across the XCDs, wherever the
-// unit's workgroups ran).  Weights as merge_splits.
+// Cooperative merge, run by every split workgroup of a unit once all nsplit have published (merge_slice).  The
+// partials were written with device-scope stores and are read with device-scope loads (coherent across the XCDs,
+// wherever the unit's workgroups ran).  Weights as merge_splits.
 // Device-scope (sc1) 16-byte accesses to the split partials of the cooperative merge: one request per 16 bytes, with
 // the cache policy of device-scope atomics (coherent across the XCDs).
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kCpolDevice = 16;  // sc1
 DSV41_DEV __amdgpu_buffer_rsrc_t pacc_rsrc(const float* pacc) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)pacc, 0, 0x7fffffff, 0x00020000);
 }
 
-template <int DV, int MS>  // MS: splits per batch of loads (one batch for up to MS splits: one round trip)
-DSV41_DEV void merge_slice_ms(const AttnArgs& a, int r, int h0, long pr, int sp) {
-  constexpr int CG = DV / 8, E = 16 * CG;
-  static_assert(E / 2 <= 512, "a slice fits the workgroup (nsplit >= 2)");
+// One (head, 8-column group) element of the merged output.  MS: splits per batch of loads (one batch for up to MS
+// splits: one round trip).
+template <int DV, int MS>
+DSV41_DEV void merge_elem(const AttnArgs& a, int r, int h, int c, long pr) {
   const int ns = a.nsplit, H = a.H;
-  const int e = (int)((long)sp * E / ns) + (int)threadIdx.x;
-  if (e >= (int)((long)(sp + 1) * E / ns)) return;
-  const int hh = e / CG, c = (e - hh * CG) * 8, h = h0 + hh;
-  if (h >= H) return;
   const long base = ((long)r * H + h) * ns;
   const __amdgpu_buffer_rsrc_t rs = pacc_rsrc(a.pacc);
   const float sink = a.sink[h];
@@ -146,12 +143,20 @@ DSV41_DEV void merge_slice_ms(const AttnArgs& a, int r, int h0, long pr, int sp)
   *(uint4*)(a.out + (long)r * a.out_rstride + (long)h * DV + c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
 }
 
-template <int DV>
+// Every split workgroup sp of a unit of NH heads (h0 ..) merges (head, 8-column group) elements
+// [sp*E/ns, (sp+1)*E/ns) of the unit's E = NH * DV / 8, one per thread (the host keeps E / ns <= the workgroup).
+template <int DV, int NH = 16>
 DSV41_DEV void merge_slice(const AttnArgs& a, int r, int h0, long pr, int sp) {
-  if (a.nsplit <= 16)
-    merge_slice_ms<DV, 16>(a, r, h0, pr, sp);
+  constexpr int CG = DV / 8, E = NH * CG;
+  const int ns = a.nsplit;
+  const int e = (int)((long)sp * E / ns) + (int)threadIdx.x;
+  if (e >= (int)((long)(sp + 1) * E / ns)) return;
+  const int hh = e / CG, c = (e - hh * CG) * 8, h = h0 + hh;
+  if (h >= a.H) return;
+  if (ns <= 16)
+    merge_elem<DV, 16>(a, r, h, c, pr);
   else
-    merge_slice_ms<DV, 32>(a, r, h0, pr, sp);
+    merge_elem<DV, 32>(a, r, h, c, pr);
 }
 
 }  // namespace

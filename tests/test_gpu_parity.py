@@ -292,6 +292,45 @@ def test_sattn2_absorbed_mla_ragged_with_drafts(H):
         attn_close(host(o), want, f"sattn2 mla ragged+drafts H={H} call {call_no} nsplit {ns}")
 
 
+@pytest.mark.parametrize("H", [64, 40])
+@pytest.mark.parametrize("rows", [4, 1])
+def test_sattn2_decode_kernels_32_and_16_heads(rows, H, monkeypatch):
+    """The decode attention's two kernels (32-head workgroups with one gather round trip per split of <= 128 keys,
+    and 16-head workgroups over 64-key tiles; DSV41_ATTN_DEC32 selects) at the C2 / C4 shapes: 576/512 absorbed MLA,
+    ring 128 + k 2048, slots at ragged positions (short contexts leave whole splits without a valid key), against
+    the oracle; calls alternating between the kernels share one workspace (its counters stay ready for either)."""
+    import dsv41_amd
+    from dsv41_amd._lib import lib
+    r = rng(19 + rows)
+    dqk, dv, win, k = 576, 512, 128, 2048
+    S, n_c = 4, 4096
+    q = O.bf16(r.standard_normal((rows, 1, H, dqk)).astype(np.float32))
+    sink = r.standard_normal(H).astype(np.float32)
+    ring = O.bf16(r.standard_normal((S, win, dqk)).astype(np.float32) * 0.1)
+    ckv = O.bf16(r.standard_normal((S, n_c, dqk)).astype(np.float32) * 0.1)
+    pos = [16383, 100, 5000, 7][:rows]
+    seq = [0, 1, 2, 3][:rows]
+    idx = np.full((rows, 1, k), -1, np.int32)
+    for b in range(rows):
+        cl = (pos[b] + 1) // 4
+        nv = min(k, cl)
+        idx[b, 0, :nv] = np.sort(r.choice(cl, nv, replace=False))
+    cos = np.zeros((1, 1), np.float32)
+    want = O.sattn2(q, ring, ckv, idx, pos, seq, pos, pos, sink, cos, cos, 0, dqk ** -0.5, dv=dv)
+    nbytes = 0
+    for flag in ("1", "0"):
+        monkeypatch.setenv("DSV41_ATTN_DEC32", flag)
+        nbytes = max(nbytes, lib().dsv41_attn_workspace_bytes(rows, H, win + k, dv, 0))
+    ws = torch.zeros(max(nbytes, 4) // 4, dtype=torch.float32, device=DEV)
+    for call_no, flag in enumerate(["1", "0", "1", "1", "0"]):
+        monkeypatch.setenv("DSV41_ATTN_DEC32", flag)
+        print(f"[sattn2 decode kernels] rows {rows} H {H} call {call_no} dec32={flag}", flush=True)
+        o = dsv41_amd.sattn2(bf(q), bf(ring), bf(ckv), torch.from_numpy(idx).to(DEV), i64(pos), f32(sink), f32(cos),
+                             f32(cos), 0, dqk ** -0.5, i64(seq), i64(pos), plim=i64(pos), d_v=dv, ws=ws)
+        attn_close(host(o), want, f"sattn2 decode rows={rows} H={H} call {call_no} dec32={flag}")
+        assert int(ws.view(torch.int32)[0].item()) == 0, "a cooperative merge stopped waiting for its unit"
+
+
 # ------------------------------------------------------------------------------------------------ indexer
 def _fp4_rows(r, shape, scale=0.1):
     return O.bf16(O.fake_quant_fp4(O.bf16(r.standard_normal(shape).astype(np.float32) * scale), 32))
