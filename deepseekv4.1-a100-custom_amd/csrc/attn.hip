@@ -16,6 +16,7 @@
 // Several splits per row write fp32 partials (m, l, acc); a combine kernel merges them with the sink and applies
 // the inverse rope (dsv41/fused2.py:381-403).  A single split writes the final bf16 output directly.
 #include <mutex>
+#include <type_traits>
 
 #include "attn_core.h"
 
@@ -692,10 +693,10 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
 //       split (exchanged through LDS: no online rescale), p = 2^(s - M), the bf16 probabilities into LDS in the PV
 //       MFMA's operand order (k = 8g + j: key 16kp + 4g + j of half 0 for j < 4, of half 1 for j >= 4), the partial
 //       sums into LDS;
-//   PV  wave w = (hb, cq = w >> 1: columns cq*DV/4 ..): O[16 heads x DV/4] = P V over the split (4 k-steps of the
-//       16x16x32 bf16 MFMA, V fragments by the LDS transpose read of both halves).
-// The partial (bf16, normalised by the split's sum) and (m, l) are stored with device-scope stores, staged through
-// LDS for 16-byte stores; the splits of a (row, 32-head) unit then merge cooperatively in the same launch, as in
+//   PV  wave w: O[32 heads x columns w*DV/8 ..] = P V over the split (4 k-steps of the 16x16x32 bf16 MFMA, each V
+//       fragment -- the LDS transpose read of both halves -- used for both head blocks).
+// The partial (bf16, normalised by the split's sum, in the MFMA's register layout) and (m, l) are stored with
+// device-scope stores; the splits of a (row, 32-head) unit then merge cooperatively in the same launch, as in
 // attn_decode_kernel (every workgroup of the launch is resident at once: the host plans it so).  The head groups of
 // a (row, split) are placed on one XCD, so the rows they both gather come through one L2.
 // Cooperative merge of the 32-head kernel's partials (register-layout tiles): split workgroup sp of unit (r, hg)
@@ -706,7 +707,7 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
 // columns (the partner column of a pair is the neighbouring lane).
 template <int DV>
 DSV41_DEV void merge_tiles32(const AttnArgs& a, int r, int hg, int HG, long pr, int sp, float* wts) {
-  constexpr int CT = DV / 64, NT = 8 * CT, MS = 32;
+  constexpr int CW = DV / 128, NT = 16 * CW, MS = 32;
   const int ns = a.nsplit, H = a.H, h0 = hg * 32;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
   const int ti = (int)((long)sp * NT / ns) + wave;
@@ -751,7 +752,7 @@ DSV41_DEV void merge_tiles32(const AttnArgs& a, int r, int hg, int HG, long pr, 
   }
   lds_barrier();
   if (!act) return;
-  const int hb = ti / (4 * CT), cq = (ti / CT) & 3, ct = ti % CT;
+  const int hb = ti / (8 * CW), w = (ti / CW) & 7, ct = ti % CW;
   const int hl = hb * 16 + 4 * g;  // heads hl .. hl + 3 of the unit
   float num[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 1
@@ -768,7 +769,7 @@ DSV41_DEV void merge_tiles32(const AttnArgs& a, int r, int hg, int HG, long pr, 
       }
     }
   }
-  const int c = cq * (DV / 4) + ct * 16 + l16;
+  const int c = w * (DV / 8) + ct * 16 + l16;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float val = round_bf16(num[i]);
@@ -792,10 +793,10 @@ __global__ void __launch_bounds__(512) attn_decode32_kernel(const AttnArgs a) {
   constexpr int HALF = 64;             // keys per half
   constexpr int HALF_ELEMS = HALF * DQK;
   constexpr int kLd = HALF * U / 512;  // 16-byte direct-to-LDS loads per lane per half
-  constexpr int CT = DV / 64;          // 16-column output tiles per PV wave (a quarter of DV)
+  constexpr int CW = DV / 128;         // 16-column output tiles per wave and head block (an eighth of DV)
   static_assert(U % 8 == 0 && HALF * U % 512 == 0 && kLd < 16, "row width");
   static_assert(32 * DQK <= HALF_ELEMS && 32 * U % 64 == 0, "Q staging fits one half, whole waves");
-  static_assert(32 * DV <= 2 * HALF_ELEMS && CT >= 1, "output staging fits the key buffer");
+  static_assert(CW >= 1, "DV a multiple of 128");
   __shared__ __align__(16) uint16_t kbuf[2 * HALF_ELEMS];  // keys (half 0 | half 1); Q staging, then the output
   __shared__ const uint16_t* rptr[2 * HALF];              // row of each key of the split (null: invalid)
   __shared__ uint4 pex[2][4][64];                          // [hb][kp][lane]: probabilities, PV operand order
@@ -809,7 +810,7 @@ __global__ void __launch_bounds__(512) attn_decode32_kernel(const AttnArgs a) {
   const int hg = jx % HG, r = grp / a.nsplit, sp = grp % a.nsplit;
   if (hg * 32 >= a.H) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hb = wave & 1, kp = wave >> 1, cq = wave >> 1;
+  const int hb = wave & 1, kp = wave >> 1;
   const int l16 = lane & 15, g = lane >> 4;
   const int H = a.H, h0 = hg * 32;
   DSV41_PH(0);
@@ -869,29 +870,39 @@ __global__ void __launch_bounds__(512) attn_decode32_kernel(const AttnArgs a) {
     rptr[tid] = p;
   }
   lds_barrier();  // (an LDS-only barrier: __syncthreads would wait for the Q loads in flight)
-  auto issue = [&](int hf) {  // direct-to-LDS loads of half hf (inline assembly: no compiler waits around them)
+  // direct-to-LDS loads of rounds [rd0, rd1) of half hf (inline assembly: no compiler waits around them)
+  auto issue = [&](int hf, auto rd0c, auto rd1c) {
+    constexpr int rd0 = decltype(rd0c)::value, rd1 = decltype(rd1c)::value;
     uint16_t* buf = kbuf + hf * HALF_ELEMS;
-    const uint16_t* src[kLd];  // all row pointers read before the first load (the loads clobber memory)
-#pragma unroll
-    for (int rd = 0; rd < kLd; ++rd) {
+    const uint16_t* src[rd1 > rd0 ? rd1 - rd0 : 1];  // row pointers read before the first load (the loads clobber
+#pragma unroll                                        // memory)
+    for (int rd = rd0; rd < rd1; ++rd) {
       const int q = rd * 512 + wave * 64 + lane;  // LDS chunk position
       const int jr = q / U, cs = q - jr * U;
       const uint16_t* p = rptr[hf * HALF + jr];
-      src[rd] = p ? p + (cs ^ (jr & 7)) * 8 : g_zero_row;
+      src[rd - rd0] = p ? p + (cs ^ (jr & 7)) * 8 : g_zero_row;
     }
 #pragma unroll
-    for (int rd = 0; rd < kLd; ++rd) lds_dma16(src[rd], buf + (rd * 512 + wave * 64) * 8);
+    for (int rd = rd0; rd < rd1; ++rd) lds_dma16(src[rd - rd0], buf + (rd * 512 + wave * 64) * 8);
   };
-  issue(0);
+  using C0 = std::integral_constant<int, 0>;
+  using CQ = std::integral_constant<int, NQ01>;  // rounds from NQ01 on lie past the Q staging (LDS chunks < QCH)
+  using CL = std::integral_constant<int, kLd>;
+  static_assert(NQ01 <= kLd, "Q staging within half 1");
+  issue(0, C0{}, CL{});
+  if (two) issue(1, CQ{}, CL{});
+  // Q has landed once at most the key loads issued after it remain (loads complete in order)
+  if (two)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kLd - NQ01));
+  else
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLd));
+  lds_barrier();  // every wave's Q chunks have landed (the key loads stay in flight)
   DSV41_PH(1);
-  // Q has landed once at most half 0's loads of this wave remain (loads complete in order)
-  __builtin_amdgcn_s_waitcnt(kLd | (0x7 << 4) | (0xf << 8));  // vmcnt(kLd)
-  lds_barrier();  // every wave's Q chunks have landed (half 0's loads stay in flight)
   uint4 qf[KS];  // B operand: Q of head 16hb + l16, k = 32 ks + 8g ..
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qlds + (hb * 16 + l16) * DQK + ks * 32 + g * 8);
-  lds_barrier();  // (Q has been read: half 1 takes its keys)
-  if (two) issue(1);
+  lds_barrier();  // (Q has been read: the rest of half 1 takes its chunks)
+  if (two) issue(1, C0{}, CQ{});
   DSV41_PH(2);
 
   // ---- S^T of this wave's 16 keys of each half (key row 16kp + l16 of the half as the A operand)
@@ -946,47 +957,54 @@ __global__ void __launch_bounds__(512) attn_decode32_kernel(const AttnArgs a) {
                                  pack_bf16x2(pv[6], pv[7]));
   lds_barrier();  // probabilities and sums visible
 
-  // ---- PV: O[heads 16hb + 4g + i][columns cq*DV/4 + 16ct + l16]
-  f32x4_t o[CT];
+  // ---- PV: O[heads 16b + 4g + i][columns w*DV/8 + 16ct + l16] for both head blocks b (each V fragment read once)
+  f32x4_t o[2][CW];
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) o[ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int ct = 0; ct < CW; ++ct) o[b][ct] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const int vj = 4 * g + (l16 >> 2);
 #pragma unroll
   for (int k4 = 0; k4 < 4; ++k4) {
-    const uint4 pa = pex[hb][k4][lane];
+    const uint4 pa0 = pex[0][k4][lane], pa1 = pex[1][k4][lane];
     const int jr = k4 * 16 + vj;  // V rows jr (half 0) and jr of half 1: (jr + 64) & 7 = jr & 7
     const uint16_t* vrow = kbuf + jr * DQK + ((l16 & 1) << 2);
     const int vsw = jr & 7;
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      const int cch = ((cq * (DV / 4) + ct * 16) >> 3) + ((l16 & 3) >> 1);  // chunk of column col0 + 4*(l16&3)
+    for (int ct = 0; ct < CW; ++ct) {
+      const int cch = ((wave * (DV / 8) + ct * 16) >> 3) + ((l16 & 3) >> 1);  // chunk of column col0 + 4*(l16&3)
       const uint16_t* pp = vrow + ((cch ^ vsw) << 3);
       const uint2 v0 = lds_read_tr16(pp);
       const uint2 v1 = two ? lds_read_tr16(pp + HALF_ELEMS) : make_uint2(0u, 0u);
-      o[ct] = mfma_bf16_16x16x32(pa, make_uint4(v0.x, v0.y, v1.x, v1.y), o[ct]);
+      const uint4 vb = make_uint4(v0.x, v0.y, v1.x, v1.y);
+      o[0][ct] = mfma_bf16_16x16x32(pa0, vb, o[0][ct]);
+      o[1][ct] = mfma_bf16_16x16x32(pa1, vb, o[1][ct]);
     }
   }
   DSV41_PH(4);
 
-  // ---- the split's partial: O / l in bf16 in the MFMA's register layout (tile (hb, cq, ct): 64 lanes x 4 heads, one
+  // ---- the split's partial: O / l in bf16 in the MFMA's register layout (tile (b, w, ct): 64 lanes x 4 heads, one
   // 8-byte device-scope store per lane and tile), m (natural-log units) and l per head
   const long pr = pos < 0 ? 0 : pos;
   {
-    float invl[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int hl = 4 * g + i;
-      const float l = ssum[hb][0][hl] + ssum[hb][1][hl] + ssum[hb][2][hl] + ssum[hb][3][hl];
-      invl[i] = l > 0.0f ? 1.0f / l : 0.0f;
-    }
     const long ub = (((long)r * HG + hg) * a.nsplit + sp) * (32L * DV);  // this split's partial (bf16 elements)
     const __amdgpu_buffer_rsrc_t rs = pacc_rsrc(a.pacc);
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      const long off = ub + ((long)((hb * 4 + cq) * CT + ct) * 64 + lane) * 4;
-      __builtin_amdgcn_raw_buffer_store_b64(
-          u32x2_t{pack_bf16x2(o[ct][0] * invl[0], o[ct][1] * invl[1]), pack_bf16x2(o[ct][2] * invl[2], o[ct][3] * invl[3])},
-          rs, (int)(off * 2), 0, kCpolDevice);
+    for (int b = 0; b < 2; ++b) {
+      float invl[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int hl = 4 * g + i;
+        const float l = ssum[b][0][hl] + ssum[b][1][hl] + ssum[b][2][hl] + ssum[b][3][hl];
+        invl[i] = l > 0.0f ? 1.0f / l : 0.0f;
+      }
+#pragma unroll
+      for (int ct = 0; ct < CW; ++ct) {
+        const long off = ub + ((long)((b * 8 + wave) * CW + ct) * 64 + lane) * 4;
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{pack_bf16x2(o[b][ct][0] * invl[0], o[b][ct][1] * invl[1]),
+                                                      pack_bf16x2(o[b][ct][2] * invl[2], o[b][ct][3] * invl[3])},
+                                              rs, (int)(off * 2), 0, kCpolDevice);
+      }
     }
   }
   if (tid < 32 && h0 + tid < H) {
@@ -1766,11 +1784,13 @@ bool use_decode_kernel(int R, int H) { return (long)R * ((H + 63) / 64) < 16; }
 
 template <int DQK, int DV>
 int launch_attn(AttnArgs& a, hipStream_t st) {
-  if (use_decode_kernel(a.R, a.H) && a.dec32) {
-    const int HG2 = (a.H + 31) / 32;
-    attn_decode32_kernel<DQK, DV><<<dim3(kXcds * HG2 * ((a.R * a.nsplit + kXcds - 1) / kXcds)), 512, 0, st>>>(a);
-    DSV41_CHECK_LAUNCH();
-    return 0;
+  if constexpr (DV % 128 == 0) {
+    if (use_decode_kernel(a.R, a.H) && a.dec32) {
+      const int HG2 = (a.H + 31) / 32;
+      attn_decode32_kernel<DQK, DV><<<dim3(kXcds * HG2 * ((a.R * a.nsplit + kXcds - 1) / kXcds)), 512, 0, st>>>(a);
+      DSV41_CHECK_LAUNCH();
+      return 0;
+    }
   }
   if (use_decode_kernel(a.R, a.H)) {
     const int HG = (a.H + 15) / 16;
@@ -1836,12 +1856,12 @@ constexpr int kDecWG = DSV41_DEC_WG;
 
 // Split plan.  Decode kernel: <= 192 workgroups over (rows x 16-head groups x splits), >= 2 tiles of 64 keys per
 // split.  64-head kernel: splits up to one workgroup per CU when rows are few, >= 2 tiles of 32 keys per split.
-// The 32-head decode kernel's plan (automatic split count only): splits of 128 keys (64 when that leaves fewer than
+// The 32-head decode kernel's plan (automatic split count only, DV a multiple of 128): splits of 128 keys (64 when that leaves fewer than
 // 96 workgroups), 8 to 64 of them, every workgroup resident at once (one per CU; the head groups of a (row, split) on one
 // XCD).  DSV41_ATTN_DEC32=0 selects the 16-head kernel instead.  Returns false when it does not apply.
-bool plan_dec32(int R, int H, int L, int* nsplit, int* chunk) {
+bool plan_dec32(int R, int H, int L, int dv, int* nsplit, int* chunk) {
   const char* env = getenv("DSV41_ATTN_DEC32");
-  if ((env && atoi(env) == 0) || !use_decode_kernel(R, H)) return false;
+  if ((env && atoi(env) == 0) || !use_decode_kernel(R, H) || dv % 128) return false;
   const int HG2 = (H + 31) / 32;
   int ch = 128;
   if ((long)R * HG2 * ((L + 127) / 128) < 96) ch = 64;
@@ -1853,8 +1873,8 @@ bool plan_dec32(int R, int H, int L, int* nsplit, int* chunk) {
   return true;
 }
 
-void plan(int R, int H, int L, int want, int* nsplit, int* chunk) {
-  if (want <= 0 && plan_dec32(R, H, L, nsplit, chunk)) return;
+void plan(int R, int H, int L, int want, int dv, int* nsplit, int* chunk) {
+  if (want <= 0 && plan_dec32(R, H, L, dv, nsplit, chunk)) return;
   const bool dec = use_decode_kernel(R, H);
   const int tile = dec ? 64 : 32;
   const int tiles = (L + tile - 1) / tile < 1 ? 1 : (L + tile - 1) / tile;
@@ -1907,7 +1927,7 @@ long workspace_bytes(int R, int H, int ns, int dv) {
 
 int finish_plan(AttnArgs& a, int want_nsplit, void* ws, long ws_bytes, int dv) {
   int ns, chunk;
-  plan(a.R, a.H, a.L, want_nsplit, &ns, &chunk);
+  plan(a.R, a.H, a.L, want_nsplit, dv, &ns, &chunk);
   a.nsplit = ns;
   a.chunk = chunk;
   if (ns > 1) {
@@ -1918,7 +1938,7 @@ int finish_plan(AttnArgs& a, int want_nsplit, void* ws, long ws_bytes, int dv) {
     a.pm = f;
     a.pl = f + (long)a.R * a.H * ns;
     a.pacc = f + 2L * a.R * a.H * ns;
-    if (dec && want_nsplit <= 0 && plan_dec32(a.R, a.H, a.L, &ns, &chunk)) {
+    if (dec && want_nsplit <= 0 && plan_dec32(a.R, a.H, a.L, dv, &ns, &chunk)) {
       a.dec32 = 1;
       a.err = (int*)ws;
       a.coop = (unsigned long long*)((char*)ws + kCounterBase + ((long)a.R * ((a.H + 15) / 16) * 4 + 7) / 8 * 8);
@@ -2020,7 +2040,7 @@ int dsv41_read_wg_attn(long long* host) { return (int)hipMemcpyFromSymbol(host, 
 
 long dsv41_attn_workspace_bytes(int R, int H, int L, int dv, int want_nsplit) {
   int ns, chunk;
-  plan(R, H, L, want_nsplit, &ns, &chunk);
+  plan(R, H, L, want_nsplit, dv, &ns, &chunk);
   return workspace_bytes(R, H, ns, dv);
 }
 

@@ -216,6 +216,8 @@ __device__ long long g_dsv41_px[1024][32];
 // (e.g. direct-to-LDS tile loads still in flight, waited for separately with a counted vmcnt).  __syncthreads()
 // would wait for every outstanding memory operation.  The memory clobber keeps the compiler from moving memory
 // accesses across it.
+// s_waitcnt immediate that waits for vmcnt <= n (n < 64) and nothing else.
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
 DSV41_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // As lds_dma16, with the destination given as a wave-uniform LDS byte address (no generic-to-LDS conversion per
