@@ -557,7 +557,10 @@ def main():
                 "index_select_kernel (scores + top-k, one launch)" if r["one_launch"] else
                 ("decode_appends_kernel + " if r["fused"] else "") +
                 "score kernel with histogram + select kernels (multi-launch)")
-    att_name = ("attn_decode_kernel<576, 512> (splits merged in-kernel)" if R < 16 else
+    dec32 = os.environ.get("DSV41_ATTN_DEC32", "1") != "0"  # the library's default kernel choice for few rows
+    att_name = ("attn_decode32_kernel<576, 512> (32-head workgroups, 128-key splits merged in-kernel)"
+                if R < 16 and dec32 else
+                "attn_decode_kernel<576, 512> (16-head workgroups, splits merged in-kernel)" if R < 16 else
                 "attn_prefill_ws_kernel<576, 512> + attn_decode_combine_kernel (key splits)")
     kernel_names = {"indexer": sel_name, "sattn": att_name}
     roof = {}
