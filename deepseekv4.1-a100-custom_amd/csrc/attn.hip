@@ -677,6 +677,9 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   }
   DSV41_PH(6);
   group_acquire(old, home);
+  // a merger off the home XCD cannot see the home members' partials (plain stores, still in the home L2): the launch
+  // reports it (the dispatch order that places workgroup b on XCD b % 8 did not hold)
+  if (tid == 0 && xcd_id() != home) __hip_atomic_store(a.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   merge_splits<DV>(a, r, h0, pr, wts);
   DSV41_PH(7);

@@ -316,7 +316,8 @@ DSV41_DEV int2 block_scan2_dpp(int v0, int v1, int2* tmp, int2* total) {
 // b % 8), where the shared L2 makes their stores visible to each other once they have left the CU (the CU caches are
 // write-through, and only lines read after the exchange are cached).  Each workgroup checks its hardware XCD id;
 // one that finds itself elsewhere publishes with a device-scope fence and flags the group, and a reader that sees
-// the flag (or is misplaced itself) acquires with a device-scope fence, so results never depend on the placement.
+// the flag acquires with a device-scope fence, so a misplaced writer is still read correctly.  A misplaced reader
+// cannot see the home members' stores (they stay in the home L2): its caller reports that case as an error.
 constexpr int kXcds = 8;
 constexpr int kMisplaced = 1 << 16;  // flag added to a group arrival counter by a misplaced workgroup
 

@@ -92,7 +92,8 @@ CHECK_ERRORS = os.environ.get("DSV41_CHECK_ERRORS", "0") == "1"
 
 _ERR_TEXT = {("index_select", 1): "a row barrier wait gave up (the row's workgroups were not resident together)",
              ("index_select", 2): "a valid count cl exceeded the positions scored (clamped)",
-             ("attention", 1): "a split merge stopped waiting for its unit (workgroups not resident together)"}
+             ("attention", 1): "a split merge stopped waiting for its unit (workgroups not resident together)",
+             ("attention", 2): "a split merge ran off its unit's XCD (workgroups not dealt to the XCDs round-robin)"}
 
 
 def check_error_word(kind: str, word: torch.Tensor) -> None:

@@ -25,8 +25,11 @@ extern "C" {
  * workspace opens with split arrival counters (placed by R and H only): allocate it zeroed once per (R, H); every
  * launch leaves the counters ready for the next, whatever its split count (launches sharing it must be
  * stream-ordered).  Its first int32 is an error word: a decode-kernel launch whose in-launch split merge stopped
- * waiting for the other workgroups of its unit (they were not resident at once) sets it to 1 -- that launch's
- * output is then unreliable; the caller polls and clears it (the Python shims do with DSV41_CHECK_ERRORS=1). */
+ * waiting for the other workgroups of its unit (they were not resident at once) sets it to 1, one whose
+ * last-arrival merge ran off its unit's XCD (workgroups not dealt to the XCDs round-robin) sets it to 2 -- that
+ * launch's output is then unreliable; the caller polls and clears it (the Python shims do with
+ * DSV41_CHECK_ERRORS=1).  DSV41_ATTN_DEC32=0 in the environment selects the 16-head decode kernel over the 32-head
+ * one (query the workspace size under the same setting: a launch given too small a workspace returns an error). */
 long dsv41_attn_workspace_bytes(int R, int H, int L, int dv, int want_nsplit);
 
 /* kernels.sparse_attn (dsv41/kernels.py:172-256) and fused.sparse_attn_decode (dsv41/fused.py:269-280).
