@@ -304,6 +304,9 @@ DSV41_DEV void merge_splits(const AttnArgs& a, int r, int h0, long pr, float (*w
 
 
 constexpr int kCoopSpinLimit = 1 << 20;
+// The cooperative merge's arrival counters (u64) lie 128 bytes apart: device-scope atomics on one cache line
+// serialise at the memory side (a unit's ~17 arrivals and polls then also wait for the other units').
+constexpr int kCoopStride = 16;
 
 // Decode attention, 8 waves per workgroup (2 per SIMD): wave w handles key rows 16*(w&3)..+15 of every 64-key tile
 // and output columns [(w>>2)*DV/2, +DV/2) (QK^T and the softmax are computed by both column halves, identically).
@@ -640,7 +643,7 @@ __global__ void __launch_bounds__(512) attn_decode_kernel(const AttnArgs a) {
   if (a.coop) {
     // ---- every split workgroup of the unit merges a slice once all have published.  Counter = epoch * 256 +
     // arrivals: the last arrival of a launch moves it to the next epoch (any nsplit <= 255, any history)
-    unsigned long long* cnt = a.coop + (long)r * ((H + 15) / 16) + hg;
+    unsigned long long* cnt = a.coop + ((long)r * ((H + 15) / 16) + hg) * kCoopStride;
     __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
     __syncthreads();
     if (tid == 0) {
@@ -1022,7 +1025,7 @@ __global__ void __launch_bounds__(512) attn_decode32_kernel(const AttnArgs a) {
 
   // ---- every split workgroup of the unit merges a slice once all have published.  Counter = epoch * 256 +
   // arrivals: the last arrival of a launch moves it to the next epoch (any nsplit <= 255, any history)
-  unsigned long long* cnt = a.coop + (long)r * HG + hg;
+  unsigned long long* cnt = a.coop + ((long)r * HG + hg) * kCoopStride;
   __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
   __syncthreads();
   if (tid == 0) {
@@ -1918,7 +1921,7 @@ bool fuse_merge(int R, int H, int ns) { (void)R; (void)H; return ns > 1 && ns <=
 constexpr long kCounterBase = 256;
 long counter_bytes(int R, int H) {
   const long units = (long)R * ((H + 15) / 16);
-  return kCounterBase + (units * 4 + 8 + units * 8 + 255) / 256 * 256;  // int counters, pad, u64 counters
+  return kCounterBase + (units * 4 + 8 + units * 8 * kCoopStride + 255) / 256 * 256;  // int counters, pad, u64 counters
 }
 
 long workspace_bytes(int R, int H, int ns, int dv) {
