@@ -55,6 +55,9 @@ constexpr int kIsSpinLimit = 1 << 20;
 
 constexpr int kIsLst = kIsChunk + 4;           // published-list slots per chunk (16-byte aligned lists)
 constexpr int kIsRd = 16;                      // published-list slots read per thread (more: the two-exchange path)
+// Per-chunk count words and flags (u64, written with device-scope stores by one chunk each) lie 128 bytes apart:
+// device-scope writes to one cache line from different CUs serialise at the memory side.
+constexpr int kIsWordStride = 16;
 // 16-byte reads of the published lists with the device-scope cache policy (sc1) of the atomics that wrote them
 typedef unsigned is_u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kIsCpolDevice = 16;
@@ -264,8 +267,8 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   // return in order) would wait for it too
   uint32_t epoch = 0, tag = 0;
   auto read_epoch = [&]() {
-    epoch = (uint32_t)(__hip_atomic_load(g.cnt + (long)r * ns + ch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >>
-                       32) + 1;
+    epoch = (uint32_t)(__hip_atomic_load(g.cnt + ((long)r * ns + ch) * kIsWordStride, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) >> 32) + 1;
     tag = epoch & ((1u << (32 - kIsTagShift)) - 1);
   };
   const int c = (int)(clr < 0 ? 0 : (clr > a.n_pos ? a.n_pos : clr)), k = g.k;
@@ -436,7 +439,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   DSV41_PH(1);
   DSV41_TS(54);
   int* gh = g.hist + (long)r * kHistBins;
-  unsigned long long* rcnt = g.cnt + (long)r * ns;
+  unsigned long long* rcnt = g.cnt + (long)r * ns * kIsWordStride;
   int* oidx = g.idx + (long)r * g.idx_rstride;
   if (!sel) {  // everything is selected: no exchange (every chunk of the row takes this branch); epoch advances
     if (ch == 0) {
@@ -444,7 +447,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
       for (int i = t; i < k; i += kIsThreads) oidx[i] = i < c ? i + g.offset : -1;
     }
     if (t == 0)
-      __hip_atomic_store(rcnt + ch, (unsigned long long)epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(rcnt + ch * kIsWordStride, (unsigned long long)epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   // ---- one-exchange selection.  Each chunk publishes the keys at or above a cut that keeps at least pub_m of its
@@ -519,9 +522,9 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     // the flag goes out after this workgroup's list has landed: a reader that sees this epoch finds the list
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    unsigned long long* const frow = g.fl + (long)r * ns;
+    unsigned long long* const frow = g.fl + (long)r * ns * kIsWordStride;
     if (t == 0)
-      __hip_atomic_store(frow + ch, (unsigned long long)epoch << 32 | (uint32_t)npub, __ATOMIC_RELAXED,
+      __hip_atomic_store(frow + ch * kIsWordStride, (unsigned long long)epoch << 32 | (uint32_t)npub, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     DSV41_PH(2);
     DSV41_PX(14);
@@ -532,7 +535,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
       unsigned long long fv = 0ull;
 #pragma unroll 1
       for (int spins = 0;; ++spins) {
-        if (t < ns) fv = __hip_atomic_load(frow + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t < ns) fv = __hip_atomic_load(frow + t * kIsWordStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (__syncthreads_and(t >= ns || (uint32_t)(fv >> 32) == epoch)) break;
         if (spins >= kIsSpinLimit) {
           if (t == 0) __hip_atomic_store(g.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -647,7 +650,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
       DSV41_PX(21);
       if (take) oidx[tot2.x + ex2.y] = pp + g.offset;
       if (t == 0)  // (the next launch's epoch)
-        __hip_atomic_store(rcnt + ch, (unsigned long long)epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(rcnt + ch * kIsWordStride, (unsigned long long)epoch << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       DSV41_PH(7);
 #ifdef DSV41_TIMING
       if (t == 0 && blockIdx.x < 1024) g_is_spins[blockIdx.x][1] = -1;  // took the one-exchange path
@@ -768,7 +771,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     unsigned ta = 0, tc = 0;
 #pragma unroll
     for (int w = 0; w < 8; ++w) ta += wcnt[w][0], tc += wcnt[w][1];
-    __hip_atomic_store(rcnt + ch, (unsigned long long)epoch << 32 | tc << 16 | ta, __ATOMIC_RELAXED,
+    __hip_atomic_store(rcnt + ch * kIsWordStride, (unsigned long long)epoch << 32 | tc << 16 | ta, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   }
   // ---- D. counts of all chunks + speculative candidate prefixes, read until every count word carries this epoch
@@ -782,7 +785,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
 #pragma unroll 1
     while (true) {
       unsigned long long cv = 0ull;
-      if (t < ns) cv = __hip_atomic_load(rcnt + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (t < ns) cv = __hip_atomic_load(rcnt + t * kIsWordStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
       for (int u = 0; u < kSpecPer; ++u) {
         const int id = u * kIsThreads + t, q = id / kIsSpec, e = id % kIsSpec;
@@ -1103,8 +1106,8 @@ int dsv41_read_ts_is(long long* host) { return (int)hipMemcpyFromSymbol(host, HI
 
 long dsv41_index_select_workspace_bytes(int R, int n_pos) {
   const long ns = is_slots(n_pos);
-  return (long)R * kHistBins * 4 + (long)R * ns * 8 + (long)R * ns * kIsChunk * 8 + (long)R * ns * 8 +
-         (long)R * ns * 8 + 16 + (long)R * ns * kIsLst * 4 + 16;
+  return (long)R * kHistBins * 4 + (long)R * ns * 8 * kIsWordStride + (long)R * ns * kIsChunk * 8 +
+         (long)R * ns * 8 + (long)R * ns * 8 * kIsWordStride + 16 + (long)R * ns * kIsLst * 4 + 16;
 }
 
 }  // extern "C"
@@ -1150,10 +1153,10 @@ int select_setup(IsArgs& g, const void* q8, long q_rstride, const float* wf, lon
   char* w = (char*)ws;
   g.hist = (int*)w;
   g.cnt = (unsigned long long*)(w + (long)R * kHistBins * 4);
-  g.cand = g.cnt + (long)R * ns;
+  g.cand = g.cnt + (long)R * ns * kIsWordStride;
   g.pub = g.cand + (long)R * ns * kIsChunk;                       // [R] u64 (in a spare [R, nslots] u64 region)
   g.fl = g.pub + (long)R * ns;
-  g.lst = (uint32_t*)(((uintptr_t)(g.fl + (long)R * ns) + 15) & ~(uintptr_t)15);  // (16-byte list reads)
+  g.lst = (uint32_t*)(((uintptr_t)(g.fl + (long)R * ns * kIsWordStride) + 15) & ~(uintptr_t)15);  // (16-byte reads)
   g.err = (int*)(w + dsv41_index_select_workspace_bytes(R, n_pos) - 16);
   // published keys per chunk on the one-exchange path: 1.5 times a chunk's share of k, plus 8 (a chunk holding
   // more of the selection than it published sends the row to the two-exchange path); DSV41_IS_PUB_M overrides it
