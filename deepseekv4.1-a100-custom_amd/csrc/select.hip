@@ -564,6 +564,10 @@ struct GroupArgs {
   int rpx;                    // rows per XCD
 };
 
+// The rows' arrival counters (u64) lie 128 bytes apart: device-scope atomics on one cache line serialise at the
+// memory side.
+constexpr int kEpochStride = 16;
+
 __global__ void __launch_bounds__(256) select_group_kernel(const GroupArgs g) {
   const SelArgs& a = g.s;
   const int home = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
@@ -590,7 +594,7 @@ __global__ void __launch_bounds__(256) select_group_kernel(const GroupArgs g) {
   for (int u = 0; u < 4; ++u) h4[u] = *(const int4*)(gh + kBins - 16 * (t + 1) + 4 * u);
   const int c = (int)(cl < 0 ? 0 : (cl > a.n ? a.n : cl)), k = a.k;
   int* orow = a.out + (long)r * a.out_rstride;
-  unsigned long long* ep = g.epoch + r;
+  unsigned long long* ep = g.epoch + (long)r * kEpochStride;
   const int zb = (kBins + nslots - 1) / nslots, z0 = ch * zb, z1 = min(kBins, z0 + zb);  // histogram slice to clear
   if (c <= k) {  // everything is selected; arrive without waiting (keeps the epoch count)
     if (ch == 0) {
@@ -788,7 +792,7 @@ int dsv41_read_ck_sel(long long* host) { return (int)hipMemcpyFromSymbol(host, H
 #endif
 
 long dsv41_select_workspace_bytes(int R, int n) {
-  return select_base_bytes(R, n) + (R + 2L) * 8;  // + per-row arrival counters, timeout flag
+  return select_base_bytes(R, n) + (R * (long)kEpochStride + 2L) * 8;  // + per-row arrival counters, timeout flag
 }
 
 int dsv41_select_topk(const float* score, long ld, int R, int n, int k, const long* cl, int offset, void* ws,
@@ -822,7 +826,7 @@ int dsv41_select_topk(const float* score, long ld, int R, int n, int k, const lo
     GroupArgs g{a, (unsigned long long*)a.above, nullptr, nullptr, rpx};
     unsigned long long* ctl = (unsigned long long*)((char*)ws + select_base_bytes(R, n));
     g.epoch = ctl;
-    g.err = (int*)(ctl + R);
+    g.err = (int*)(ctl + (long)R * kEpochStride);
     select_group_kernel<<<kXcds * rpx * nch, 256, 0, st>>>(g);
     DSV41_CHECK_LAUNCH();
     return 0;
