@@ -720,12 +720,14 @@ DSV41_DEV void merge_tiles32(const AttnArgs& a, int r, int hg, int HG, long pr, 
   const bool act = ti < (int)((long)(sp + 1) * NT / ns);  // wave-uniform
   const __amdgpu_buffer_rsrc_t rs = pacc_rsrc(a.pacc);
   const long ub0 = ((long)r * HG + hg) * ns * (32L * DV) + ((long)ti * 64 + lane) * 4;  // split 0's entry of the lane
-  auto load_batch = [&](int s0, uint2 (&v)[MS]) {
+  auto load_batch = [&](int s0, uint2 (&v)[MS]) {  // (only the batch's splits: each load costs issue time)
 #pragma unroll
     for (int u = 0; u < MS; ++u) {
-      const int s = s0 + u < ns ? s0 + u : ns - 1;
-      const auto x = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)((ub0 + (long)s * (32L * DV)) * 2), 0, kCpolDevice);
-      v[u] = make_uint2(x[0], x[1]);
+      if (s0 + u < ns) {  // wave-uniform
+        const auto x = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)((ub0 + (long)(s0 + u) * (32L * DV)) * 2), 0,
+                                                            kCpolDevice);
+        v[u] = make_uint2(x[0], x[1]);
+      }
     }
   };
   uint2 v[MS];
