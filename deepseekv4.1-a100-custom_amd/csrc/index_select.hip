@@ -3,7 +3,8 @@
 // score[r, 0..cl) in ascending index order with -1 padding as dsv41/fused3.py:65-75, ties lowest index first).
 //
 // Grid: R x nslots workgroups of 512 threads (chunk ch of row r is workgroup ch * R + r, so a row's chunks spread
-// over the XCDs; FUSED: 3 R append workgroups first), all resident at once (at most kIsMaxWG: 2 per CU).  Each
+// over the XCDs), all resident at once (at most kIsMaxWG: 2 per CU).  FUSED: chunk workgroups also do the step's
+// cache appends while their key loads are in flight (the chunk holding the new key's position scores it itself).  Each
 // workgroup scores its 512 positions (8 waves x 64 keys, every key load issued up front, e4m3 keys against the
 // prepared e4m3 queries, fp8 MFMA) and keeps them in LDS.  Then, on the one-exchange path (pub_m > 0):
 //   P. publishes the keys at or above a cut that keeps at least pub_m of its positions (4096 bins over its own key
@@ -146,6 +147,34 @@ DSV41_DEV RowOp is_app_op(const IsAppend& ap, int r, long slot, long ppos, int w
   return o;
 }
 
+// The index-key append of a step that closes a group, to table row `row` (= compress_len - 1), with the LDS copy.
+DSV41_DEV RowOp is_key_op(const IsAppend& ap, int r, long slot, long ppos, long row, uint8_t* knew, float* ksnew) {
+  RowOp o{};
+  o.cos_t = ap.cos_t;
+  o.sin_t = ap.sin_t;
+  o.rd = ap.rd;
+  o.eps = ap.eps;
+  o.x = ap.k_raw + (long)r * 128;
+  o.D = 128;
+  o.norm_w = ap.k_norm;
+  o.pos = ppos + 1 - ap.ratio;
+  o.qmode = 1;
+  o.group = 32;
+  o.out = ap.kbf ? ap.kbf + slot * ap.kbf_sstride + row * 128L : nullptr;
+  o.k8 = ap.k8 + slot * ap.k8_sstride + row * 128L;
+  o.ks = ap.ks + slot * ap.ks_sstride + row;
+  o.k8_lds = knew;
+  o.ks_lds = ksnew;
+  return o;
+}
+
+// The appends in bit set `late` of row r (bit w: is_app_op's operation w), one after another (whole-block barriers).
+DSV41_DEV void is_late_appends(const IsAppend& ap, int r, long slot, long ppos, int late, float* red) {
+  if (late & 1) row_op<512>(is_app_op(ap, r, slot, ppos, 0, nullptr, nullptr), red);
+  if (late & 2) row_op<512>(is_app_op(ap, r, slot, ppos, 1, nullptr, nullptr), red);
+  if (late & 4) row_op<512>(is_app_op(ap, r, slot, ppos, 2, nullptr, nullptr), red);
+}
+
 // Largest u32 over the 64 lanes of a wave, in every lane: DPP lane moves as wave_incl_scan (lanes a move does not
 // reach keep their own value), then lane 63's result.
 DSV41_DEV uint32_t wave_umax(uint32_t x) {
@@ -210,7 +239,6 @@ struct IsArgs {
   unsigned long long* cnt;    // [R, nslots]: epoch << 32 | candidates << 16 | above
   unsigned long long* cand;   // [R, nslots * kIsChunk]
   int* err;
-  unsigned long long* pub;    // (FUSED) [R]: epoch << 32 | the score of the row's new key (its append workgroup's)
   IsAppend app;               // FUSED instances only
   // one-exchange selection (pub_m > 0): every chunk publishes its top entries (at least pub_m of the chunk's keys)
   int pub_m;
@@ -229,11 +257,8 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   static_assert(MAXC <= kIsThreads && MAXC % 64 == 0, "one thread per chunk");
   const ScoreArgs& a = g.s;
   const int R = a.R, ns = g.nslots;
-  // (FUSED) the 3 R append-only workgroups come first in the grid: the new key's score, which its row's selection
-  // waits for, is then computed from the launch's start
-  const bool extra = FUSED && (int)blockIdx.x < 3 * R;
-  const int bx = FUSED ? (extra ? (int)blockIdx.x : (int)blockIdx.x - 3 * R) : (int)blockIdx.x;
-  const int r = extra ? bx / 3 : bx % R, ch = extra ? 0 : bx / R;
+  const int bx = (int)blockIdx.x;
+  const int r = bx % R, ch = bx / R;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
   __shared__ int lhist[kHistBins];
@@ -259,7 +284,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   // (FUSED) the row's queries first, in flight with the row data: issued after the key loads instead, they were
   // waited for before the key addresses could reuse their address registers
   if constexpr (FUSED)
-    if (!extra) qprep512_load(g.app.q_idx + (long)r * a.HI * 128, g.app.w_idx + (long)r * a.HI, a.HI, qp);
+    qprep512_load(g.app.q_idx + (long)r * a.HI * 128, g.app.w_idx + (long)r * a.HI, a.HI, qp);
   const long clr = row_cl(a, r);
   const long slot = a.seq ? a.seq[r] : (long)(r / a.rows_per_slot);
   // this launch's epoch: one more than the one this chunk's count word holds (earlier launches have completed).
@@ -267,86 +292,41 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   // return in order) would wait for it too
   uint32_t epoch = 0, tag = 0;
   auto read_epoch = [&]() {
-    epoch = (uint32_t)(__hip_atomic_load(g.cnt + ((long)r * ns + ch) * kIsWordStride, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT) >> 32) + 1;
+    // (the high word alone: a 64-bit load whose low half is dead lets the compiler reuse that register, which
+    // then waits for the load -- the last one issued, so for every key load)
+    epoch = __hip_atomic_load((const uint32_t*)(g.cnt + ((long)r * ns + ch) * kIsWordStride) + 1, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT) + 1;
     tag = epoch & ((1u << (32 - kIsTagShift)) - 1);
   };
   const int c = (int)(clr < 0 ? 0 : (clr > a.n_pos ? a.n_pos : clr)), k = g.k;
-  if (clr > a.n_pos && ch == 0 && t == 0)  // positions beyond n_pos were promised never to be valid
-    __hip_atomic_store(g.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int nht = (a.HI + 15) / 16;
   i32x8_t qa8[kHT];
   uint4 qa16[kHT][4];  // (bf16 queries: unused here)
   float wl[kHT];
-  // FUSED: the ring row, the compressed row and the index key are written by 3 append-only workgroups per row after
-  // the row grid; a row whose group closes gets its new key at position cl - 1: its append workgroup also scores it
-  // (the same MFMA tile as the chunks', so the same bits), adds it to the row histogram and publishes the score with
-  // this launch's epoch; the chunk holding the position skips it (its table row is read before it is written) and
-  // takes the published score with the histogram (the row barrier covers the entry)
+  // FUSED: the step's cache appends are done by chunk workgroups.  When the step closes a group, the chunk holding
+  // the new key's position writes the key with one wave while its key loads are in flight (its operands loaded
+  // before them, so waiting for those does not wait for the keys; every chunk issues those few loads, so that no
+  // branch holds them) and scores it from its LDS copy in place of the table row its
+  // loads read.  The ring row (chunk 0), the compressed row (chunk 1) and a non-closing step's key (chunk 2, to the
+  // no-write row) are nothing this launch reads: they are written while the chunk waits at the row barrier (a row
+  // of fewer chunks gives several to one).
   const IsAppend& ap = g.app;
   long ppos = 0, knew_row = -1;
   bool holder = false;  // (FUSED) this chunk holds the new key's position
-  auto make_op = [&](int which) { return is_app_op(ap, r, slot, ppos, which, knew, &ksnew); };
+  int late = 0;         // (FUSED) bit w: append w (0 ring, 1 compressed row, 2 index key) is this chunk's, written late
+  RowRegs<64, 128> rr;  // (FUSED) the key's operands: one wave's share of a 128-wide row
+  RowOp kop{};
   if constexpr (FUSED) {
     ppos = ap.pos[r];
     const bool closes = ((ppos + 1) % ap.ratio) == 0;
     if (closes) knew_row = (ppos + 1) / ap.ratio - 1;
-    if (extra) {  // the ring row, the compressed row or the index-key row; then done
-      read_epoch();
-      const int which = bx % 3;
-      if (which == 1 && !(ap.latent && ap.ckv)) return;
-      if (which == 0) {  // (constant operation indices: the row operation's fields stay in registers)
-        row_op<kIsThreads>(make_op(0), redf);
-        return;
-      }
-      if (which == 1) {
-        row_op<kIsThreads>(make_op(1), redf);
-        return;
-      }
-      if (!closes) {
-        row_op<kIsThreads>(make_op(2), redf);
-        return;
-      }
-      qprep512_load(ap.q_idx + (long)r * a.HI * 128, ap.w_idx + (long)r * a.HI, a.HI, qp);
-      row_op<kIsThreads>(make_op(2), redf);  // the key row, into the table and knew / ksnew
-      qprep512_store(qp, a.HI, qs, wfl);
-      __syncthreads();
-      if (wave == 0) {
-        // column 0 of the tile holds the key (lanes with l16 = 0: bytes 32 g4 .. +32), the others zero
-        const uint4 z = make_uint4(0, 0, 0, 0);
-        const uint4 k0n = l16 == 0 ? *(const uint4*)(knew + g4 * 32) : z;
-        const uint4 k1n = l16 == 0 ? *(const uint4*)(knew + g4 * 32 + 16) : z;
-        float wr[kHT][4];
-#pragma unroll
-        for (int ht = 0; ht < kHT; ++ht) {
-          const int h = ht * 16 + l16;
-          const int hc = ht < nht && h < a.HI ? h : 0;
-          const uint4 u0 = *(const uint4*)(qs + hc * 128 + g4 * 32), u1 = *(const uint4*)(qs + hc * 128 + g4 * 32 + 16);
-          qa8[ht] = i32x8_t{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
-          wl[ht] = ht < nht && h < a.HI ? wfl[h] : 0.0f;
-        }
-#pragma unroll
-        for (int ht = 0; ht < kHT; ++ht)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) wr[ht][i] = __shfl(wl[ht], 4 * g4 + i, 64);
-        const float sum = score_tile<1>(qa8, qa16, wr, nht, k0n, k1n, nullptr);
-        if (lane == 0 && knew_row < c) {
-          const float v = is_cand(a, r, knew_row) ? sum * ksnew : -__builtin_inff();
-          if (a.out && knew_row < a.n_pos) a.out[(long)r * a.out_rstride + knew_row] = v;
-          if (c > k) {  // (otherwise nobody reads the histogram or the score)
-            DSV41_PH(1);
-            // (one-exchange path: the chunk holding the position adds it to its own counts, even when it falls back)
-            if (g.pub_m == 0)
-              __hip_atomic_fetch_add(g.hist + (long)r * kHistBins + (score_key(v) >> 20), 1, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(g.pub + r, (unsigned long long)epoch << 32 | __float_as_uint(v), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      }
-      return;
-    }
     holder = closes && knew_row >= 0 && knew_row < c && ch == (int)(knew_row / kIsChunk);
+    late = (ch == 0 ? 1 : 0) | (ch == min(1, ns - 1) && ap.latent && ap.ckv ? 2 : 0);
+    if (!(closes && knew_row >= 0 && knew_row < c) && ch == min(2, ns - 1)) late |= 4;
+    // (every chunk loads the key's operands -- valid addresses whether or not the step closes a group --, so no
+    // branch holds the loads; only the holder uses them)
+    kop = is_key_op(ap, r, slot, ppos, knew_row < 0 ? 0 : knew_row, knew, &ksnew);
+    row_load<64, 128>(kop, rr);
   } else {
     // the row's queries (64 heads x 128 e4m3 = 512 chunks of 16 bytes) go to LDS once, one direct load per thread
     // (every wave needs all of them); heads >= HI are never read back
@@ -379,12 +359,19 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     ksc[nt] = a.kscale[slot * a.ks_sstride + pl];
   }
   read_epoch();
+  // (stored after the row's loads are issued: a global store before them makes the compiler load the row data
+  // through the vector path and wait for every earlier load)
+  if (clr > a.n_pos && ch == 0 && t == 0)  // positions beyond n_pos were promised never to be valid
+    __hip_atomic_store(g.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   DSV41_TS(50);
   DSV41_PX(2);
   if constexpr (FUSED) {
     DSV41_PX(4);
     qprep512_store(qp, a.HI, qs, wfl);
-    lds_barrier();  // queries and weights staged
+    // the new key by one wave (no barriers: a whole-block row operation's chain of barriers held every wave of the
+    // holder up); the others go on to wait for their key loads
+    if (holder && wave == 0) row_compute<64, true, 128>(kop, rr, redf);
+    lds_barrier();  // queries and weights staged (and the new key's LDS copy)
     DSV41_PX(5);
 #pragma unroll
     for (int ht = 0; ht < kHT; ++ht) {
@@ -412,20 +399,22 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int p = pw + nt * 16 + l16;
+    if (FUSED && holder && p == knew_row) {  // the new key: this launch's LDS copy, not the table row loaded
+      k0[nt] = *(const uint4*)(knew + g4 * 32);
+      k1[nt] = *(const uint4*)(knew + g4 * 32 + 16);
+      ksc[nt] = ksnew;
+    }
     const float sum = score_tile<1>(qa8, qa16, wr, nht, k0[nt], k1[nt], nullptr);
     if (g4 == 0) {
       const float v = p < c ? (is_cand(a, r, p) ? sum * ksc[nt] : -__builtin_inff()) : 0.0f;
       sc[p - ch * kIsChunk] = v;
-      if (p < c && !(FUSED && holder && p == knew_row)) {
+      if (p < c) {
         const uint32_t kv = score_key(v);
         kmax = max(kmax, kv);
         kmin_c = max(kmin_c, ~kv);
       }
-      // (FUSED: the new key's position is its append workgroup's: scored, counted and written there)
-      if (!(FUSED && holder && p == knew_row)) {
-        if (p < c && sel && g.pub_m == 0) atomicAdd(&lhist[score_key(v) >> 20], 1);
-        if (orow && p < a.n_pos) orow[p] = p < c ? v : -__builtin_inff();
-      }
+      if (p < c && sel && g.pub_m == 0) atomicAdd(&lhist[score_key(v) >> 20], 1);
+      if (orow && p < a.n_pos) orow[p] = p < c ? v : -__builtin_inff();
     }
   }
   DSV41_TS(53);
@@ -442,6 +431,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   unsigned long long* rcnt = g.cnt + (long)r * ns * kIsWordStride;
   int* oidx = g.idx + (long)r * g.idx_rstride;
   if (!sel) {  // everything is selected: no exchange (every chunk of the row takes this branch); epoch advances
+    if (FUSED && late) is_late_appends(ap, r, slot, ppos, late, redf);
     if (ch == 0) {
 #pragma unroll 1
       for (int i = t; i < k; i += kIsThreads) oidx[i] = i < c ? i + g.offset : -1;
@@ -462,25 +452,6 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
   if (g.pub_m > 0) {
     static_assert(kIsPer == 1, "one position per thread");
     DSV41_PX(10);
-    if constexpr (FUSED) {
-      if (holder) {  // the new key's score comes from its append workgroup
-        if (t == 0) {
-          unsigned long long pv = 0ull;
-#pragma unroll 1
-          for (int sp = 0;; ++sp) {
-            pv = __hip_atomic_load(g.pub + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if ((uint32_t)(pv >> 32) == epoch) break;
-            if (sp >= kIsSpinLimit) {
-              __hip_atomic_store(g.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-          }
-          sc[knew_row - ch * kIsChunk] = __uint_as_float((uint32_t)pv);
-        }
-        __syncthreads();
-      }
-    }
     const int pp = ch * kIsChunk + t;
     const bool valid = pp < c;
     const uint32_t kk = valid ? score_key(sc[t]) : 0u;
@@ -490,11 +461,6 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
       uint32_t mx = 0u, nmn = 0u;  // the largest key and the complement of the smallest (the scoring loop's)
 #pragma unroll
       for (int w = 0; w < 8; ++w) mx = max(mx, ured[w]), nmn = max(nmn, ured[8 + w]);
-      if (FUSED && holder) {  // (the new key's score arrived after the scoring loop)
-        const uint32_t kn = score_key(sc[knew_row - ch * kIsChunk]);
-        mx = max(mx, kn);
-        nmn = max(nmn, ~kn);
-      }
       const int sh = bin_shift(mx - ~nmn);
       DSV41_PX(11);
       if (valid) atomicAdd(&lhist[(mx - kk) >> sh], 1);  // bin 0: the chunk's largest key (lhist is zero here)
@@ -528,6 +494,10 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
                          __HIP_MEMORY_SCOPE_AGENT);
     DSV41_PH(2);
     DSV41_PX(14);
+    if (FUSED && late) {  // (while the row's other chunks publish)
+      is_late_appends(ap, r, slot, ppos, late, redf);
+      late = 0;
+    }
 #pragma unroll
     for (int j = 0; j < kHistBins / kIsThreads; ++j) lhist[t + j * kIsThreads] = 0;  // (read after the barriers below)
     if (t == 0) s_m1 = 0, s_tie = 1;
@@ -669,6 +639,7 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     const uint32_t lo = (uint32_t)lhist[2 * i], hi = (uint32_t)lhist[2 * i + 1];
     if (lo | hi) atomicAdd((unsigned long long*)(gh + 2 * i), ((unsigned long long)hi << 32) | lo);
   }
+  if (FUSED && late) is_late_appends(ap, r, slot, ppos, late, redf);  // (while the row's other chunks add theirs)
   // ---- B. the row histogram once it holds all c valid positions (row barrier and data in one read), threshold bin
   DSV41_PH(2);
   if (t == 0) {
@@ -680,7 +651,6 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
     constexpr int BP = kHistBins / kIsThreads;  // bins per thread: 4095 - BP*t (h[0]) down to 4096 - BP*(t+1)
     int h[BP];
     int local, total, above, spins = 0;
-    unsigned long long pubv = 0ull;  // (FUSED holder) the new key's published score, read with the histogram
 #pragma unroll 1
     while (true) {
 #pragma unroll
@@ -690,7 +660,6 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
         h[BP - 1 - 2 * u] = (int)(v & 0xffffffffu);
         h[BP - 2 - 2 * u] = (int)(v >> 32);
       }
-      if (FUSED && holder && t == 0) pubv = __hip_atomic_load(g.pub + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       local = 0;
 #pragma unroll
       for (int i = 0; i < BP; ++i) local += h[i];
@@ -706,19 +675,6 @@ __global__ void __launch_bounds__(kIsThreads, 4) index_select_kernel(const IsArg
 #ifdef DSV41_TIMING
     if (t == 0 && blockIdx.x < 1024) g_is_spins[blockIdx.x][0] = spins;
 #endif
-    if (FUSED && holder && t == 0) {
-      // the score is published right after its histogram entry: wait for this launch's epoch on it
-#pragma unroll 1
-      for (int sp2 = 0; (uint32_t)(pubv >> 32) != epoch; ++sp2) {
-        if (sp2 >= kIsSpinLimit) {
-          __hip_atomic_store(g.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-        pubv = __hip_atomic_load(g.pub + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      sc[knew_row - ch * kIsChunk] = __uint_as_float((uint32_t)pubv);
-    }
     if (above < k && k <= above + local) {
 #pragma unroll 1
       for (int i = 0; i < BP; ++i) {
@@ -1154,8 +1110,7 @@ int select_setup(IsArgs& g, const void* q8, long q_rstride, const float* wf, lon
   g.hist = (int*)w;
   g.cnt = (unsigned long long*)(w + (long)R * kHistBins * 4);
   g.cand = g.cnt + (long)R * ns * kIsWordStride;
-  g.pub = g.cand + (long)R * ns * kIsChunk;                       // [R] u64 (in a spare [R, nslots] u64 region)
-  g.fl = g.pub + (long)R * ns;
+  g.fl = g.cand + (long)R * ns * kIsChunk + (long)R * ns;  // (after a spare [R, nslots] u64 region)
   g.lst = (uint32_t*)(((uintptr_t)(g.fl + (long)R * ns * kIsWordStride) + 15) & ~(uintptr_t)15);  // (16-byte reads)
   g.err = (int*)(w + dsv41_index_select_workspace_bytes(R, n_pos) - 16);
   // published keys per chunk on the one-exchange path: 1.5 times a chunk's share of k, plus 8 (a chunk holding
@@ -1168,7 +1123,7 @@ int select_setup(IsArgs& g, const void* q8, long q_rstride, const float* wf, lon
 
 template <bool FUSED>
 int select_launch(const IsArgs& g, hipStream_t st) {
-  const int grid = g.s.R * g.nslots + (FUSED ? 3 * g.s.R : 0);  // (FUSED: the append-only workgroups first)
+  const int grid = g.s.R * g.nslots;
   if (g.nslots <= 128)
     index_select_kernel<128, FUSED><<<grid, kIsThreads, 0, st>>>(g);
   else

@@ -85,27 +85,40 @@ struct RowOp {
 // The operands of one row operation, loaded ahead of its arithmetic (row_load, then row_compute), for rows of up to
 // MAXD elements.  The NT threads doing a row operation are a whole block, or (NT = 64) one wave of a larger block;
 // element e lives in thread e % NT of the group.
+// (the bf16 operands are held as loaded and converted in row_compute: a conversion next to the load would make the
+// compiler wait for it there, before any loads issued after row_load)
 template <int NT, int MAXD = kRowMaxD>
 struct RowRegs {
   static constexpr int IT = MAXD / NT;
-  float v[IT], w[IT], cs[IT], sn[IT];
+  uint32_t vb[IT], wb[IT];
+  float cs[IT], sn[IT];
 };
 
+// Stand-ins read by row_load in place of a missing norm weight (bf16 1.0) or rope table.
+__device__ uint16_t g_row_one_bf16 = 0x3f80u;
+__device__ float g_row_zero_f32 = 0.0f;
+
+// Every operand load is unconditional (absent operands read a stand-in, columns are clamped): a load under a
+// condition would make the compiler wait for it where the branches merge, before any load issued after row_load.
 template <int NT, int MAXD = kRowMaxD>
 DSV41_DEV void row_load(const RowOp& o, RowRegs<NT, MAXD>& g) {
   const int t = threadIdx.x & (NT - 1);
   const int p = o.pos < 0 ? 0 : (int)o.pos;
+  const bool nw = o.norm_w != nullptr, rp = o.rd > 0;
+  const uint16_t* const wp = nw ? o.norm_w : &g_row_one_bf16;
+  const float* const cp = rp ? o.cos_t : &g_row_zero_f32;
+  const float* const sp = rp ? o.sin_t : &g_row_zero_f32;
 #pragma unroll
   for (int u = 0; u < RowRegs<NT, MAXD>::IT; ++u) {
     const int e = t + u * NT;
     const int ec = e < o.D ? e : 0;
-    g.v[u] = bf2f(o.x[ec]);
-    g.w[u] = o.norm_w ? bf2f(o.norm_w[ec]) : 1.0f;
-    const int j = (ec - (o.D - o.rd)) >> 1;
-    const bool rope = o.rd > 0 && e < o.D && e >= o.D - o.rd;
-    g.cs[u] = rope ? o.cos_t[(long)p * (o.rd / 2) + j] : 1.0f;
-    g.sn[u] = rope ? o.sin_t[(long)p * (o.rd / 2) + j] : 0.0f;
-    if (e >= o.D) g.v[u] = 0.0f;
+    g.vb[u] = o.x[ec];  // (elements e >= D are zeroed in row_compute)
+    g.wb[u] = wp[nw ? ec : 0];
+    // (elements outside the rope columns never use cs / sn)
+    const bool rope = e < o.D && e >= o.D - o.rd;
+    const long j = rp && rope ? (long)p * (o.rd / 2) + ((ec - (o.D - o.rd)) >> 1) : 0;
+    g.cs[u] = cp[j];
+    g.sn[u] = sp[j];
   }
 }
 
@@ -114,7 +127,9 @@ template <int NT, bool LB = false, int MAXD = kRowMaxD>
 DSV41_DEV void row_compute(const RowOp& o, RowRegs<NT, MAXD>& g, float* red) {
   constexpr int IT = RowRegs<NT, MAXD>::IT;
   const int t = threadIdx.x & (NT - 1);
-  float* v = g.v;
+  float v[IT];
+#pragma unroll
+  for (int u = 0; u < IT; ++u) v[u] = t + u * NT < o.D ? bf2f((uint16_t)g.vb[u]) : 0.0f;
   if (o.norm_w) {
     float ss = 0.0f;
 #pragma unroll
@@ -122,7 +137,7 @@ DSV41_DEV void row_compute(const RowOp& o, RowRegs<NT, MAXD>& g, float* red) {
     ss = block_sum<NT, LB>(ss, red);
     const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)o.D) + o.eps));
 #pragma unroll
-    for (int u = 0; u < IT; ++u) v[u] = round_bf16(v[u] * inv * g.w[u]);
+    for (int u = 0; u < IT; ++u) v[u] = round_bf16(v[u] * inv * bf2f((uint16_t)g.wb[u]));
   }
 #pragma unroll
   for (int u = 0; u < IT; ++u) {
