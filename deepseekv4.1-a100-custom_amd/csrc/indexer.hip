@@ -291,6 +291,7 @@ constexpr int kGRows = 6;                          // rows per group
 constexpr int kGSplit = 2;                         // waves per row (each scores a 1/kGSplit slice of the chunk)
 constexpr int kGThreads = 64 * kGRows * kGSplit;   // 12 waves: three per SIMD
 constexpr int kGFlushItems = 255;  // chunks counted into the 16-bit bins between flushes
+constexpr int kGItemCost = 20, kGStartCost = 13;  // a run's cost per item and per group it starts (~3.1 / ~2 us)
 
 __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const ScoreArgs a) {
   __shared__ __align__(16) uint8_t kbuf[2][kPChunk * 128];
@@ -298,6 +299,7 @@ __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const S
   __shared__ uint32_t gh[kGRows][kHistBins / 2];
   __shared__ int gstart[kLoopMaxRows + 1];  // group g: rows [gstart[g], gstart[g + 1])
   __shared__ int gpre[kLoopMaxRows + 1];    // items of this XCD in groups < g
+  __shared__ int gwpre[kLoopMaxRows + 1];   // their cost (kGItemCost per item + kGStartCost per group started)
   __shared__ int glim[kLoopMaxRows];        // longest valid count of group g (clamped to n_pos)
   __shared__ long gslot[kLoopMaxRows];
   __shared__ int rlim[kLoopMaxRows];
@@ -354,13 +356,26 @@ __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const S
       cnt = nx > x ? (nx - x + kXcds - 1) / kXcds : 0;
     }
     const int inc = wave_incl_scan(cnt);
-    if (lane < G) gpre[lane + 1] = inc;
-    if (lane == 0) gpre[0] = 0;
+    const int winc = wave_incl_scan(cnt > 0 ? cnt * kGItemCost + kGStartCost : 0);
+    if (lane < G) gpre[lane + 1] = inc, gwpre[lane + 1] = winc;
+    if (lane == 0) gpre[0] = 0, gwpre[0] = 0;
   }
   __syncthreads();
   const int G = ngroups;
-  const int total = gpre[G];
-  const int j0 = (int)((long)m * total / M), j1 = (int)((long)(m + 1) * total / M);
+  // the workgroup's items: an equal share of the XCD's cost, an item of group g at cost gwpre[g] + start + item *
+  // i taken by the share its cost starts in (a run that starts a group pays its histogram flush and query loads)
+  auto item_at = [&](long w) {  // the first item whose cost starts at or after w (workgroup-uniform)
+    const bool le = lane < G && gwpre[lane] <= w;
+    const int g = __popcll(__ballot(le)) - 1;
+    if (g < 0) return 0;
+    if (g >= G) return gpre[G];
+    const long d = w - gwpre[g] - kGStartCost;
+    const int cnt = gpre[g + 1] - gpre[g];
+    const int i = d <= 0 ? 0 : (int)((d + kGItemCost - 1) / kGItemCost);
+    return gpre[g] + (i < cnt ? i : cnt);
+  };
+  const long wtot = gwpre[G];
+  const int j0 = item_at((long)m * wtot / M), j1 = item_at((long)(m + 1) * wtot / M);
   if (j0 >= j1) return;
   struct Item {
     int grp, c0;
