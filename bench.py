@@ -222,7 +222,8 @@ def run_prefill(args, dev):
     [window history | chunk | compressed] with 128 + 2048 indices per query.  The window and compressed rows are
     read in place (two KV sources) and the selection is written into the compressed columns of one preallocated
     index buffer (the reference concatenates both, dsv41/model.py:1442-1443).  us_per_chunk: a HIP graph of the
-    chunk's launches, replayed (events on the launch stream); phase_us: eager launches with events between the
+    chunk's launches, 5 warm-up replays, then the median of 20 replays each between two events on the launch stream;
+    phase_us: eager launches with events between the
     phases, median of the repetitions (the eager appends phase includes host launch time)."""
     import numpy as np
     import torch
@@ -296,17 +297,20 @@ def run_prefill(args, dev):
     torch.cuda.synchronize(dev)
     with torch.cuda.graph(gr, stream=s2):
         step()
-    gr.replay()
-    torch.cuda.synchronize(dev)
-    reps = max(3, min(args.prefill_reps, 20))
-    e0, e1 = E(), E()
-    e0.record(stream)
-    for _ in range(reps):
+    for _ in range(5):  # (warm: the clocks settle over the first replays)
         gr.replay()
-    e1.record(stream)
     torch.cuda.synchronize(dev)
-    t_graph = e0.elapsed_time(e1) * 1000.0 / reps
-    log(f"[bench] prefill C3 graph: {t_graph:.1f} us/chunk")
+    reps = 20
+    ev = [E() for _ in range(reps + 1)]
+    ev[0].record(stream)
+    for i in range(reps):
+        gr.replay()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize(dev)
+    per = np.array([ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(reps)])
+    t_graph = float(np.median(per))
+    log(f"[bench] prefill C3 graph: median {t_graph:.1f} us/chunk over {reps} replays (min {per.min():.1f}, "
+        f"max {per.max():.1f})")
     T = cfg.n_c
     idx_flops = sum(2 * HI * DI * ((cfg.prior + i + 1) // cfg.ratio) for i in range(S))
     att_flops = S * (WIN + cfg.topk) * H * (DQK + DV) * 2
@@ -314,6 +318,8 @@ def run_prefill(args, dev):
     return {"config": f"{cfg.name}: {S}-token chunk after {cfg.prior} tokens, ratio {cfg.ratio}, top-k {cfg.topk}, "
                       f"{T} compressed rows, 64 heads x 576",
             "tok_per_s": round(S / (t_graph * 1e-6), 1), "us_per_chunk": round(t_graph, 1),
+            "timing": {"replays": reps, "median_us": round(t_graph, 1), "min_us": round(float(per.min()), 1),
+                       "max_us": round(float(per.max()), 1)},
             "phase_us": {k: round(v, 1) for k, v in t.items()},
             "mfma_frac": {"indexer_fp8": round(idx_flops / (t["indexer"] * 1e-6) / (MFMA_FP8_TFLOPS * 1e12), 4),
                           "attention_bf16": round(att_flops / (t["attention"] * 1e-6) / (MFMA_BF16_TFLOPS * 1e12), 4),
