@@ -546,6 +546,36 @@ __global__ void __launch_bounds__(kGThreads, 1) index_score_group_kernel(const S
 
 // ------------------------------------------------------------------------------------------------ top-k
 
+// Lanes 0 .. n-1 as a wave mask (n clamped to 0 .. 64); whether this lane is set in a mask; a lane's rank among
+// the set lanes of m below it.
+DSV41_DEV unsigned long long lanes_below(int n) {
+  return n >= 64 ? ~0ull : (n <= 0 ? 0ull : (1ull << n) - 1ull);
+}
+DSV41_DEV bool lane_in(unsigned long long m) { return __builtin_amdgcn_inverse_ballot_w64(m); }  // (exec = m)
+DSV41_DEV int lane_rank(unsigned long long m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// A wave's pass over positions [i0, i1) in batches of 64 B: key_of(i) for position b0 + 64 u + lane, then
+// body(b0, keys, full) -- full (a compile-time flag) when the whole batch lies inside the range, so its reads need
+// no clamp; the last, partial batch reads position i1 - 1 in place of those past the range.
+template <int B, typename KeyOf, typename Body>
+DSV41_DEV void wave_batches(int i0, int i1, int lane, KeyOf key_of, Body body) {
+  int b0 = i0;
+  for (; b0 + 64 * B <= i1; b0 += 64 * B) {
+    uint32_t kk[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) kk[u] = key_of(b0 + u * 64 + lane);
+    body(b0, kk, std::true_type{});
+  }
+  if (b0 < i1) {
+    uint32_t kk[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) kk[u] = key_of(min(b0 + u * 64 + lane, i1 - 1));
+    body(b0, kk, std::false_type{});
+  }
+}
+
 struct TopkArgs {
   const float* score;
   long ld;
@@ -588,7 +618,7 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
   __shared__ uint32_t red_min[NW], red_max[NW];
   __shared__ int w_gt[NW], w_eq[NW], w_take[NW], w_base[NW], w_nc[NW];
   __shared__ int s_digit, s_rem, s_bin, s_over;
-  const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (uniform: the wave's chunk bounds and masks stay scalar)
   const float* row = a.score + (long)r * a.ld;
   int* orow = a.out + (long)r * a.out_rstride;
   long clr = a.cl ? a.cl[r] : (a.cl_start + (long)(r % a.rows_per_seq) + 1) / a.cl_ratio;
@@ -598,6 +628,7 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
     for (int i = tid; i < k; i += kTopkThreads) orow[i] = i < c ? i + a.offset : -1;
     return;
   }
+  DSV41_PX(0);
   const bool cached = c <= kTopkCache;
   uint32_t* hb16 = (uint32_t*)hist;  // 16-bit bin b: half (b & 1) of word b >> 1
   if (cached) {
@@ -669,6 +700,7 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
       }
     }
   }
+  DSV41_PX(1);
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
     kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, m, 64));
@@ -686,9 +718,9 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
     kmin = min(kmin, red_min[w]);
     kmax = max(kmax, red_max[w]);
   }
+  DSV41_PX(2);
   const int chunk = ((c + NW * 64 - 1) / (NW * 64)) * 64;
   const int i0 = min(c, wave * chunk), i1 = min(c, i0 + chunk);
-  const unsigned long long lt = (1ull << lane) - 1ull;
   uint32_t thr = 0u;  // the k-th largest key; `remaining` elements equal to it are taken
   int remaining = k;
   bool fast = cached;
@@ -713,37 +745,36 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
       greater += hb[i];
     }
     __syncthreads();
+    DSV41_PX(3);
     const uint32_t bn = (uint32_t)s_bin;
     const int need = s_rem;  // candidates of bin bn to take
     // ---- per wave: entries above bn, and the list of bin-bn candidates
     uint32_t* wl = hb16 + wave * kList;
+    // masks of 64 positions at a time: two compares per key (bin >= bn, bin > bn), the counts and the candidates'
+    // list slots from the ballots (scalar popcounts, mbcnt lane ranks)
+    const uint32_t lo = bn << 20, hi_incl = lo | 0xfffffu;
     int gt = 0, nc = 0;
-    for (int b0 = i0; b0 < i1; b0 += 64 * B) {
-      uint32_t kk[B];
+    wave_batches<B>(i0, i1, lane, [&](int i) { return keys[i]; }, [&](int b0, const uint32_t(&kk)[B], auto full) {
 #pragma unroll
       for (int u = 0; u < B; ++u) {
-        const int i = b0 + u * 64 + lane;
-        kk[u] = keys[i < i1 ? i : i0];
+        const unsigned long long inm = full ? ~0ull : lanes_below(i1 - (b0 + u * 64));
+        const unsigned long long gem = __ballot(kk[u] >= lo) & inm, gtm = __ballot(kk[u] > hi_incl) & inm;
+        const unsigned long long cm = gem & ~gtm;
+        gt += __popcll(gtm);
+        if (cm) {
+          const int p = nc + lane_rank(cm);
+          if (lane_in(cm) && p < kList) wl[p] = kk[u];
+          nc += __popcll(cm);
+        }
       }
-#pragma unroll
-      for (int u = 0; u < B; ++u) {
-        const bool in = b0 + u * 64 + lane < i1;
-        const uint32_t bin = kk[u] >> 20;
-        gt += in && bin > bn;
-        const bool cand = in && bin == bn;
-        const unsigned long long bc = __ballot(cand);
-        const int p = nc + __popcll(bc & lt);
-        if (cand && p < kList) wl[p] = kk[u];
-        nc += __popcll(bc);
-      }
-    }
-    gt = __reduce_add_sync(~0ull, gt);
+    });
     if (lane == 0) {
       w_gt[wave] = gt;
       w_nc[wave] = nc;
       if (nc > kList) s_over = 1;
     }
     __syncthreads();
+    DSV41_PX(4);
     if (s_over == 0) {
       // ---- radix select of the need-th largest listed candidate on the low 20 bits (10 + 10)
       uint32_t prefix = 0u, pmask = 0u;
@@ -753,12 +784,13 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
         const int shift = pass == 0 ? 10 : 0;
         for (int i = tid; i < 512; i += kTopkThreads) h2[i] = 0u;
         __syncthreads();
-#pragma unroll 1
-        for (int w = 0; w < NW; ++w) {
-          const int n = w_nc[w];
-#pragma unroll 1
-          for (int j = tid; j < n; j += kTopkThreads) {
-            const uint32_t d = hb16[w * kList + j] & 0xfffffu;
+        // every wave's list as one index space: slot j of list j / kList (all loads independent)
+        static_assert(NW * kList % kTopkThreads == 0, "list slots per thread");
+#pragma unroll
+        for (int q = 0; q < NW * kList / kTopkThreads; ++q) {
+          const int j = q * kTopkThreads + tid, w = j / kList;
+          if (j - w * kList < min(w_nc[w], kList)) {
+            const uint32_t d = hb16[j] & 0xfffffu;
             if ((d & pmask) == prefix) {
               const uint32_t dg = (d >> shift) & 1023u;
               atomicAdd(&h2[dg >> 1], 1u << ((dg & 1u) * 16));
@@ -790,6 +822,7 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
         rem = s_rem;
         __syncthreads();
       }
+      DSV41_PX(5);
       thr = (bn << 20) | prefix;
       remaining = rem;
       // per wave: its listed candidates above / equal to the threshold
@@ -895,31 +928,38 @@ __global__ void __launch_bounds__(NT) topk_kernel(const TopkArgs a) {
     }
   }
   __syncthreads();
-  // ---- ordered emission over the wave's chunk, 64 positions per step
+  DSV41_PX(6);
+  // ---- ordered emission over the wave's chunk, 64 positions per step: the selected lanes as a mask (keys above
+  // the threshold, and the wave's first `take` keys equal to it), their output slots from mbcnt lane ranks
   const int take = w_take[wave];
   int base = w_base[wave], eq_seen = 0;
-  for (int b0 = i0; b0 < i1; b0 += 64 * B) {
-    uint32_t kk[B];
+  auto emit = [&](auto key_of) {
+    wave_batches<B>(i0, i1, lane, key_of, [&](int b0, const uint32_t(&kk)[B], auto full) {
 #pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const int i = b0 + u * 64 + lane;
-      kk[u] = key_at(i < i1 ? i : i0);
-    }
-#pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const int i = b0 + u * 64 + lane;
-      const bool in = i < i1;
-      const bool is_gt = in && kk[u] > thr;
-      const bool is_eq = in && kk[u] == thr;
-      const unsigned long long beq = __ballot(is_eq);
-      const bool sel = is_gt || (is_eq && eq_seen + __popcll(beq & lt) < take);
-      const unsigned long long bsel = __ballot(sel);
-      const int p = base + __popcll(bsel & lt);
-      if (sel && p < k) orow[p] = i + a.offset;
-      base += __popcll(bsel);
-      eq_seen += __popcll(beq);
-    }
-  }
+      for (int u = 0; u < B; ++u) {
+        const int i = b0 + u * 64 + lane;
+        const unsigned long long inm = full ? ~0ull : lanes_below(i1 - (b0 + u * 64));
+        unsigned long long selm = __ballot(kk[u] > thr) & inm;
+        const unsigned long long eqm = __ballot(kk[u] == thr) & inm;
+        if (eqm) {  // (uniform) equal keys: taken in position order until `take` are
+          const int avail = take - eq_seen;
+          if (avail >= (int)__popcll(eqm))  // (signed: avail < 0 once the wave's share is taken)
+            selm |= eqm;
+          else if (avail > 0)
+            selm |= __ballot(lane_in(eqm) && lane_rank(eqm) < avail);
+          eq_seen += __popcll(eqm);
+        }
+        const int p = base + lane_rank(selm);
+        if (lane_in(selm) && p < k) orow[(uint32_t)p] = i + a.offset;
+        base += __popcll(selm);
+      }
+    });
+  };
+  if (cached)
+    emit([&](int i) { return keys[i]; });
+  else
+    emit([&](int i) { return score_key(row[i]); });
+  DSV41_PX(7);
 }
 
 // Compute units of the current device (queried once per device; 256 when the query fails).
