@@ -1054,253 +1054,6 @@ __global__ void __launch_bounds__(512) attn_decode32_kernel(const AttnArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ prefill kernel
-// Many query rows (prefill chunk): one workgroup per (query row, 64 heads), whole key list, no split.  8 waves (2 per
-// SIMD), two roles per 64-key tile:
-//   QK  wave w = (hb = w & 3: heads 16hb..16hb+15, kh = w >> 2: keys 32kh..32kh+31): S[16 keys x 16 heads] for its
-//       two key blocks (16x16x32 bf16 MFMA, Q in VGPRs); the two waves of a head block exchange their per-head tile
-//       maxima (common lazy reference), keep l over their keys, and publish the probability fragments (bf16, MFMA
-//       operand order) and the rescale factors through LDS;
-//   PV  wave w = (hh = w & 1: heads 32hh..32hh+31, cq = w >> 1: columns cq*DV/4 ..): O[32 heads x DV/4] += P V over
-//       the tile's 64 keys (16x16x16 bf16 MFMA, V fragments from the transpose read, each used for both head blocks).
-// Tiles are gathered with direct-to-LDS loads two ahead (counted vmcnt waits, LDS-only barriers); the index entries of
-// tile i + 2 are loaded at the top of iteration i.  The output is staged through LDS for 16-byte stores.
-template <int DQK, int DV>
-__global__ void __launch_bounds__(512) attn_prefill_kernel(const AttnArgs a) {
-  constexpr int KS = DQK / 32;  // 32-deep k steps of QK^T
-  constexpr int CT = DV / 64;   // 16-column output tiles per wave (a quarter of DV)
-  constexpr int U = DQK / 8;    // 16-byte chunks per row; chunk c of row j at j*U + (c ^ (j & 7))
-  static_assert(U % 8 == 0 && CT >= 1, "row widths");
-  constexpr int TILE = 64;
-  constexpr int TILE_ELEMS = TILE * DQK;
-  constexpr int kLoadsPerTile = TILE * U / 512;
-  static_assert(kLoadsPerTile < 16, "vmcnt immediate");
-  static_assert(64 * DV * 4 <= 2 * TILE_ELEMS * 2, "output staging fits the tile buffers");
-  constexpr float kRescale = 8.0f;
-  __shared__ __align__(16) uint16_t ktile[2 * TILE_ELEMS];
-  __shared__ const uint16_t* rptr[3][TILE];
-  __shared__ uint2 pex[4][4][64];  // [head block][key block][lane]
-  __shared__ float smax[4][2][16];  // [head block][key half][head]
-  __shared__ float salpha[64];      // per head: rescale factor of this tile (1 when the reference stays)
-  __shared__ float sls[4][2][16];
-  __shared__ float hfac[64];
-
-  // rows of a chunk are consecutive query positions whose index lists overlap heavily: XCD x (workgroup b runs on XCD
-  // b % 8) takes a contiguous range of rows, so the shared gathered rows are served by its L2
-  const int hg64 = blockIdx.y;
-  const int per_xcd = (a.R + kXcds - 1) / kXcds, zb = blockIdx.z;
-  const int r = (zb % kXcds) * per_xcd + zb / kXcds;
-  if (r >= a.R) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hb = wave & 3, kh = wave >> 2;  // QK role
-  const int hh = wave & 1, cq = wave >> 1;  // PV role
-  const int l16 = lane & 15, g = lane >> 4;
-  const int H = a.H;
-
-  const int W = a.n1;
-  const int* irow = a.t > 0 ? a.idx + (long)r * a.idx_rstride : nullptr;
-  const int L = a.L;
-  const int ntiles = (L + TILE - 1) / TILE;
-  auto load_ix = [&](int ti) {  // threads 0..63: index-list entry of key position ti*TILE + tid (or -1)
-    const int j = ti * TILE + tid;
-    const int jj = a.mode == 1 ? j - W : j;
-    return tid < TILE && j < L && jj >= 0 && irow ? irow[jj] : -1;
-  };
-  const int ix0 = load_ix(0), ix1 = load_ix(1);
-  uint4 qf[KS];  // B operand: head 16hb + l16, k = 32 ks + 8 g .. + 7
-  {
-    const int h = hg64 * 64 + hb * 16 + l16;
-    const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)(h < H ? h : H - 1) * DQK + g * 8;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qrow + ks * 32);
-  }
-  long slot, pos = 0, pmax = 0, plim = 0;
-  if (a.mode == 1) {
-    slot = a.seq[r];
-    pos = a.pos[r];
-    pmax = a.pmax[r];
-    plim = a.plim ? a.plim[r] : pos;
-  } else {
-    slot = r / a.rows_per_slot;
-  }
-  const uint16_t* base1 = a.kv1 + slot * a.kv1_sstride;
-  const uint16_t* base2 = a.kv2 ? a.kv2 + slot * a.kv2_sstride : nullptr;
-
-  auto resolve = [&](int ti, int ix) {  // threads 0..63: row pointer of key position ti*TILE + tid
-    if (tid < TILE) {
-      const int j = ti * TILE + tid;
-      const uint16_t* p = nullptr;
-      if (j < L) {
-        if (a.mode == 1 && j < W) {
-          int m = (int)(pmax - j) % W;
-          m = m < 0 ? m + W : m;
-          const long held = pmax - m;
-          if (held >= 0 && held <= plim && pos - held < W) p = base1 + (long)j * DQK;
-        } else if (a.mode == 1) {
-          if (ix >= 0 && ix < a.n2) p = base2 + (long)ix * DQK;
-        } else if (ix >= 0 && ix < a.n1 + a.n2) {
-          p = ix < a.n1 ? base1 + (long)ix * DQK : base2 + (long)(ix - a.n1) * DQK;
-        }
-      }
-      rptr[ti % 3][tid] = p;
-    }
-  };
-  auto issue = [&](int ti) {  // direct-to-LDS 16-byte loads (inline assembly: no compiler waits around them)
-    uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
-    const uint16_t* const* rp = rptr[ti % 3];
-    const uint16_t* src[kLoadsPerTile];  // all row pointers read before the first load (the loads clobber memory)
-#pragma unroll
-    for (int rd = 0; rd < kLoadsPerTile; ++rd) {
-      const int cc = rd * 512 + wave * 64 + lane;  // LDS chunk position
-      const int j = cc / U, cs = cc - j * U;
-      const int c = cs ^ (j & 7);
-      const uint16_t* p = rp[j];
-      src[rd] = p ? p + c * 8 : g_zero_row;
-    }
-#pragma unroll
-    for (int rd = 0; rd < kLoadsPerTile; ++rd) lds_dma16(src[rd], buf + (rd * 512 + wave * 64) * 8);
-  };
-
-  __builtin_amdgcn_s_waitcnt(0);  // Q, the first index entries and the row's positions have arrived
-  if (ntiles > 0) resolve(0, ix0);
-  if (ntiles > 1) resolve(1, ix1);
-  __syncthreads();
-  if (ntiles > 0) issue(0);
-  if (ntiles > 1) issue(1);
-
-  float m_ref = -1e30f, l_run = 0.0f;  // QK role: head 16hb + l16, log2 units; l over this wave's keys
-  f32x4_t o[2][CT];                    // PV role: heads 32hh + 16 b2 + 4g + i, columns cq*DV/4 + 16 ct + l16
-#pragma unroll
-  for (int b2 = 0; b2 < 2; ++b2)
-#pragma unroll
-    for (int c = 0; c < CT; ++c) o[b2][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const float sl2 = a.scale * kLog2e;
-
-  for (int ti = 0; ti < ntiles; ++ti) {
-    const int ix_next = ti + 2 < ntiles ? load_ix(ti + 2) : -1;  // consumed at the end of the iteration
-    if (ti + 1 < ntiles)
-      __builtin_amdgcn_s_waitcnt(kLoadsPerTile | (0x7 << 4) | (0xf << 8));  // vmcnt(kLoadsPerTile)
-    else
-      __builtin_amdgcn_s_waitcnt(0);
-    lds_barrier();
-    DSV41_TS(8 * (ti % 6) + 0);
-    const uint16_t* buf = ktile + (ti & 1) * TILE_ELEMS;
-    const uint16_t* const* rp = rptr[ti % 3];
-    // ---- QK: s[b][i] = key 32kh + 16b + 4g + i, head 16hb + l16
-    f32x4_t s[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int jr = 32 * kh + 16 * b + l16;
-      const uint16_t* krow = buf + jr * DQK;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        s[b] = mfma_bf16_16x16x32(*(const uint4*)(krow + (((ks * 4 + g) ^ (jr & 7)) * 8)), qf[ks], s[b]);
-    }
-    DSV41_TS(8 * (ti % 6) + 1);
-    float tmax = -1e30f;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[b][i] = rp[32 * kh + 16 * b + 4 * g + i] ? s[b][i] * sl2 : -1e30f;
-        tmax = fmaxf(tmax, s[b][i]);
-      }
-    tmax = row_max4(tmax);
-    if (g == 0) smax[hb][kh][l16] = tmax;
-    lds_barrier();
-    tmax = fmaxf(smax[hb][0][l16], smax[hb][1][l16]);  // both key halves: the tile maximum of the head
-    {
-      const bool bump = tmax > m_ref + kRescale;
-      const float m_new = bump ? tmax : m_ref;
-      const float alpha = exp2f(m_ref - m_new);
-      l_run *= alpha;
-      m_ref = m_new;
-      if (kh == 0 && g == 0) salpha[16 * hb + l16] = alpha;
-      float psum = 0.0f;
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        float p[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[i] = s[b][i] > -1e29f ? exp2f(s[b][i] - m_ref) : 0.0f;
-          psum += p[i];
-        }
-        pex[hb][2 * kh + b][lane] = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
-      }
-      psum = row_sum4(psum);
-      l_run += psum;
-    }
-    lds_barrier();
-    DSV41_TS(8 * (ti % 6) + 2);
-    // ---- PV: rescale, then o[:, this wave's columns] += P V over the 64 keys
-#pragma unroll
-    for (int b2 = 0; b2 < 2; ++b2) {
-      float al[4];
-      bool any = false;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        al[i] = salpha[32 * hh + 16 * b2 + 4 * g + i];
-        any = any || al[i] != 1.0f;
-      }
-      if (__ballot(any)) {
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[b2][ct][i] *= al[i];
-      }
-    }
-#pragma unroll 1
-    for (int kb = 0; kb < 4; ++kb) {
-      const uint2 pa0 = pex[2 * hh][kb][lane], pa1 = pex[2 * hh + 1][kb][lane];
-      const int vj = 16 * kb + 4 * g + (l16 >> 2);
-      const uint16_t* vrow = buf + vj * DQK + ((l16 & 1) << 2);
-      const int vsw = vj & 7;
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const int cch = ((cq * (DV / 4) + ct * 16) >> 3) + ((l16 & 3) >> 1);
-        const uint2 vb = lds_read_tr16(vrow + ((cch ^ vsw) << 3));
-        o[0][ct] = mfma_bf16_16x16x16(pa0, vb, o[0][ct]);
-        o[1][ct] = mfma_bf16_16x16x16(pa1, vb, o[1][ct]);
-      }
-    }
-    DSV41_TS(8 * (ti % 6) + 3);
-    if (ti + 2 < ntiles) {
-      resolve(ti + 2, ix_next);
-      lds_barrier();  // buffer ti & 1 is free, the pointers of tile ti + 2 are visible; salpha / pex reusable
-      issue(ti + 2);
-    } else {
-      lds_barrier();  // salpha / pex reusable
-    }
-    DSV41_TS(8 * (ti % 6) + 4);
-  }
-  // ---- per-head sums over both key halves, normalisation factors, output staged for 16-byte stores
-  if (g == 0) sls[hb][kh][l16] = l_run;
-  __syncthreads();
-  if (kh == 0 && g == 0) {
-    const int hl = 16 * hb + l16, h = hg64 * 64 + hl;
-    hfac[hl] = 1.0f / (sls[hb][0][l16] + sls[hb][1][l16] + exp2f(a.sink[h < H ? h : H - 1] * kLog2e - m_ref));
-  }
-  float* stg = (float*)ktile;  // [64 heads][DV]
-#pragma unroll
-  for (int b2 = 0; b2 < 2; ++b2)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        stg[(hh * 32 + 16 * b2 + 4 * g + i) * DV + cq * (DV / 4) + ct * 16 + l16] = o[b2][ct][i];
-  __syncthreads();
-  constexpr int CG = DV / 8;
-#pragma unroll 1
-  for (int e = tid; e < 64 * CG; e += 512) {
-    const int hl = e / CG, c = (e - hl * CG) * 8, h = hg64 * 64 + hl;
-    if (h >= H) continue;
-    const float f = hfac[hl];
-    const float4 x0 = *(const float4*)(stg + hl * DV + c), x1 = *(const float4*)(stg + hl * DV + c + 4);
-    *(uint4*)(a.out + (long)r * a.out_rstride + (long)h * DV + c) =
-        make_uint4(pack_bf16x2(x0.x * f, x0.y * f), pack_bf16x2(x0.z * f, x0.w * f), pack_bf16x2(x1.x * f, x1.y * f),
-                   pack_bf16x2(x1.z * f, x1.w * f));
-  }
-}
-
 // Many query rows, pipelined roles: one workgroup per (query row, 64 heads), whole key list, 32-key tiles, three
 // stages in flight across the waves (iteration t, one workgroup barrier B0 each):
 //   QK waves 0..3, w = (hb = w & 1: heads 32hb..32hb+31, kb = w >> 1: keys 16kb..16kb+15 of the tile): the MFMAs of
