@@ -381,6 +381,39 @@ def test_topk_bit_exact(n, k, cl):
     np.testing.assert_array_equal(got, want)
 
 
+def test_topk_many_rows_ties_and_fallback():
+    """The many-row top-k (512-thread workgroups, rows staged in LDS) on ragged rows built to reach each of its paths:
+    no ties; ties at the threshold taken in part by several waves (coarse values); an all-equal row (the first k
+    positions); ties every 5th position; every key in one 12-bit histogram bin (the candidate lists overflow: the
+    range-normalised radix path); +0 / -0 mixtures (-0 equals +0); valid counts of k + 1 and of 64 m + 1; bit-exact
+    against the oracle."""
+    import dsv41_amd
+    r = rng(13)
+    R, n, k = 512, 6000, 2048
+    sc = r.standard_normal((R, n)).astype(np.float32)
+    cl = r.integers(k + 1, n + 1, R)
+    cl[:3] = [k + 1, n, 4097]
+    for b in range(R):
+        kind = b % 6
+        if kind == 1:
+            sc[b] = np.round(sc[b] * 4) / 4
+        elif kind == 2:
+            sc[b] = 1.0
+        elif kind == 3:
+            sc[b, ::5] = 0.25
+        elif kind == 4:
+            sc[b] = 1.0 + r.random(n).astype(np.float32) * 0.1  # [1, 1.1): one bin of the top 12 key bits
+        elif kind == 5:
+            sc[b] = np.where(r.random(n) < 0.5, np.float32(0.0), np.float32(-0.0))
+            sc[b, ::7] = r.random(len(sc[b, ::7])).astype(np.float32) + 0.5
+        sc[b, cl[b]:] = -np.inf
+    print(f"[topk many rows] R {R} n {n} k {k} cl {cl.min()}..{cl.max()}", flush=True)
+    got = dsv41_amd.topk_indices(f32(sc), k, i64(cl)).cpu().numpy()[:, 0]
+    want = O.topk_indices(sc, k, cl)
+    bad = np.nonzero((got != want).any(1))[0]
+    assert len(bad) == 0, f"rows {bad[:10].tolist()} (kinds {(bad[:10] % 6).tolist()}) differ"
+
+
 def test_index_topk_prefill():
     """Indexer.__call__ chunk selection (dsv41/model.py:766-893): per-query causal compressed length."""
     import dsv41_amd
