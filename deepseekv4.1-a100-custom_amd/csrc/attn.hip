@@ -1056,19 +1056,19 @@ __global__ void __launch_bounds__(512) attn_decode32_kernel(const AttnArgs a) {
 // ------------------------------------------------------------------------------------------------ prefill kernel
 // Many query rows, pipelined roles: one workgroup per (query row, 64 heads), whole key list, 32-key tiles, three
 // stages in flight across the waves (iteration t, one workgroup barrier B0 each):
-//   QK waves 0..3, w = (hb = w & 1: heads 32hb..32hb+31, kb = w >> 1: keys 16kb..16kb+15 of the tile): the MFMAs of
-//       S for tile t (16x16x32 bf16, Q of 32 heads in VGPRs, each K fragment used for two head blocks), and while
-//       they run the softmax of tile t - 1: its per-lane partial maxima of both key halves were written to LDS in
-//       iteration t - 1, so B0 publishes them and no wave waits for a partner inside an iteration.  The probabilities
-//       (bf16, MFMA operand order) and the per-head rescale factor of tile t - 1 go to LDS, then the partial maxima of
-//       tile t.  Wave 0 also loads the index entries and resolves the row pointers three tiles ahead.
+//   QK waves 0..3, hq = w: heads 16hq..16hq+15 over all 32 keys of the tile: the MFMAs of S for tile t (16x16x32
+//       bf16; Q of 16 heads in VGPRs leaves room for the K fragments of both 16-key blocks, read six k steps ahead
+//       of their MFMAs -- the QK wave's K reads set the tile's pace), then the softmax of tile t - 1, whose maximum
+//       per head was taken in iteration t - 1 inside the wave (the four lane groups by row swaps; no exchange).
+//       The probabilities (bf16, MFMA operand order) and the per-head rescale factor of tile t - 1 go to LDS.
+//       Wave 0 also loads the index entries and resolves the row pointers three tiles ahead.
 //   PV waves 4..7, cq = w - 4: O[64 heads x columns cq*DV/4 ..] += P V for tile t - 2 (16x16x32 bf16 MFMA over the
 //       tile's 32 keys, each transposed V fragment used for four head blocks; the V fragments were read into VGPRs
 //       in iteration t - 1), interleaved with the direct-to-LDS gathers of tile t + 2 (counted vmcnt waits), then
 //       the V fragments of tile t - 1.
 // Four tile buffers: tile t (QK), t - 1 (V read by the PV waves), t + 1 and t + 2 (in flight; tile t + 2 goes into
-// tile t - 2's buffer, whose last read ended before B0).  B0: tile t has landed; P / rescale of tile t - 2, the
-// partial maxima of tile t - 1 and the row pointers of tile t + 2 are visible.  Keep the PV waves free of register
+// tile t - 2's buffer, whose last read ended before B0).  B0: tile t has landed; P / rescale of tile t - 2 and the
+// row pointers of tile t + 2 are visible.  Keep the PV waves free of register
 // spills: a scratch reload waits for every outstanding load (vmcnt(0)), the in-flight gathers included.
 template <int DQK, int DV>
 __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) {
@@ -1086,7 +1086,6 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   __shared__ const uint16_t* rptr[NBUF][TILE];  // row of each key (the zero row when invalid: no test per gather)
   __shared__ uint32_t rvalid[NBUF];            // bit j: key j of the tile is valid
   __shared__ uint2 pex[2][4][2][64];  // [tile parity][head block][key block][lane]
-  __shared__ float xmax[2][2][4][64];  // [tile parity][key half][lane group][head]: partial maxima; at the end sums
   __shared__ __align__(16) float salpha[2][64];  // [tile parity][head]: rescale factor (1 when the reference stays)
   __shared__ __align__(16) int srescale[2][4];    // [tile parity][head block]: some factor differs from 1
   __shared__ float hfac[64];
@@ -1097,8 +1096,7 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   if (r >= a.R) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool qk = wave < 4;
-  const int hb = wave & 1, kb = (wave >> 1) & 1;  // QK role
-  const int cq = wave & 3;                        // PV role
+  const int cq = wave & 3;  // PV role
   const int l16 = lane & 15, g = lane >> 4;
   const int H = a.H;
 
@@ -1156,7 +1154,6 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
     resolve(2, p1);
     resolve(3, p1);  // (every slot holds valid pointers: the gathers past the row read through stale slots)
   }
-  (&xmax[1][0][0][0])[tid] = -1e30f;  // (512 entries: the maxima "of tile -1")
   // zero probabilities and rescale words "of tiles -2 and -1": the PV waves' first two iterations multiply zeros
   // instead of branching around their MFMAs
 #pragma unroll
@@ -1168,129 +1165,122 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   // The two roles run separate loops (so Q and the O accumulators never share registers) with the same barrier
   // sequence: one after the prologue, B0 per iteration t = 0..ntiles, two in the epilogue.
   if (qk) {
-    // Q of heads 32hb + 16b + l16 (B operand, k = 32 ks + 8 g ..); lazy reference and per-lane sums (log2 units)
-    uint4 qf[2][KS];
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int h = hg64 * 64 + hb * 32 + b * 16 + l16;
+    const int hq = wave;  // heads 16 hq .. 16 hq + 15, all 32 keys of each tile
+    uint4 qf[KS];
+    {
+      const int h = hg64 * 64 + 16 * hq + l16;
       const uint16_t* qrow = a.q + (long)r * a.q_rstride + (long)(h < H ? h : H - 1) * DQK + g * 8;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qf[b][ks] = *(const uint4*)(qrow + ks * 32);
+      for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const uint4*)(qrow + ks * 32);
     }
-    float m_ref[2] = {-1e30f, -1e30f}, l_run[2] = {0.0f, 0.0f};
+    float m_ref = -1e30f, l_run = 0.0f, tmax_prev = -1e30f;
     const float sl2 = a.scale * kLog2e;
-    // wave 0: index entries of tiles (t+3 rounded down to even, +1) in ix_cur, of the next pair in ix_nxt
     int ix_cur = load_ix2(1), ix_nxt = load_ix2(2);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    float scp[2][4];  // scaled, masked scores of the previous tile (key 16kb + 4g + i, head 32hb + 16b + l16)
+    float scp[2][4];  // scaled, masked scores of the previous tile (key 16 kbk + 4 g + i, head 16 hq + l16)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int kbk = 0; kbk < 2; ++kbk)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) scp[b][i] = -1e30f;
+      for (int i = 0; i < 4; ++i) scp[kbk][i] = -1e30f;
     for (int t = 0; t <= ntiles + 1; ++t) {
       PF_TS(0, 0);
       lds_barrier();  // B0
       PF_TS(1, 0);
       if (t > ntiles) break;
-      if (t + 3 < ntiles) {  // wave 0: pointers of tile t + 3 (its slot last served tile t - 1, now done)
+      if (t + 3 < ntiles) {
         resolve(t + 3, ix_cur);
-        if ((t + 3) & 1) {  // pair consumed: the next one moves up, the one after is loaded (two tiles ahead)
+        if ((t + 3) & 1) {
           ix_cur = ix_nxt;
           ix_nxt = load_ix2((t + 3) / 2 + 2);
         }
       }
-      // One scheduling region (no branches): the partial maxima of tile t - 1 and the K fragments of tile t are
-      // read, the MFMAs of tile t are issued with the softmax of tile t - 1 between them, then the partial maxima of
-      // tile t are written.  At t == ntiles the MFMAs run on a stale buffer and their maxima are never read.
       const int tp = t - 1;
-      float xm[2][8];
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int u = 0; u < 8; ++u) xm[b][u] = xmax[tp & 1][u >> 2][u & 3][32 * hb + 16 * b + l16];
       const uint16_t* buf = ktile + (t % NBUF) * TILE_ELEMS;
-      const int jr = 16 * kb + l16;
-      // chunk (4 ks + g) ^ (jr & 7) = 4 ks + (g ^ (jr & 3)) + (jr & 4) for even ks, - (jr & 4) for odd ks: two
-      // base addresses and immediate offsets
-      const uint16_t* kre = buf + jr * DQK + ((g ^ (jr & 3)) + (jr & 4)) * 8;
-      const uint16_t* kro = kre - (jr & 4) * 16;
-      const uint32_t vbits = rvalid[t % NBUF] >> (16 * kb + 4 * g);
-      bool ok[4];
+      const uint32_t vall = rvalid[t % NBUF];
+      uint4 kf[2][KS];
+      const uint16_t* kbase[2][2];  // [key block][k-step parity]
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ok[i] = (vbits >> i) & 1u;
-      uint4 kf[KS];
+      for (int kbk = 0; kbk < 2; ++kbk) {
+        const int jr = 16 * kbk + l16;
+        kbase[kbk][0] = buf + jr * DQK + ((g ^ (jr & 3)) + (jr & 4)) * 8;
+        kbase[kbk][1] = kbase[kbk][0] - (jr & 4) * 16;
+      }
+      f32x4_t s[2][2];  // [key block][k-step parity]
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[ks] = *(const uint4*)((ks & 1 ? kro : kre) + ks * 32);
-      f32x4_t s[2][2];  // [head block][k-step parity]: four independent accumulator chains
+      for (int kbk = 0; kbk < 2; ++kbk) s[kbk][0] = s[kbk][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      // K fragments read KD k steps ahead of their MFMAs, each k step's group pinned by a scheduling barrier (the
+      // compiler's own schedule kept two or three reads in flight).  KD = 6 keeps at most ~14 LDS operations of the
+      // wave outstanding; the same loop with every read issued up front (36 outstanding) gave wrong results.
+      constexpr int KD = KS < 6 ? KS : 6;
 #pragma unroll
-      for (int b = 0; b < 2; ++b) s[b][0] = s[b][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int ks = 0; ks < KD; ++ks)
+#pragma unroll
+        for (int kbk = 0; kbk < 2; ++kbk) kf[kbk][ks] = *(const uint4*)(kbase[kbk][ks & 1] + ks * 32);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        s[0][ks & 1] = mfma_bf16_16x16x32(kf[ks], qf[0][ks], s[0][ks & 1]);
-        s[1][ks & 1] = mfma_bf16_16x16x32(kf[ks], qf[1][ks], s[1][ks & 1]);
+        s[0][ks & 1] = mfma_bf16_16x16x32(kf[0][ks], qf[ks], s[0][ks & 1]);
+        s[1][ks & 1] = mfma_bf16_16x16x32(kf[1][ks], qf[ks], s[1][ks & 1]);
+        if (ks + KD < KS) {
+#pragma unroll
+          for (int kbk = 0; kbk < 2; ++kbk)
+            kf[kbk][ks + KD] = *(const uint4*)(kbase[kbk][(ks + KD) & 1] + (ks + KD) * 32);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // softmax of tile t - 1 (at t == 0: scp = -1e30 and the maxima slot holds -1e30, so nothing changes)
+      // softmax of tile t - 1 (at t == 0 the maximum and the scores of "tile -1" are -1e30: its probabilities meet
+      // zero V fragments in the PV waves, and the first valid tile's factor 2^(-1e30 - m) = 0 clears the sum)
+      {
+        const float m_new = tmax_prev > m_ref + kRescale ? tmax_prev : m_ref;
+        const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
+        l_run *= alpha;
+        m_ref = m_new;
+        if (g == 0) salpha[tp & 1][16 * hq + l16] = alpha;
+        const unsigned long long moved = __ballot(alpha != 1.0f);
+        if (lane == 0) srescale[tp & 1][hq] = moved != 0;
+        float psum = 0.0f;
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int hl = 32 * hb + 16 * b + l16;
-        float tmax = xm[b][0];
+        for (int kbk = 0; kbk < 2; ++kbk) {
+          float p[4];
 #pragma unroll
-        for (int u = 1; u < 8; ++u) tmax = fmaxf(tmax, xm[b][u]);
-        const float m_new = tmax > m_ref[b] + kRescale ? tmax : m_ref[b];
-        const float alpha = __builtin_amdgcn_exp2f(m_ref[b] - m_new);  // v_exp_f32: arguments <= 0 here
-        l_run[b] *= alpha;
-        m_ref[b] = m_new;
-        if (kb == 0 && g == 0) salpha[tp & 1][hl] = alpha;
-        if (kb == 0) {  // one word per head block: did any of its heads move its reference (the PV waves' test)
-          const unsigned long long moved = __ballot(alpha != 1.0f);
-          if (lane == 0) srescale[tp & 1][2 * hb + b] = moved != 0;
+          for (int i = 0; i < 4; ++i) {
+            p[i] = __builtin_amdgcn_exp2f(scp[kbk][i] - m_new);
+            psum += p[i];
+          }
+          pex[tp & 1][hq][kbk][lane] = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
         }
-        float p[4], psum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[i] = __builtin_amdgcn_exp2f(scp[b][i] - m_new);  // masked keys: 2^(-1e30 - m) = 0
-          psum += p[i];
-        }
-        pex[tp & 1][2 * hb + b][kb][lane] = make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]));
-        l_run[b] += psum;  // this lane's keys only; summed over the lane groups at the end
+        l_run += psum;
       }
       PF_TS(2, 0);
-      // scores of tile t, scaled to log2 units and masked; partial maxima of the 4 keys of this lane
+      float tm = -1e30f;
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        float tm = -1e30f;
+      for (int kbk = 0; kbk < 2; ++kbk) {
+        const uint32_t vb = vall >> (16 * kbk + 4 * g);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          scp[b][i] = ok[i] ? (s[b][0][i] + s[b][1][i]) * sl2 : -1e30f;
-          tm = fmaxf(tm, scp[b][i]);
+          scp[kbk][i] = (vb >> i) & 1u ? (s[kbk][0][i] + s[kbk][1][i]) * sl2 : -1e30f;
+          tm = fmaxf(tm, scp[kbk][i]);
         }
-        xmax[t & 1][kb][g][32 * hb + 16 * b + l16] = tm;
       }
+      tmax_prev = row_max4(tm);
       PF_TS(3, 0);
     }
-    // per-head sums over both key halves and the 4 lane groups, normalisation factors
-    __syncthreads();  // E1: every wave is past its last read of xmax
-    xmax[0][kb][g][32 * hb + l16] = l_run[0];
-    xmax[0][kb][g][32 * hb + 16 + l16] = l_run[1];
-    lds_barrier();  // QK waves only see each other's sums after this (the PV waves pass it too)
-    if (kb == 0 && g == 0) {
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int hl = 32 * hb + 16 * b + l16, h = hg64 * 64 + hl;
-        float l = 0.0f;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) l += xmax[0][u >> 2][u & 3][hl];
-        if (a.nsplit > 1) {  // split partial: normalised by its own sum; m (natural-log units) and l for the merge
-          hfac[hl] = l > 0.0f ? 1.0f / l : 0.0f;
-          if (h < H) {
-            const long pi = ((long)r * H + h) * a.nsplit + sp;
-            a.pm[pi] = m_ref[b] * 0.6931471805599453f;
-            a.pl[pi] = l;
-          }
-        } else {
-          hfac[hl] = 1.0f / (l + exp2f(a.sink[h < H ? h : H - 1] * kLog2e - m_ref[b]));
+    __syncthreads();  // E1
+    const float lsum = row_sum4(l_run);
+    lds_barrier();  // (the barrier sequence of the other form)
+    if (g == 0) {
+      const int hl = 16 * hq + l16, h = hg64 * 64 + hl;
+      const float l = lsum;
+      if (a.nsplit > 1) {
+        hfac[hl] = l > 0.0f ? 1.0f / l : 0.0f;
+        if (h < H) {
+          const long pi = ((long)r * H + h) * a.nsplit + sp;
+          a.pm[pi] = m_ref * 0.6931471805599453f;
+          a.pl[pi] = l;
         }
+      } else {
+        hfac[hl] = 1.0f / (l + exp2f(a.sink[h < H ? h : H - 1] * kLog2e - m_ref));
       }
     }
     __syncthreads();  // E3
