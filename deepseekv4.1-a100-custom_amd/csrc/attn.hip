@@ -1085,6 +1085,7 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   __shared__ __align__(16) uint16_t ktile[NBUF * TILE_ELEMS];
   __shared__ const uint16_t* rptr[NBUF][TILE];  // row of each key (the zero row when invalid: no test per gather)
   __shared__ uint32_t rvalid[NBUF];            // bit j: key j of the tile is valid
+  __shared__ int ixring[8][64];  // index entries of tile T in slot T & 7 (entries 0..31; 32..63 unused)
   __shared__ uint2 pex[2][4][2][64];  // [tile parity][head block][key block][lane]
   __shared__ __align__(16) float salpha[2][64];  // [tile parity][head]: rescale factor (1 when the reference stays)
   __shared__ __align__(16) int srescale[2][4];    // [tile parity][head block]: some factor differs from 1
@@ -1108,10 +1109,14 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   const int jb = tb * TILE, jend = min(a.L, te * TILE);
   const int ntiles = te - tb;
   // wave 0 loads index entries for two tiles at a time (tile 2u + (lane >> 5), key lane & 31) ...
-  auto load_ix2 = [&](int u) {
-    const int j = jb + (2 * u + (lane >> 5)) * TILE + (lane & 31);
+  // wave 0 brings the index entries of tile T into ring slot T & 7 by direct-to-LDS loads (entries outside the list
+  // read the zero row; resolve() applies the validity).  A register load would not do: the compiler waited for it
+  // where the branch that hands it on joined -- a memory round trip on the critical wave every other tile.
+  auto ix_dma = [&](int T) {
+    const int j = jb + T * TILE + (lane & 31);
     const int jj = a.mode == 1 ? j - W : j;
-    return wave == 0 && j < jend && jj >= 0 && irow ? irow[jj] : -1;
+    const bool ok = lane < 32 && j < jend && jj >= 0 && irow;
+    lds_dma4_at(ok ? (const void*)(irow + jj) : (const void*)g_zero_row, lds_addr_of(&ixring[T & 7][0]));
   };
   long slot, pos = 0, pmax = 0, plim = 0;
   if (a.mode == 1) {
@@ -1125,9 +1130,10 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   const uint16_t* base1 = a.kv1 + slot * a.kv1_sstride;
   const uint16_t* base2 = a.kv2 ? a.kv2 + slot * a.kv2_sstride : nullptr;
   // ... and the lanes holding tile ti (half ti & 1 of the wave) resolve its row pointers
-  auto resolve = [&](int ti, int ix) {
+  auto resolve = [&](int ti) {
     if (wave == 0 && (lane >> 5) == (ti & 1)) {
       const int j = jb + ti * TILE + (lane & 31);
+      const int ix = irow ? ixring[ti & 7][lane & 31] : -1;
       const uint16_t* p = nullptr;
       if (j < jend) {
         if (a.mode == 1 && j < W) {
@@ -1148,11 +1154,15 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   };
 
   {
-    const int p0 = load_ix2(0), p1 = load_ix2(1);
-    resolve(0, p0);
-    resolve(1, p0);
-    resolve(2, p1);
-    resolve(3, p1);  // (every slot holds valid pointers: the gathers past the row read through stale slots)
+    if (wave == 0) {
+#pragma unroll
+      for (int T = 0; T < 5; ++T) ix_dma(T);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+    resolve(0);
+    resolve(1);
+    resolve(2);
+    resolve(3);  // (every slot holds valid pointers: the gathers past the row read through stale slots)
   }
   // zero probabilities and rescale words "of tiles -2 and -1": the PV waves' first two iterations multiply zeros
   // instead of branching around their MFMAs
@@ -1160,6 +1170,9 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
   for (int u = 0; u < 4; ++u) ((uint32_t*)&pex[0][0][0][0])[u * 512 + tid] = 0u;
   if (tid < 8) (&srescale[0][0])[tid] = 0;
   float* stg = (float*)ktile;  // output staging [64 heads][DV] once the tiles are done
+#ifndef DSV41_QKT
+#define DSV41_QKT 0
+#endif
 #define PF_TS(k, thr) \
   if (t >= 30 && t < 34) DSV41_TST(16 * (t - 30) + (k), thr)
   // The two roles run separate loops (so Q and the O accumulators never share registers) with the same barrier
@@ -1175,7 +1188,6 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
     }
     float m_ref = -1e30f, l_run = 0.0f, tmax_prev = -1e30f;
     const float sl2 = a.scale * kLog2e;
-    int ix_cur = load_ix2(1), ix_nxt = load_ix2(2);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     float scp[2][4];  // scaled, masked scores of the previous tile (key 16 kbk + 4 g + i, head 16 hq + l16)
@@ -1184,17 +1196,16 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
 #pragma unroll
       for (int i = 0; i < 4; ++i) scp[kbk][i] = -1e30f;
     for (int t = 0; t <= ntiles + 1; ++t) {
-      PF_TS(0, 0);
+      PF_TS(0, DSV41_QKT);
       lds_barrier();  // B0
-      PF_TS(1, 0);
+      PF_TS(1, DSV41_QKT);
       if (t > ntiles) break;
-      if (t + 3 < ntiles) {
-        resolve(t + 3, ix_cur);
-        if ((t + 3) & 1) {
-          ix_cur = ix_nxt;
-          ix_nxt = load_ix2((t + 3) / 2 + 2);
-        }
+      if (t + 3 < ntiles && wave == 0) {  // pointers of tile t + 3 (its slot last served tile t - 1, now done)
+        ix_dma(t + 5);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2));  // tile t + 3's entries (two loads were issued after them)
+        resolve(t + 3);
       }
+      PF_TS(4, DSV41_QKT);
       const int tp = t - 1;
       const uint16_t* buf = ktile + (t % NBUF) * TILE_ELEMS;
       const uint32_t vall = rvalid[t % NBUF];
@@ -1252,7 +1263,7 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
         }
         l_run += psum;
       }
-      PF_TS(2, 0);
+      PF_TS(2, DSV41_QKT);
       float tm = -1e30f;
 #pragma unroll
       for (int kbk = 0; kbk < 2; ++kbk) {
@@ -1264,7 +1275,7 @@ __global__ void __launch_bounds__(512) attn_prefill_ws_kernel(const AttnArgs a) 
         }
       }
       tmax_prev = row_max4(tm);
-      PF_TS(3, 0);
+      PF_TS(3, DSV41_QKT);
     }
     __syncthreads();  // E1
     const float lsum = row_sum4(l_run);
