@@ -730,6 +730,14 @@ DSV41_DEV void merge_tiles32(const AttnArgs& a, int r, int hg, int HG, long pr, 
       }
     }
   };
+  // this lane's output column and, for the last rd columns, its inverse-rope cos / sin: loaded once, before the
+  // partials and unconditionally (the zero row when there is no rope), so that they share the partials' round trip
+  // instead of each head's rotation waiting for its own load
+  const int c = ((ti / CW) & 7) * (DV / 8) + (ti % CW) * 16 + l16;
+  const bool rope = a.rd > 0 && c >= DV - a.rd;
+  const long cidx = rope ? pr * (a.rd / 2) + ((c - (DV - a.rd)) >> 1) : 0;
+  const float rcos = (a.rd > 0 ? a.cos_t : (const float*)g_zero_row)[cidx];
+  const float rsin = (a.rd > 0 ? a.sin_t : (const float*)g_zero_row)[cidx];
   uint2 v[MS];
   if (act) load_batch(0, v);
   // weights: thread (head hh = tid >> 4, q = tid & 15) takes splits q, q + 16, q + 32, q + 48 (one batch of loads);
@@ -777,15 +785,14 @@ DSV41_DEV void merge_tiles32(const AttnArgs& a, int r, int hg, int HG, long pr, 
       }
     }
   }
-  const int c = w * (DV / 8) + ct * 16 + l16;
+  (void)w;
+  (void)ct;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float val = round_bf16(num[i]);
     const float partner = dpp_mov<0xB1>(val);  // lane ^ 1: column c ^ 1 of the same head
-    if (a.rd > 0 && c >= DV - a.rd) {
-      const int jj = (c - (DV - a.rd)) >> 1;
-      const float cs = a.cos_t[pr * (a.rd / 2) + jj];
-      const float sn = -a.sin_t[pr * (a.rd / 2) + jj];
+    if (rope) {
+      const float cs = rcos, sn = -rsin;
       val = (c & 1) ? (partner * sn + val * cs) : (val * cs - partner * sn);
     }
     const int h = h0 + hl + i;
@@ -1450,7 +1457,20 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const AttnArgs
   const long base = ((long)r * H + h) * ns;
   const long pr = (a.mode == 1 && a.pos) ? (a.pos[r] < 0 ? 0 : a.pos[r]) : 0;
   const uint16_t* pb = (const uint16_t*)a.pacc;
-  auto finish = [&](int c, const float (&num)[8], float den) {
+  // the inverse rope's cos / sin of the 4 column pairs at c (the last rd columns), issued with the partials'
+  // loads and unconditionally (the zero row when there is no rope): one round trip instead of one per pair
+  auto rope_load = [&](int c, float (&rc)[4], float (&rs)[4]) {
+    const float* cb = a.rd > 0 ? a.cos_t : (const float*)g_zero_row;
+    const float* sb = a.rd > 0 ? a.sin_t : (const float*)g_zero_row;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int cc = c + 2 * e;
+      const long idx = a.rd > 0 && cc >= DV - a.rd ? pr * (a.rd / 2) + ((cc - (DV - a.rd)) >> 1) : 0;
+      rc[e] = cb[idx];
+      rs[e] = sb[idx];
+    }
+  };
+  auto finish = [&](int c, const float (&num)[8], float den, const float (&rc)[4], const float (&rs)[4]) {
     const float inv = 1.0f / den;
     uint32_t pk[4];
 #pragma unroll
@@ -1458,9 +1478,7 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const AttnArgs
       float re = round_bf16(num[e] * inv), im = round_bf16(num[e + 1] * inv);
       const int cc = c + e;
       if (a.rd > 0 && cc >= DV - a.rd) {
-        const int jj = (cc - (DV - a.rd)) >> 1;
-        const float cs = a.cos_t[pr * (a.rd / 2) + jj];
-        const float sn = -a.sin_t[pr * (a.rd / 2) + jj];
+        const float cs = rc[e / 2], sn = -rs[e / 2];
         const float yr = re * cs - im * sn, yi = re * sn + im * cs;
         re = yr;
         im = yi;
@@ -1481,6 +1499,8 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const AttnArgs
       m[u] = u < ns ? a.pm[base + s] : -1e30f;
       l[u] = a.pl[base + s];
     }
+    float rc[4], rs[4];
+    rope_load(c, rc, rs);
     float mx = -1e30f;
 #pragma unroll
     for (int u = 0; u < B; ++u) mx = fmaxf(mx, m[u]);
@@ -1497,7 +1517,7 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const AttnArgs
         num[2 * e + 1] += wg * __uint_as_float(vv[e] & 0xffff0000u);
       }
     }
-    finish(c, num, den);
+    finish(c, num, den, rc, rs);
     return;
   }
   float mx = -1e30f;
@@ -1510,6 +1530,8 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const AttnArgs
   }
   const float sink_term = exp2f((a.sink[h] - mx) * kLog2e);
   for (int c = (threadIdx.x & 63) * 8; c < DV; c += 512) {
+    float rc[4], rs[4];
+    rope_load(c, rc, rs);
     float num[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float den = sink_term;
     for (int s0 = 0; s0 < ns; s0 += B) {
@@ -1532,7 +1554,7 @@ __global__ void __launch_bounds__(256) attn_decode_combine_kernel(const AttnArgs
         }
       }
     }
-    finish(c, num, den);
+    finish(c, num, den, rc, rs);
   }
 }
 
